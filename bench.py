@@ -1,0 +1,323 @@
+#!/usr/bin/env python
+"""Benchmark of the fused MLM attention path (flash-mlm API on MI355X / gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+
+A step is one pass of the hot path over one synthetic batch with inputs resident in
+HBM: for the default workload (packed varlen fp16 with a
+full-batch cached context) that is flash_attn_mlm_compressed + unpack_from_kernel
+(pack metadata is built once and memoised, as in the reference's own benchmark).
+Prints one JSON line: effective attention TFLOP/s (padding excluded, formula
+4*H*D*sum_b Lq_b*(Lctx_b + Lmain_b)), ms per step, the attention kernel's roofline
+fraction against the MI355X dense fp16/bf16 MFMA peak (kernel time from HIP events
+around back-to-back launches on its stream), and the reference's per-sequence
+PyTorch SDPA path timed on this host's CPU cores as a reported baseline.
+
+The configs (BASELINE.json "configs") are built by `make_case`, which the GPU tests
+reuse for parity checks.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Callable
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "flash-mlm_amd"))
+
+import torch  # noqa: E402
+
+METRIC = "effective attention TFLOP/s + ms/call, packed varlen w/ context, 1 MI355X"
+MFMA_PEAK_TFLOPS = {torch.bfloat16: 2516.6, torch.float16: 2516.6, torch.float32: 157.3}
+HBM_PEAK_GBS = 8000.0
+DEFAULT_CONFIG = 3
+
+DTYPE_NAMES = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+@dataclass
+class Case:
+    cfg: int
+    workload: str
+    dtype: torch.dtype
+    H: int
+    D: int
+    lengths_q: list[int]
+    lengths_ctx: list[int]  # per query sequence (shared contexts repeated)
+    causal: bool
+    prefill: bool
+    is_mla: bool
+    step: Callable[[], torch.Tensor]  # one pass of the hot path
+    attention: Callable[[], None]  # the attention kernel alone (prepared ABI call)
+    tensors: dict = field(default_factory=dict)  # inputs, kept for checks
+    config: dict = field(default_factory=dict)
+
+    @property
+    def flops(self) -> float:
+        lq = self.lengths_q
+        main = list(_cumsum(lq)[1:]) if self.causal else lq
+        ctx = [0] * len(lq) if self.prefill else self.lengths_ctx
+        return 4.0 * self.H * self.D * sum(a * (c + m) for a, c, m in zip(lq, ctx, main))
+
+    @property
+    def flops_reference_formula(self) -> float:
+        """src/benchmark/common.py:39-57 (Lmain = Lq even under causal_query_seq_attn)."""
+        ctx = [0] * len(self.lengths_q) if self.prefill else self.lengths_ctx
+        return 4.0 * self.H * self.D * sum(a * (c + a) for a, c in zip(self.lengths_q, ctx))
+
+    @property
+    def attention_bytes(self) -> float:
+        """Algorithmic HBM bytes of the attention kernel: q and o once, main K/V once
+        per head (MLA: one latent), each context row once per head it serves."""
+        esz = torch.finfo(self.dtype).bits // 8
+        T = sum(self.lengths_q)
+        hk = 1 if self.is_mla else self.H
+        m = 1 if self.is_mla else 2
+        ctx_rows = 0 if self.prefill else self.config.get("unique_ctx_tokens", 0)
+        return esz * self.D * (2 * self.H * T + m * hk * T + m * hk * ctx_rows)
+
+
+def _cumsum(xs):
+    out = [0]
+    for x in xs:
+        out.append(out[-1] + x)
+    return out
+
+
+def _randn(shape, gen, device, dtype, std=1.0):
+    t = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+    if std != 1.0:
+        t.mul_(std)
+    return t.to(dtype)
+
+
+def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
+    """Build BASELINE config `cfg` (1..5; config 5 variant "prefill" is 5b) with
+    seeded synthetic inputs: lengths from a CPU generator seeded 1000+cfg (query
+    lengths first, then context lengths), tensors from a device generator with the
+    same seed, fp32 normal * std cast to the config dtype."""
+    import flash_mlm as fm
+
+    seed = 1000 + cfg
+    gcpu = torch.Generator().manual_seed(seed)
+    gdev = torch.Generator(device=device).manual_seed(seed)
+
+    if cfg == 1:
+        B, H, N, D = 2, 8, 128, 64
+        dt = torch.float32
+        q, k, v = (_randn((B, H, N, D), gdev, device, dt) for _ in range(3))
+        scale = 1.0 / math.sqrt(D)
+        out_plan = fm.host.host._dense_impl(q, k, v, scale, None, None, False, None, False, run=False)
+        return Case(
+            cfg, "cfg1 dense flash_attn_mlm fp32 [2,8,128,64], no cache", dt, H, D, [N] * B, [0] * B,
+            False, False, False,
+            step=lambda: fm.flash_attn_mlm(q, k, v, scale),
+            attention=out_plan[1],
+            tensors=dict(q=q, k=k, v=v, scale=scale),
+            config=dict(B=B, H=H, N=N, D=D, seed=seed),
+        )
+
+    if cfg == 2:
+        B, H, N, D, C = 8, 16, 512, 64, 2048
+        dt = torch.bfloat16
+        scale = 1.0 / math.sqrt(D)
+        q0, k0, v0 = (_randn((1, H, C, D), gdev, device, dt) for _ in range(3))
+        q, k, v = (_randn((B, H, N, D), gdev, device, dt) for _ in range(3))
+        cache = fm.InferenceCache()
+        fm.flash_attn_mlm(q0, k0, v0, scale, inference_cache=cache, layer_id=0, prefill=True)
+        plan = fm.host.host._dense_impl(q, k, v, scale, cache, 0, False, None, False, run=False)[1]
+        return Case(
+            cfg, "cfg2 dense flash_attn_mlm bf16 [8,16,512,64] + shared prefilled ctx 2048", dt, H, D,
+            [N] * B, [C] * B, False, False, False,
+            step=lambda: fm.flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0),
+            attention=plan,
+            tensors=dict(q=q, k=k, v=v, k0=k0, v0=v0, scale=scale, cache=cache),
+            config=dict(B=B, H=H, N=N, D=D, context=C, seed=seed, unique_ctx_tokens=C),
+        )
+
+    if cfg in (3, 4, 5):
+        if cfg == 3:
+            B, H, N, D, bn = 32, 16, 1024, 128, 64
+            dt, std = torch.float16, 1.0
+            lq = torch.randint(256, 1024 + 1, (B,), generator=gcpu)
+            lc = torch.randint(512, 2048 + 1, (B,), generator=gcpu)
+            cbs, mla, causal = B, False, False
+        elif cfg == 4:
+            B, H, N, D, bn = 16, 12, 512, 64, 64
+            dt, std = torch.bfloat16, 1.0
+            lq = torch.randint(64, 512 + 1, (B,), generator=gcpu)
+            lc = torch.tensor([4096])
+            cbs, mla, causal = 1, False, True
+        else:
+            B, H, N, D, bn = 8, 64, 2048, 512, 64
+            dt, std = torch.bfloat16, 0.5
+            lq = torch.randint(512, 2048 + 1, (B,), generator=gcpu)
+            lc = torch.full((B,), 8192)
+            cbs, mla, causal = B, True, False
+        prefill = variant == "prefill"
+        scale = 1.0 / math.sqrt(D)
+        q = _randn((B, H, N, D), gdev, device, dt, std)
+        k = _randn((B, H, N, D), gdev, device, dt, std)
+        v = k if mla else _randn((B, H, N, D), gdev, device, dt, std)
+        cu_kv = torch.zeros(lc.numel() + 1, dtype=torch.int32)
+        cu_kv[1:] = torch.cumsum(lc, 0)
+        Tc = int(cu_kv[-1])
+        hk = 1 if mla else H
+        k_cache = _randn((hk * Tc, D), gdev, device, dt, std)
+        v_cache = None if mla else _randn((hk * Tc, D), gdev, device, dt, std)
+        cache = fm.InferenceCache()
+        cache.prefill_kv_cache(
+            0, k_cache=k_cache, v_cache=v_cache, total_context_len=Tc, cu_seqlens_kv=cu_kv.to(device),
+            context_batch_size=cbs, is_mla=mla, num_heads=H, head_dim=D,
+        )
+        meta = cache.packing.get_pack_metadata(lq.to(device=device, dtype=torch.int32), N=N, block_n=bn)
+        kw = dict(is_mla=mla, block_n=bn, causal_query_seq_attn=causal)
+
+        def step():
+            out = fm.flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, prefill=prefill, **kw)
+            return fm.unpack_from_kernel(out, meta, H)
+
+        # the attention launch alone; prefill replaces the layer entry, so plan it on a copy
+        plan_cache = cache
+        if prefill:
+            plan_cache = fm.InferenceCache()
+            plan_cache._layer_kv = dict(cache._layer_kv)
+        plan = fm.host.host._compressed_impl(
+            q, k, v, H, meta, scale, plan_cache, 0, mla, None, 64, bn, False, prefill, causal, run=False
+        )[1]
+        lengths_ctx = [int(lc[0])] * B if cbs == 1 else [int(x) for x in lc]
+        names = {
+            3: "cfg3 packed varlen fp16 B=32 H=16 N=1024 D=128, per-seq cached ctx U[512,2048]",
+            4: "cfg4 packed causal_query_seq_attn bf16 B=16 H=12 D=64, shared ctx 4096",
+            5: "cfg5 MLA bf16 B=8 64 heads : 1 latent D=512, cached latent ctx 8192/seq",
+        }
+        return Case(
+            cfg, names[cfg] + (" (prefill=True)" if prefill else ""), dt, H, D,
+            [int(x) for x in lq], lengths_ctx, causal, prefill, mla,
+            step=step,
+            attention=plan,
+            tensors=dict(q=q, k=k, v=v, k_cache=k_cache, v_cache=v_cache, cu_kv=cu_kv, meta=meta,
+                         scale=scale, cache=cache, cbs=cbs, Tc=Tc),
+            config=dict(B=B, H=H, N=N, D=D, block_n=bn, seed=seed, total_q_tokens=int(lq.sum()),
+                        total_ctx_tokens=Tc, unique_ctx_tokens=Tc, context_batch_size=cbs),
+        )
+    raise ValueError(f"unknown config {cfg}")
+
+
+def _time_steps(fn, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def _kernel_ms(attention, reps: int) -> float:
+    """Average attention-kernel duration: HIP events on the launch stream around
+    `reps` back-to-back prepared launches (host enqueue is far faster than the kernel)."""
+    stream = torch.cuda.ExternalStream(attention.stream) if attention.stream else torch.cuda.current_stream()
+    for _ in range(3):
+        attention()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        attention()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def cpu_baseline(case: Case, budget_s: float = 20.0) -> dict:
+    """The reference's per-sequence PyTorch SDPA path (oracle/cpu_baseline.py) on this
+    host's CPU cores, fp32, over a bounded prefix of the workload's sequences."""
+    sys.path.insert(0, str(REPO))
+    from oracle import cpu_baseline as cb
+
+    return cb.time_case(case, budget_s=budget_s)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=DEFAULT_CONFIG)
+    ap.add_argument("--variant", default="")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(
+            "bench.py measures one GPU only: this path has no multi-GPU implementation in this "
+            "build (it would shard by head with no exchange); run with --gpus 1",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    case = make_case(args.config, device, variant=args.variant)
+    print(f"[bench] {case.workload}: built inputs", file=sys.stderr, flush=True)
+
+    ms = _time_steps(case.step, args.steps, args.warmup)
+    print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step", file=sys.stderr, flush=True)
+    kms = _kernel_ms(case.attention, args.kernel_reps)
+    print(f"[bench] attention kernel: {kms:.4f} ms", file=sys.stderr, flush=True)
+
+    F = case.flops
+    value = F / (ms * 1e-3) / 1e12
+    k_tflops = F / (kms * 1e-3) / 1e12
+    peak = MFMA_PEAK_TFLOPS[case.dtype]
+    roofline = {
+        "bound": "mfma",
+        "achieved": round(k_tflops, 3),
+        "peak": peak,
+        "unit": "TFLOP/s",
+        "frac": round(k_tflops / peak, 5),
+        "traffic": None,
+        "kernel_ms": round(kms, 5),
+        "algorithmic_bytes": case.attention_bytes,
+    }
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(case)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_NAMES[case.dtype],
+        "data": "synthetic (seeded normal inputs, seeded uniform lengths)",
+        "config": {"workload": case.workload, **case.config,
+                   "effective_gflop": round(F / 1e9, 4),
+                   "reference_formula_gflop": round(case.flops_reference_formula / 1e9, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,368 @@
+// Indexing kernels of the packed MLM path: pack metadata, pack and unpack.
+//
+// These replace the torch-op chains of the reference host layer:
+//   build_pack_metadata / _build_query_tile_map_from_cu_seqlens  host_utils.py:27-107
+//   _pack_flatten_for_kernel_into (+ its permute().contiguous())  host_utils.py:397-420
+//   unpack_from_kernel (zeros + index_copy_ + permute)           host_utils.py:587-615
+// Each is one pass over HBM: pack reads every valid padded row once and writes
+// every packed row once; unpack writes every padded row once (zeros included).
+#include "fmlm_common.h"
+
+namespace fmlm {
+
+// ---------------------------------------------------------------------------
+// Pack metadata, step 1: one workgroup scans the lengths.
+//   cu[0] = 0, cu[i+1] = cu[i] + L_i                         (host_utils.py:49-50)
+//   tiles_i = ceil(L_i / block_n), tp = exclusive scan       (host_utils.py:84-96)
+// Lengths outside [0, N] are counted (host_utils.py:42-43) and treated as 0 in
+// the scan so every later index stays in bounds.
+// ---------------------------------------------------------------------------
+constexpr int kScanThreads = 1024;
+
+template <typename LT>
+__global__ __launch_bounds__(kScanThreads) void metadata_scan_kernel(
+    const LT* __restrict__ lengths, int B, int N, int block_n, int32_t* __restrict__ lengths_i32,
+    int32_t* __restrict__ aux) {
+  __shared__ int s_len[kScanThreads];
+  __shared__ int s_til[kScanThreads];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  int32_t* cu = aux;
+  int32_t* summary = aux + B + 1;
+  int32_t* tp = aux + B + 5;
+  if (tid == 0) {
+    s_bad = 0;
+    cu[0] = 0;
+    tp[0] = 0;
+  }
+  int carry_len = 0, carry_til = 0;
+  __syncthreads();
+  for (int base = 0; base < B; base += kScanThreads) {
+    const int i = base + tid;
+    int len = 0;
+    if (i < B) {
+      const LT raw = lengths[i];
+      const bool ok = raw >= 0 && raw <= (LT)N;
+      lengths_i32[i] = (int32_t)raw;
+      if (!ok) atomicAdd(&s_bad, 1);
+      len = ok ? (int)raw : 0;
+    }
+    s_len[tid] = len;
+    s_til[tid] = (len + block_n - 1) / block_n;
+    __syncthreads();
+    // Hillis-Steele inclusive scan over the chunk.
+    for (int off = 1; off < kScanThreads; off <<= 1) {
+      int a = 0, t = 0;
+      if (tid >= off) {
+        a = s_len[tid - off];
+        t = s_til[tid - off];
+      }
+      __syncthreads();
+      s_len[tid] += a;
+      s_til[tid] += t;
+      __syncthreads();
+    }
+    if (i < B) {
+      cu[i + 1] = carry_len + s_len[tid];
+      tp[i + 1] = carry_til + s_til[tid];
+    }
+    carry_len += s_len[kScanThreads - 1];
+    carry_til += s_til[kScanThreads - 1];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    summary[0] = carry_len;  // total_tokens
+    summary[1] = carry_til;  // n_tiles
+    summary[2] = s_bad;      // lengths outside [0, N]
+    summary[3] = 0;
+  }
+}
+
+// Pack metadata, step 2: every (b, t < L_b) writes its packed token index and
+// every (b, j < tiles_b) its tile entry (host_utils.py:52-55, 97-106).
+__global__ __launch_bounds__(256) void metadata_fill_kernel(
+    const int32_t* __restrict__ lengths_i32, const int32_t* __restrict__ aux, int B, int N,
+    int block_n, int chunks_per_seq, int64_t* __restrict__ token_indices,
+    int32_t* __restrict__ batch_ids, int32_t* __restrict__ tile_starts) {
+  if (aux[B + 3] != 0) return;  // invalid lengths: the host raises
+  const int b = blockIdx.x / chunks_per_seq;
+  const int t = (blockIdx.x % chunks_per_seq) * 256 + threadIdx.x;
+  const int len = lengths_i32[b];
+  const int start = aux[b];
+  if (t < len) token_indices[start + t] = (int64_t)b * N + t;
+  const int tiles = (len + block_n - 1) / block_n;
+  if (t < tiles) {
+    const int slot = aux[B + 5 + b] + t;
+    batch_ids[slot] = b;
+    tile_starts[slot] = start + t * block_n;
+  }
+}
+
+// Tile map from cu_seqlens (host_utils.py:74-107): one workgroup scans the tile
+// counts and writes (b, cu[b] + j*block_n) for every tile, capped at capacity.
+__global__ __launch_bounds__(kScanThreads) void tile_map_kernel(const int32_t* __restrict__ cu,
+                                                                int B, int block_n, int capacity,
+                                                                int32_t* __restrict__ batch_ids,
+                                                                int32_t* __restrict__ tile_starts,
+                                                                int32_t* __restrict__ count) {
+  __shared__ int s_til[kScanThreads];
+  const int tid = threadIdx.x;
+  int carry = 0;
+  for (int base = 0; base < B; base += kScanThreads) {
+    const int b = base + tid;
+    int tiles = 0, start = 0;
+    if (b < B) {
+      start = cu[b];
+      const int len = cu[b + 1] - start;
+      tiles = len > 0 ? (len + block_n - 1) / block_n : 0;
+    }
+    s_til[tid] = tiles;
+    __syncthreads();
+    for (int off = 1; off < kScanThreads; off <<= 1) {
+      const int t = tid >= off ? s_til[tid - off] : 0;
+      __syncthreads();
+      s_til[tid] += t;
+      __syncthreads();
+    }
+    const int first = carry + s_til[tid] - tiles;
+    for (int j = 0; j < tiles && first + j < capacity; ++j) {
+      batch_ids[first + j] = b;
+      tile_starts[first + j] = start + j * block_n;
+    }
+    carry += s_til[kScanThreads - 1];
+    __syncthreads();
+  }
+  if (tid == 0) *count = carry;
+}
+
+// ---------------------------------------------------------------------------
+// Pack: one thread per VB-byte chunk of a packed row.
+// ---------------------------------------------------------------------------
+template <int VB>
+struct VecOf;
+template <>
+struct VecOf<16> {
+  typedef u32x4 type;
+};
+template <>
+struct VecOf<8> {
+  typedef u32x2 type;
+};
+template <>
+struct VecOf<4> {
+  typedef uint32_t type;
+};
+template <>
+struct VecOf<2> {
+  typedef uint16_t type;
+};
+template <>
+struct VecOf<1> {
+  typedef uint8_t type;
+};
+
+struct PackArgs {
+  fmlm_pack_tensor t[3];
+};
+
+template <int VB>
+__global__ __launch_bounds__(256) void pack_kernel(PackArgs args, int esz, int B, int N, int D,
+                                                   const int32_t* __restrict__ cu, int T,
+                                                   int T_pad) {
+  typedef typename VecOf<VB>::type V;
+  const fmlm_pack_tensor& tt = args.t[blockIdx.y];
+  const int cpr = D * esz / VB;  // chunks per row
+  const int64_t total = (int64_t)tt.heads * T_pad * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
+       c += (int64_t)gridDim.x * blockDim.x) {
+    const int chunk = (int)(c % cpr);
+    const int64_t row = c / cpr;  // h*T_pad + t
+    const int t = (int)(row % T_pad);
+    const int h = (int)(row / T_pad);
+    V val = V{};
+    int b = 0, p = N;
+    if (t < T) {
+      if (cu) {
+        b = find_seq(cu, B, t);
+        p = t - cu[b];
+      } else {
+        b = t / N;
+        p = t - b * N;
+      }
+    }
+    if (p < N) {  // p >= N only for t >= T or an inconsistent cu: leave the row zero
+      const char* src = (const char*)tt.src +
+                        ((int64_t)b * tt.s_sb + (int64_t)h * tt.s_sh + (int64_t)p * tt.s_sn) * esz;
+      val = *(const V*)(src + (int64_t)chunk * VB);
+    }
+    *(V*)((char*)tt.dst + row * D * esz + (int64_t)chunk * VB) = val;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Unpack: one thread per VB-byte chunk of a padded output row (b, h, n).
+// ---------------------------------------------------------------------------
+template <int VB>
+__global__ __launch_bounds__(256) void unpack_kernel(const char* __restrict__ packed, int64_t p_sh,
+                                                     char* __restrict__ dst, int B, int H, int N,
+                                                     int D, int esz,
+                                                     const int32_t* __restrict__ cu) {
+  typedef typename VecOf<VB>::type V;
+  const int cpr = D * esz / VB;
+  const int64_t total = (int64_t)B * H * N * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
+       c += (int64_t)gridDim.x * blockDim.x) {
+    const int chunk = (int)(c % cpr);
+    const int64_t row = c / cpr;  // (b*H + h)*N + n
+    const int n = (int)(row % N);
+    const int64_t bh = row / N;
+    const int h = (int)(bh % H);
+    const int b = (int)(bh / H);
+    const int start = cu[b];
+    const int len = cu[b + 1] - start;
+    V val;
+    if (n < len)
+      val = *(const V*)(packed + ((int64_t)h * p_sh + (int64_t)(start + n) * D) * esz +
+                        (int64_t)chunk * VB);
+    else
+      val = V{};
+    *(V*)(dst + row * D * esz + (int64_t)chunk * VB) = val;
+  }
+}
+
+// Widest vector width (bytes) that divides the row size and every address.
+static int pick_vec(int64_t row_bytes, std::initializer_list<uint64_t> addrs_bytes) {
+  for (int vb : {16, 8, 4, 2, 1}) {
+    if (row_bytes % vb) continue;
+    bool ok = true;
+    for (uint64_t a : addrs_bytes) ok = ok && (a % vb == 0);
+    if (ok) return vb;
+  }
+  return 0;
+}
+
+static int grid_for(int64_t work, int threads) {
+  int64_t g = (work + threads - 1) / threads;
+  const int64_t cap = 256 * 64;  // grid-stride beyond 64 workgroups per CU
+  if (g > cap) g = cap;
+  return (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace fmlm
+
+using namespace fmlm;
+
+extern "C" int fmlm_abi_version(void) { return FMLM_ABI_VERSION; }
+extern "C" int fmlm_pack_tensor_size(void) { return (int)sizeof(fmlm_pack_tensor); }
+
+extern "C" int fmlm_pack_metadata(const void* lengths, int32_t lengths_is_i64, int32_t B,
+                                  int32_t N, int32_t block_n, int32_t* lengths_i32, int32_t* aux,
+                                  int64_t* token_indices, int32_t* batch_ids,
+                                  int32_t* tile_starts, void* stream) {
+  if (B < 0 || N < 0 || block_n < 1 || !aux) return FMLM_E_ARG;
+  if (B > 0 && (!lengths || !lengths_i32)) return FMLM_E_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  if (lengths_is_i64)
+    hipLaunchKernelGGL(metadata_scan_kernel<int64_t>, dim3(1), dim3(kScanThreads), 0, s,
+                       (const int64_t*)lengths, B, N, block_n, lengths_i32, aux);
+  else
+    hipLaunchKernelGGL(metadata_scan_kernel<int32_t>, dim3(1), dim3(kScanThreads), 0, s,
+                       (const int32_t*)lengths, B, N, block_n, lengths_i32, aux);
+  int rc = launch_status();
+  if (rc || B == 0 || N == 0) return rc;
+  if (!token_indices || !batch_ids || !tile_starts) return FMLM_E_ARG;
+  const int chunks = (N + 255) / 256;
+  const int64_t blocks = (int64_t)B * chunks;
+  if (blocks > 0x7fffffff) return FMLM_E_ARG;
+  hipLaunchKernelGGL(metadata_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, s, lengths_i32,
+                     aux, B, N, block_n, chunks, token_indices, batch_ids, tile_starts);
+  return launch_status();
+}
+
+extern "C" int fmlm_tile_map(const int32_t* cu_seqlens, int32_t B, int32_t block_n,
+                             int32_t capacity, int32_t* batch_ids, int32_t* tile_starts,
+                             int32_t* count, void* stream) {
+  if (B < 0 || block_n < 1 || capacity < 0 || !count) return FMLM_E_ARG;
+  if (B > 0 && !cu_seqlens) return FMLM_E_ARG;
+  if (capacity > 0 && (!batch_ids || !tile_starts)) return FMLM_E_ARG;
+  hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(kScanThreads), 0, (hipStream_t)stream,
+                     cu_seqlens, B, block_n, capacity, batch_ids, tile_starts, count);
+  return launch_status();
+}
+
+static bool valid_elem_bytes(int e) { return e == 1 || e == 2 || e == 4 || e == 8; }
+
+extern "C" int fmlm_pack(const fmlm_pack_tensor* tensors, int32_t n_tensors, int32_t elem_bytes,
+                         int32_t B, int32_t N, int32_t D, const int32_t* cu_seqlens, int32_t T,
+                         int32_t T_pad, void* stream) {
+  const int esz = elem_bytes;
+  if (!valid_elem_bytes(esz)) return FMLM_E_DTYPE;
+  if (!tensors || n_tensors < 1 || n_tensors > 3 || B < 0 || N < 0 || D < 1 || T < 0 ||
+      T_pad < T)
+    return FMLM_E_ARG;
+  if (!cu_seqlens && T != B * N) return FMLM_E_ARG;
+  PackArgs args = {};
+  int64_t max_work = 0;
+  int vb = 16;
+  for (int i = 0; i < n_tensors; ++i) {
+    const fmlm_pack_tensor& t = tensors[i];
+    if (t.heads < 1 || !t.dst || (T > 0 && !t.src)) return FMLM_E_ARG;
+    args.t[i] = t;
+    const int v = pick_vec((int64_t)D * esz,
+                           {(uint64_t)t.src, (uint64_t)t.dst, (uint64_t)(t.s_sb * esz),
+                            (uint64_t)(t.s_sh * esz), (uint64_t)(t.s_sn * esz)});
+    if (!v) return FMLM_E_ALIGN;
+    vb = v < vb ? v : vb;
+    const int64_t w = (int64_t)t.heads * T_pad * D * esz;
+    max_work = w > max_work ? w : max_work;
+  }
+  if (T_pad == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(grid_for(max_work / vb, 256), n_tensors);
+#define FMLM_PACK_CASE(VB)                                                                       \
+  case VB:                                                                                       \
+    hipLaunchKernelGGL(pack_kernel<VB>, grid, dim3(256), 0, s, args, esz, B, N, D, cu_seqlens, \
+                       T, T_pad);                                                                \
+    break;
+  switch (vb) {
+    FMLM_PACK_CASE(16)
+    FMLM_PACK_CASE(8)
+    FMLM_PACK_CASE(4)
+    FMLM_PACK_CASE(2)
+    FMLM_PACK_CASE(1)
+  }
+#undef FMLM_PACK_CASE
+  return launch_status();
+}
+
+extern "C" int fmlm_unpack(int32_t elem_bytes, const void* packed, int64_t p_sh, void* dst,
+                           int32_t B, int32_t H, int32_t N, int32_t D, const int32_t* cu_seqlens,
+                           void* stream) {
+  const int esz = elem_bytes;
+  if (!valid_elem_bytes(esz)) return FMLM_E_DTYPE;
+  if (B < 0 || H < 0 || N < 0 || D < 1 || p_sh < 0 || !cu_seqlens) return FMLM_E_ARG;
+  const int64_t rows = (int64_t)B * H * N;
+  if (rows == 0) return 0;
+  if (!dst) return FMLM_E_ARG;
+  const int vb = pick_vec((int64_t)D * esz,
+                          {(uint64_t)packed, (uint64_t)dst, (uint64_t)(p_sh * esz)});
+  if (!vb) return FMLM_E_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(grid_for(rows * D * esz / vb, 256));
+  const char* pk = (const char*)packed;
+  char* out = (char*)dst;
+#define FMLM_UNPACK_CASE(VB)                                                                    \
+  case VB:                                                                                      \
+    hipLaunchKernelGGL(unpack_kernel<VB>, grid, dim3(256), 0, s, pk, p_sh, out, B, H, N, D, esz, \
+                       cu_seqlens);                                                             \
+    break;
+  switch (vb) {
+    FMLM_UNPACK_CASE(16)
+    FMLM_UNPACK_CASE(8)
+    FMLM_UNPACK_CASE(4)
+    FMLM_UNPACK_CASE(2)
+    FMLM_UNPACK_CASE(1)
+  }
+#undef FMLM_UNPACK_CASE
+  return launch_status();
+}

@@ -1,0 +1,297 @@
+"""Host-side state of the MLM attention path: pack metadata, packing workspaces and
+the per-layer KV context cache.
+
+Mirrors src/flash_mlm/host/cache.py of the reference (PackMetadata :5-17,
+PackingCache :20-73, LayerKVEntry :76-87, InferenceCache :90-280): the same
+fields, the same lookup keys, the same ValueError messages, and the same
+"store views, never copy" contract for cached KV.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+
+@dataclass
+class PackMetadata:
+    """Indexing of a padded [B, N] batch as packed variable-length tokens.
+
+    Fields follow the reference (cache.py:5-17).  ``cu_seqlens_host`` is an extra,
+    optional host copy of ``cu_seqlens`` filled by :func:`build_pack_metadata`; it lets
+    the launchers size padded workspaces without a device-to-host synchronisation.
+    ``kernel_schedules`` caches the attention kernel's device work lists built from
+    ``cu_seqlens`` (one per kernel tile size), so repeated layers skip rebuilding them.
+    """
+
+    B: int
+    N: int
+    lengths: torch.Tensor
+    cu_seqlens: torch.Tensor
+    token_indices: torch.Tensor
+    total_tokens: int
+    batch_ids_block_n: int
+    batch_ids_q: torch.Tensor
+    q_tile_starts_q: torch.Tensor
+    cu_seqlens_host: tuple[int, ...] | None = field(default=None, repr=False, compare=False)
+    kernel_schedules: dict = field(default_factory=dict, repr=False, compare=False)
+
+    def host_cu_seqlens(self) -> tuple[int, ...]:
+        if self.cu_seqlens_host is None:
+            self.cu_seqlens_host = tuple(int(x) for x in self.cu_seqlens.to("cpu").tolist())
+        return self.cu_seqlens_host
+
+
+class PackingCache:
+    """Grow-only named 2-D workspaces plus a memo of pack metadata (cache.py:20-73)."""
+
+    def __init__(self) -> None:
+        self._buffers: dict[tuple, torch.Tensor] = {}
+        self._pack_meta: dict[tuple, PackMetadata] = {}
+
+    def get_2d(
+        self,
+        name: str,
+        rows: int,
+        cols: int,
+        *,
+        dtype: torch.dtype,
+        device: torch.device,
+    ) -> torch.Tensor:
+        """Return a [rows, cols] view of the workspace ``name``, reallocating only to grow."""
+        if rows < 0:
+            raise ValueError("rows must be >= 0")
+        if cols < 1:
+            raise ValueError("cols must be >= 1")
+        device = torch.device(device)
+        key = (name, device.type, device.index, dtype, cols)
+        buf = self._buffers.get(key)
+        if buf is None or buf.shape[0] < rows:
+            buf = torch.empty((rows, cols), dtype=dtype, device=device)
+            self._buffers[key] = buf
+        return buf[:rows]
+
+    def get_pack_metadata(self, lengths: torch.Tensor, *, N: int, block_n: int) -> PackMetadata:
+        """Memoised :func:`build_pack_metadata`, keyed by (device, N, block_n, lengths)."""
+        signature = tuple(int(x) for x in lengths.to(device="cpu", dtype=torch.int32).tolist())
+        key = (lengths.device.type, lengths.device.index, N, block_n, signature)
+        meta = self._pack_meta.get(key)
+        if meta is None:
+            from flash_mlm.host.host_utils import build_pack_metadata
+
+            meta = build_pack_metadata(lengths, N, block_n)
+            self._pack_meta[key] = meta
+        return meta
+
+    def clear(self) -> None:
+        self._buffers.clear()
+        self._pack_meta.clear()
+
+
+@dataclass
+class LayerKVEntry:
+    """One layer's cached context (cache.py:76-87).
+
+    Layout of ``k_cache`` / ``v_cache`` rows:
+      * MLA: one shared latent head, row = token            ([total_context_len, D])
+      * non-MLA, packed entries: head-major, row = h*total_context_len + token
+      * non-MLA, dense entries: [context_batch, H, context_len] flattened
+    """
+
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor | None
+    total_context_len: int
+    cu_seqlens_kv: torch.Tensor | None
+    context_batch_size: int
+    is_mla: bool
+    num_heads: int
+    head_dim: int
+    dtype: torch.dtype
+    device: torch.device
+
+
+def _check_rank2(t: torch.Tensor, what: str) -> None:
+    if t.ndim != 2:
+        raise ValueError(f"{what} must be a rank-2 packed tensor")
+
+
+class InferenceCache:
+    """Layer-scoped KV context store plus a :class:`PackingCache` (cache.py:90-280).
+
+    Entries hold the given tensors themselves (views, no copies); storing a layer
+    again replaces its entry.
+    """
+
+    def __init__(self) -> None:
+        self.packing = PackingCache()
+        self._layer_kv: dict[str, LayerKVEntry] = {}
+
+    @staticmethod
+    def _layer_key(layer_id: int | str) -> str:
+        return str(layer_id)
+
+    @staticmethod
+    def _validate_kv_common_inputs(
+        *,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor | None,
+        total_context_len: int,
+        is_mla: bool,
+        num_heads: int,
+        head_dim: int,
+    ) -> None:
+        _check_rank2(k_cache, "k_cache")
+        if k_cache.shape[1] != head_dim:
+            raise ValueError("k_cache second dim must match head_dim")
+        if not k_cache.is_contiguous():
+            raise ValueError("k_cache must be contiguous")
+        if is_mla:
+            if v_cache is not None:
+                _check_rank2(v_cache, "MLA v_cache")
+                if v_cache.shape != k_cache.shape:
+                    raise ValueError("MLA v_cache shape must match k_cache shape")
+                if not v_cache.is_contiguous():
+                    raise ValueError("MLA v_cache must be contiguous")
+        else:
+            if v_cache is None:
+                raise ValueError("non-MLA cache requires v_cache")
+            _check_rank2(v_cache, "v_cache")
+            if v_cache.shape != k_cache.shape:
+                raise ValueError("v_cache shape must match k_cache shape")
+            if v_cache.shape[1] != head_dim:
+                raise ValueError("v_cache second dim must match head_dim")
+            if not v_cache.is_contiguous():
+                raise ValueError("v_cache must be contiguous")
+        rows = total_context_len * (1 if is_mla else num_heads)
+        if k_cache.shape[0] != rows:
+            raise ValueError(f"k_cache first dim mismatch: expected {rows} rows for is_mla={is_mla}")
+        if not is_mla and v_cache.shape[0] != rows:
+            raise ValueError(f"v_cache first dim mismatch: expected {rows} rows for is_mla={is_mla}")
+
+    @staticmethod
+    def _validate_kv_entry_inputs(
+        *,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor | None,
+        total_context_len: int,
+        cu_seqlens_kv: torch.Tensor,
+        context_batch_size: int,
+        is_mla: bool,
+        num_heads: int,
+        head_dim: int,
+    ) -> None:
+        InferenceCache._validate_kv_common_inputs(
+            k_cache=k_cache,
+            v_cache=v_cache,
+            total_context_len=total_context_len,
+            is_mla=is_mla,
+            num_heads=num_heads,
+            head_dim=head_dim,
+        )
+        if cu_seqlens_kv.ndim != 1 or cu_seqlens_kv.numel() < 2:
+            raise ValueError("cu_seqlens_kv must be rank-1 with at least 2 elements")
+        if context_batch_size < 1:
+            raise ValueError("context_batch_size must be >= 1")
+        if cu_seqlens_kv.numel() < context_batch_size + 1:
+            raise ValueError("context_batch_size is incompatible with cu_seqlens_kv length")
+
+    def prefill_kv_cache(
+        self,
+        layer_id: int | str,
+        *,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor | None = None,
+        total_context_len: int | None = None,
+        cu_seqlens_kv: torch.Tensor | None = None,
+        context_batch_size: int,
+        is_mla: bool,
+        num_heads: int,
+        head_dim: int,
+    ) -> None:
+        """Store pre-packed KV buffers as the context of ``layer_id`` (no copy)."""
+        if context_batch_size < 1:
+            raise ValueError("context_batch_size must be >= 1")
+        if num_heads < 1:
+            raise ValueError("num_heads must be >= 1")
+
+        if total_context_len is not None:
+            total_context_len = int(total_context_len)
+        elif is_mla:
+            total_context_len = int(k_cache.shape[0])
+        else:
+            if k_cache.shape[0] % num_heads:
+                raise ValueError("non-MLA k_cache rows must be divisible by num_heads")
+            total_context_len = int(k_cache.shape[0] // num_heads)
+
+        if cu_seqlens_kv is None:
+            self._validate_kv_common_inputs(
+                k_cache=k_cache,
+                v_cache=v_cache,
+                total_context_len=total_context_len,
+                is_mla=is_mla,
+                num_heads=num_heads,
+                head_dim=head_dim,
+            )
+            if total_context_len % context_batch_size:
+                raise ValueError(
+                    "when cu_seqlens_kv is omitted, total_context_len must be divisible by "
+                    "context_batch_size"
+                )
+        else:
+            self._validate_kv_entry_inputs(
+                k_cache=k_cache,
+                v_cache=v_cache,
+                total_context_len=total_context_len,
+                cu_seqlens_kv=cu_seqlens_kv,
+                context_batch_size=context_batch_size,
+                is_mla=is_mla,
+                num_heads=num_heads,
+                head_dim=head_dim,
+            )
+
+        self._layer_kv[self._layer_key(layer_id)] = LayerKVEntry(
+            k_cache=k_cache,
+            v_cache=None if is_mla else v_cache,
+            total_context_len=total_context_len,
+            cu_seqlens_kv=None if cu_seqlens_kv is None else cu_seqlens_kv.contiguous(),
+            context_batch_size=int(context_batch_size),
+            is_mla=bool(is_mla),
+            num_heads=int(num_heads),
+            head_dim=int(head_dim),
+            dtype=k_cache.dtype,
+            device=k_cache.device,
+        )
+
+    def get_kv_cache(
+        self,
+        layer_id: int | str,
+        *,
+        is_mla: bool,
+        num_heads: int,
+        head_dim: int,
+        dtype: torch.dtype,
+        device: torch.device,
+    ) -> LayerKVEntry:
+        """Return the entry of ``layer_id``; ValueError if absent or of another shape/mode."""
+        entry = self._layer_kv.get(self._layer_key(layer_id))
+        if entry is None:
+            raise ValueError(f"No cached KV context for layer_id={layer_id}")
+        checks = (
+            (entry.is_mla == is_mla, "Cached KV mode (is_mla) does not match request"),
+            (entry.num_heads == num_heads, "Cached num_heads does not match request"),
+            (entry.head_dim == head_dim, "Cached head_dim does not match request"),
+            (entry.dtype == dtype, "Cached KV dtype does not match request"),
+            (entry.device == device, "Cached KV device does not match request"),
+        )
+        for ok, message in checks:
+            if not ok:
+                raise ValueError(message)
+        return entry
+
+    def clear_layer(self, layer_id: int | str) -> None:
+        self._layer_kv.pop(self._layer_key(layer_id), None)
+
+    def clear(self) -> None:
+        self.packing.clear()
+        self._layer_kv.clear()

@@ -1,0 +1,605 @@
+"""Launchers of the fused MLM attention path on MI355X.
+
+Public signatures, argument meaning, cache/prefill semantics and ValueError
+messages follow src/flash_mlm/host/host.py of the reference:
+  flash_attn_mlm                (host.py:47-225)
+  flash_attn_mlm_compressed     (host.py:228-530)
+  flash_attn_mlm_precompressed  (host.py:533-789)
+
+What changes is below the API: one HIP kernel (fmlm_attn_fwd, C ABI in
+include/flash_mlm_hip.h) reads the padded [B, H, N, D] q/k/v directly through
+(sequence, head, position) addressing, so the compressed path does not pack
+q/k/v at all unless prefill asks for a packed cache entry; the output is written
+straight into the packed [H*T, D] result (no unpad copy).  ``block_m`` /
+``block_n`` / ``auto_tune_tiles`` keep their role in the metadata contract and in
+the padded prefill length; the HIP kernel picks its own tiles from the head dim.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from flash_mlm import _lib
+from flash_mlm.host.cache import InferenceCache, PackMetadata
+from flash_mlm.host.host_utils import (
+    _compute_total_q_len_padded,
+    _device_scope,
+    _maybe_get_cache_context,
+    _pack_rows,
+    make_contiguous,
+    require_cuda_tensors,
+    validate_cache_request,
+    validate_cu_seqlens_rank1_min2,
+    validate_head_dim_supported,
+    validate_packed_cache_shapes,
+    validate_qkv_same_shape_rank4,
+)
+
+# largest BLOCK_M the reference's autotuner may pick (mlm_kernel.py:114); it sets the
+# padded prefill length when auto_tune_tiles=True (host.py:326)
+_AUTOTUNE_MAX_BLOCK_M = 128
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    """Row-addressable by the kernel: unit stride in D, 16-byte aligned rows."""
+    if t.numel() == 0:
+        return True
+    es = t.element_size()
+    if t.stride(-1) != 1 or t.data_ptr() % 16:
+        return False
+    return all((s * es) % 16 == 0 for s in t.stride()[:-1])
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    return t if _aligned(t) else t.contiguous()
+
+
+def _workspace(inference_cache: InferenceCache | None, nbytes: int, device: torch.device):
+    if nbytes <= 0:
+        return None
+    if inference_cache is not None:
+        return inference_cache.packing.get_2d("fmlm:attn_workspace", 1, nbytes, dtype=torch.uint8, device=device)
+    return torch.empty((1, nbytes), dtype=torch.uint8, device=device)
+
+
+class AttnLaunch:
+    """A prepared fmlm_attn_fwd call: the parameter block plus the tensors it points to."""
+
+    __slots__ = ("lib", "params", "stream", "device", "keep")
+
+    def __init__(self, lib, params, stream, device, keep):
+        self.lib, self.params, self.stream, self.device, self.keep = lib, params, stream, device, keep
+
+    def __call__(self) -> None:
+        with _device_scope(self.device):
+            rc = self.lib.fmlm_attn_fwd(self.params, self.stream)
+        _lib.check(rc, "fmlm_attn_fwd")
+
+
+def _launch(*, run: bool = True, **kw) -> AttnLaunch:
+    plan = _prepare(**kw)
+    if run:
+        plan()
+    return plan
+
+
+def _prepare(
+    *,
+    q: torch.Tensor,
+    out: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor | None,
+    B: int,
+    H: int,
+    D: int,
+    N: int,
+    total_q: int,
+    cu_seqlens_q: torch.Tensor | None,
+    q_strides: tuple[int, int, int],
+    q_layout: int,
+    o_strides: tuple[int, int, int],
+    o_layout: int,
+    k_strides: tuple[int, int, int],
+    v_strides: tuple[int, int, int],
+    kv_layout: int,
+    k_ctx: torch.Tensor,
+    v_ctx: torch.Tensor | None,
+    c_strides: tuple[int, int, int],
+    cu_seqlens_kv: torch.Tensor | None,
+    ctx_len: int,
+    ctx_batch: int,
+    ctx_rows: int,
+    scale: float,
+    flags: int,
+    inference_cache: InferenceCache | None,
+    schedule_cache: dict | None = None,
+) -> AttnLaunch:
+    lib = _lib.load()
+    p = _lib.AttnParams()
+    p.dtype = _lib.dtype_code(q.dtype)
+    p.flags = flags
+    p.B, p.H, p.D, p.N = B, H, D, N
+    p.total_q = total_q
+    p.ctx_len = ctx_len
+    p.ctx_batch = ctx_batch
+    p.ctx_rows = ctx_rows
+    p.q_layout, p.o_layout, p.kv_layout = q_layout, o_layout, kv_layout
+    p.scale = float(scale)
+    p.cu_seqlens_q = _lib.ptr(cu_seqlens_q)
+    p.cu_seqlens_kv = _lib.ptr(cu_seqlens_kv)
+    p.q = q.data_ptr()
+    p.q_sb, p.q_sh, p.q_sn = q_strides
+    p.o = out.data_ptr()
+    p.o_sb, p.o_sh, p.o_sn = o_strides
+    p.k = k.data_ptr()
+    p.k_sb, p.k_sh, p.k_sn = k_strides
+    p.v = (v if v is not None else k).data_ptr()
+    p.v_sb, p.v_sh, p.v_sn = v_strides
+    p.k_ctx = k_ctx.data_ptr() if k_ctx.numel() else None
+    p.v_ctx = v_ctx.data_ptr() if (v_ctx is not None and v_ctx.numel()) else p.k_ctx
+    p.c_sb, p.c_sh, p.c_sn = c_strides
+    ws_bytes = int(lib.fmlm_attn_workspace_bytes(p))
+    _lib.check(ws_bytes if ws_bytes < 0 else 0, "fmlm_attn_workspace_bytes")
+    stream = _lib.stream_of(q.device)
+    with _device_scope(q.device):
+        if ws_bytes > 0 and schedule_cache is not None:
+            key = (p.dtype, D, B, total_q)
+            sched = schedule_cache.get(key)
+            if sched is None:
+                sched = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+                _lib.check(lib.fmlm_attn_schedule(p, sched.data_ptr(), ws_bytes, stream), "fmlm_attn_schedule")
+                schedule_cache[key] = sched
+            p.schedule = sched.data_ptr()
+            ws = None
+        else:
+            sched = None
+            ws = _workspace(inference_cache, ws_bytes, q.device)
+            p.workspace = None if ws is None else ws.data_ptr()
+            p.workspace_bytes = ws_bytes
+    keep = (q, out, k, v, k_ctx, v_ctx, cu_seqlens_q, cu_seqlens_kv, ws, sched)
+    return AttnLaunch(lib, p, stream, q.device, keep)
+
+
+def _check_cache_dtype(k_cache: torch.Tensor, q: torch.Tensor) -> None:
+    if k_cache.numel() and k_cache.dtype != q.dtype:
+        raise ValueError("cached context dtype must match q dtype")
+
+
+def flash_attn_mlm(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    inference_cache: InferenceCache | None = None,
+    layer_id: int | str | None = None,
+    is_mla: bool = False,
+    context_batch_size: int | None = None,
+    block_m: int = 64,
+    block_n: int = 32,
+    auto_tune_tiles: bool = False,
+    prefill: bool = False,
+) -> torch.Tensor:
+    """Dense MLM attention: q, k, v [B, H, N, D] -> out [B, H, N, D].
+
+    Every query attends (non-causally) to [cached context of its batch || all N keys
+    of its (b, h)].  Cached context rows (``InferenceCache`` entry of ``layer_id``):
+    MLA [context_batch * context_len, D] shared by all heads, otherwise
+    [context_batch, H, context_len, D] flattened; ``context_batch_size`` 1 shares
+    batch 0.  MLA keeps per-head main keys and uses V = K.  ``prefill=True`` skips
+    the context and afterwards stores this call's K/V (MLA: head 0 of k) as the
+    layer's new context with context_batch_size = B.
+    """
+    return _dense_impl(q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill)[0]
+
+
+def _dense_impl(q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill, run=True):
+    """Body of :func:`flash_attn_mlm`; returns (out, prepared launch or None)."""
+    b, h, n, d = validate_qkv_same_shape_rank4(q, k, v, error_prefix="q/k/v")
+    validate_cache_request(prefill=prefill, inference_cache=inference_cache, layer_id=layer_id)
+    ctx = _maybe_get_cache_context(
+        inference_cache=inference_cache,
+        layer_id=layer_id,
+        batch_size=b,
+        is_mla=is_mla,
+        num_heads=h,
+        head_dim=d,
+        context_batch_size=context_batch_size,
+        dtype=q.dtype,
+        device=q.device,
+        compressed=False,
+    )
+    k_cache, v_cache = ctx.k_cache, ctx.v_cache
+    cbs, context_len = ctx.context_batch_size, ctx.context_len
+
+    require_cuda_tensors(q, k, v, k_cache, v_cache)
+    if cbs is None or cbs < 1:
+        raise ValueError("context_batch_size must be >= 1")
+    validate_head_dim_supported(d, is_mla=is_mla)
+    if cbs > 1 and cbs < b and not prefill and context_len > 0:
+        raise ValueError("context_batch_size must be 1 or at least the batch size")
+    _check_cache_dtype(k_cache, q)
+
+    q_, k_, v_ = _rows(q), _rows(k), _rows(v)
+    k_cache, v_cache = make_contiguous(k_cache, v_cache)
+    out = torch.empty((b, h, n, d), dtype=q.dtype, device=q.device)
+
+    # dense context layout (mlm_kernel_impl.py:132-141)
+    if is_mla:
+        c_strides = (context_len * d, 0, d)
+    else:
+        c_strides = (h * context_len * d, context_len * d, d)
+    flags = (_lib.FLAG_MLA if is_mla else 0) | (_lib.FLAG_PREFILL if prefill else 0)
+    plan = None
+    if b * h * n > 0:
+        plan = _launch(
+            run=run,
+            q=q_,
+            out=out,
+            k=k_,
+            v=None if is_mla else v_,
+            B=b,
+            H=h,
+            D=d,
+            N=n,
+            total_q=b * n,
+            cu_seqlens_q=None,
+            q_strides=(q_.stride(0), q_.stride(1), q_.stride(2)),
+            q_layout=_lib.LAYOUT_PADDED,
+            o_strides=(out.stride(0), out.stride(1), out.stride(2)),
+            o_layout=_lib.LAYOUT_PADDED,
+            k_strides=(k_.stride(0), k_.stride(1), k_.stride(2)),
+            v_strides=(k_.stride(0), k_.stride(1), k_.stride(2))
+            if is_mla
+            else (v_.stride(0), v_.stride(1), v_.stride(2)),
+            kv_layout=_lib.LAYOUT_PADDED,
+            k_ctx=k_cache,
+            v_ctx=None if is_mla else v_cache,
+            c_strides=c_strides,
+            cu_seqlens_kv=None,
+            ctx_len=context_len,
+            ctx_batch=cbs,
+            ctx_rows=context_len,
+            scale=scale,
+            flags=flags,
+            inference_cache=inference_cache,
+        )
+
+    if prefill and inference_cache is not None:
+        # the dense entry stores this call's K/V with context_len = N per batch (host.py:206-223)
+        if is_mla:
+            k_prefill = torch.empty((b * n, d), dtype=k.dtype, device=k.device)
+            if k_prefill.numel():
+                _pack_rows(
+                    [(k[:, :1], 1)], [k_prefill], cu_seqlens=None, B=b, N=n, D=d, total=b * n, total_padded=b * n
+                )
+            v_prefill = k_prefill
+        else:
+            k_prefill = k.contiguous().view(b * h * n, d)
+            v_prefill = v.contiguous().view(b * h * n, d)
+        inference_cache.prefill_kv_cache(
+            layer_id,
+            k_cache=k_prefill,
+            v_cache=v_prefill,
+            context_batch_size=int(b),
+            is_mla=is_mla,
+            num_heads=h,
+            head_dim=d,
+        )
+    return out, plan
+
+
+def _packed_context(ctx, *, num_heads: int, d: int, is_mla: bool, b: int, prefill: bool):
+    """Strides / sizes of a packed (head-major) context entry, validated."""
+    total_context_len = int(ctx.total_context_len)
+    cu_kv = ctx.cu_seqlens_kv
+    cbs = ctx.context_batch_size
+    if cbs is None:
+        cbs = int(cu_kv.numel() - 1)
+    if cbs < 1:
+        raise ValueError("context_batch_size must be >= 1")
+    if cbs + 1 > cu_kv.numel():
+        raise ValueError("context_batch_size is incompatible with cu_seqlens_kv length")
+    if 1 < cbs < b and not prefill and total_context_len > 0:
+        raise ValueError("context_batch_size must be 1 or at least the batch size")
+    c_strides = (0, 0 if is_mla else total_context_len * d, d)
+    return cbs, c_strides
+
+
+def flash_attn_mlm_compressed(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    num_heads: int,
+    q_meta: PackMetadata,
+    scale: float,
+    inference_cache: InferenceCache | None = None,
+    layer_id: int | str | None = None,
+    is_mla: bool = False,
+    context_batch_size: int | None = None,
+    block_m: int = 64,
+    block_n: int = 32,
+    auto_tune_tiles: bool = False,
+    prefill: bool = False,
+    causal_query_seq_attn: bool = False,
+) -> torch.Tensor:
+    """Packed variable-length MLM attention over padded q/k/v [B, H, N, D].
+
+    Query token t < L_b of sequence b attends to [its cached context
+    cu_seqlens_kv[cb]..cu_seqlens_kv[cb+1] || main keys], main keys being the tokens of
+    sequence b, or with ``causal_query_seq_attn`` the packed tokens of sequences 0..b.
+    Returns the packed output [H * T, D] (T = q_meta.total_tokens, head-major).
+    MLA: main K = V = head 0 of k (``v`` is ignored), context is a shared latent.
+    ``prefill=True`` skips the context and stores this call's packed, zero-padded
+    K/V [H_kv * T_pad, D] as the layer's context (cu_seqlens_kv = q_meta.cu_seqlens,
+    context_batch_size = B) before the attention runs.
+    """
+    return _compressed_impl(
+        q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
+        block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn,
+    )[0]
+
+
+def _compressed_impl(
+    q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
+    block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, run=True,
+):
+    """Body of :func:`flash_attn_mlm_compressed`; returns (out, prepared launch or None)."""
+    b, h, n, d = validate_qkv_same_shape_rank4(q, k, v, error_prefix="q/k/v")
+    if h != num_heads:
+        raise ValueError("q/k/v head dimension must match num_heads")
+    validate_cache_request(prefill=prefill, inference_cache=inference_cache, layer_id=layer_id)
+    if q_meta.B != b or q_meta.N != n:
+        raise ValueError("q_meta shape metadata does not match q/k/v padded shape")
+    if q_meta.batch_ids_block_n != block_n:
+        raise ValueError("q_meta was built with different block_n")
+    cu_seqlens_q = q_meta.cu_seqlens
+    T = int(q_meta.total_tokens)
+
+    ctx = _maybe_get_cache_context(
+        inference_cache=inference_cache,
+        layer_id=layer_id,
+        batch_size=b,
+        is_mla=is_mla,
+        num_heads=num_heads,
+        head_dim=d,
+        context_batch_size=context_batch_size,
+        dtype=q.dtype,
+        device=q.device,
+        compressed=True,
+    )
+    require_cuda_tensors(q, k, v, ctx.k_cache, ctx.v_cache, ctx.cu_seqlens_kv)
+    if not (q_meta.batch_ids_q.is_cuda and cu_seqlens_q.is_cuda):
+        raise ValueError("batch_ids_q and cu_seqlens_q must be CUDA tensors")
+    if num_heads < 1:
+        raise ValueError("num_heads must be >= 1")
+    validate_packed_cache_shapes(
+        ctx.k_cache,
+        ctx.v_cache,
+        num_heads=num_heads,
+        total_context_len=int(ctx.total_context_len),
+        head_dim=d,
+        is_mla=is_mla,
+    )
+    validate_head_dim_supported(d, is_mla=is_mla)
+    validate_cu_seqlens_rank1_min2(cu_seqlens_q, ctx.cu_seqlens_kv)
+    cbs, c_strides = _packed_context(ctx, num_heads=num_heads, d=d, is_mla=is_mla, b=b, prefill=prefill)
+    num_q_tiles = int(q_meta.q_tile_starts_q.numel())
+    if q_meta.batch_ids_q.ndim != 1 or q_meta.batch_ids_q.numel() != num_q_tiles:
+        raise ValueError("batch_ids_q must be rank-1 with exactly one entry per query tile")
+    if q_meta.q_tile_starts_q.ndim != 1:
+        raise ValueError("q_tile_starts_q must be rank-1")
+    _check_cache_dtype(ctx.k_cache, q)
+
+    if prefill and inference_cache is not None:
+        # packed, zero-padded K/V written straight into the layer's named workspace and
+        # stored (as views) before the launch (host.py:326-364)
+        pad_block_m = _AUTOTUNE_MAX_BLOCK_M if auto_tune_tiles else block_m
+        T_pad = _compute_total_q_len_padded(T, q_meta.host_cu_seqlens(), pad_block_m, block_n)
+        key = str(layer_id)
+        kv_heads = 1 if is_mla else num_heads
+        packing = inference_cache.packing
+        k_entry = packing.get_2d(f"layer:{key}:k_cache", kv_heads * T_pad, d, dtype=k.dtype, device=k.device)
+        if is_mla:
+            v_entry = k_entry
+            sources, outs = [(k[:, :1], 1)], [k_entry]
+        else:
+            v_entry = packing.get_2d(f"layer:{key}:v_cache", kv_heads * T_pad, d, dtype=v.dtype, device=v.device)
+            sources, outs = [(k, num_heads), (v, num_heads)], [k_entry, v_entry]
+        if T_pad > 0:
+            _pack_rows(
+                sources,
+                outs,
+                cu_seqlens=cu_seqlens_q.to(torch.int32).contiguous(),
+                B=b,
+                N=n,
+                D=d,
+                total=T,
+                total_padded=T_pad,
+            )
+        inference_cache.prefill_kv_cache(
+            layer_id,
+            k_cache=k_entry,
+            v_cache=None if is_mla else v_entry,
+            total_context_len=int(T_pad),
+            cu_seqlens_kv=cu_seqlens_q,
+            context_batch_size=int(b),
+            is_mla=is_mla,
+            num_heads=num_heads,
+            head_dim=d,
+        )
+
+    out = torch.empty((num_heads * T, d), dtype=q.dtype, device=q.device)
+    if T == 0 or num_heads == 0:
+        return out, None
+    q_, k_, v_ = _rows(q), _rows(k), _rows(v)
+    k_cache, v_cache = make_contiguous(ctx.k_cache, ctx.v_cache)
+    cu_q = cu_seqlens_q.to(torch.int32).contiguous()
+    cu_kv = ctx.cu_seqlens_kv.to(torch.int32).contiguous()
+    if is_mla:
+        k_strides = (k_.stride(0), 0, k_.stride(2))  # every head reads head 0
+        v_strides = k_strides
+    else:
+        k_strides = (k_.stride(0), k_.stride(1), k_.stride(2))
+        v_strides = (v_.stride(0), v_.stride(1), v_.stride(2))
+    flags = (
+        (_lib.FLAG_MLA if is_mla else 0)
+        | (_lib.FLAG_PREFILL if prefill else 0)
+        | (_lib.FLAG_CAUSAL_SEQ if causal_query_seq_attn else 0)
+    )
+    plan = _launch(
+        run=run,
+        q=q_,
+        out=out,
+        k=k_,
+        v=None if is_mla else v_,
+        B=b,
+        H=num_heads,
+        D=d,
+        N=n,
+        total_q=T,
+        cu_seqlens_q=cu_q,
+        q_strides=(q_.stride(0), q_.stride(1), q_.stride(2)),
+        q_layout=_lib.LAYOUT_PADDED,
+        o_strides=(0, T * d, d),
+        o_layout=_lib.LAYOUT_PACKED,
+        k_strides=k_strides,
+        v_strides=v_strides,
+        kv_layout=_lib.LAYOUT_PADDED,
+        k_ctx=k_cache,
+        v_ctx=None if is_mla else v_cache,
+        c_strides=c_strides,
+        cu_seqlens_kv=cu_kv,
+        ctx_len=0,
+        ctx_batch=cbs,
+        ctx_rows=int(ctx.total_context_len),
+        scale=scale,
+        flags=flags,
+        inference_cache=inference_cache,
+        schedule_cache=q_meta.kernel_schedules if isinstance(q_meta, PackMetadata) else None,
+    )
+    return out, plan
+
+
+def flash_attn_mlm_precompressed(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    num_heads: int,
+    total_q_len: int,
+    cu_seqlens_q: torch.Tensor,
+    batch_ids_q: torch.Tensor,
+    q_tile_starts_q: torch.Tensor,
+    scale: float,
+    inference_cache: InferenceCache | None = None,
+    layer_id: int | str | None = None,
+    is_mla: bool = False,
+    context_batch_size: int | None = None,
+    block_m: int = 64,
+    block_n: int = 32,
+    auto_tune_tiles: bool = False,
+    prefill: bool = False,
+    causal_query_seq_attn: bool = False,
+) -> torch.Tensor:
+    """Like :func:`flash_attn_mlm_compressed` for already packed inputs.
+
+    q [H*total_q_len, D]; k, v [total_q_len, D] (MLA) or [H*total_q_len, D], head-major
+    with sequence b at rows cu_seqlens_q[b]..cu_seqlens_q[b+1] of each head.  Returns
+    [H*total_q_len, D]; rows of padding tokens are left unwritten.  The kernel schedules
+    its own tiles from ``cu_seqlens_q``; ``batch_ids_q`` / ``q_tile_starts_q`` are
+    validated as in the reference.  ``prefill=True`` stores k / v (views) as the
+    layer's context after the launch.
+    """
+    validate_cache_request(prefill=prefill, inference_cache=inference_cache, layer_id=layer_id)
+    if q.ndim != 2 or k.ndim != 2 or v.ndim != 2:
+        raise ValueError("q/k/v must be pre-packed rank-2 tensors")
+    d = int(q.shape[1])
+    if k.shape[1] != d or v.shape[1] != d:
+        raise ValueError("q/k/v head_dim (dim 1) must match")
+    if q.shape[0] != num_heads * total_q_len:
+        raise ValueError("q first dim must equal num_heads * total_q_len")
+    kv_rows = total_q_len if is_mla else num_heads * total_q_len
+    if k.shape[0] != kv_rows or v.shape[0] != kv_rows:
+        raise ValueError(f"k/v first dim mismatch: expected {kv_rows} rows for is_mla={is_mla}")
+    b = int(cu_seqlens_q.numel()) - 1
+    ctx = _maybe_get_cache_context(
+        inference_cache=inference_cache,
+        layer_id=layer_id,
+        batch_size=b,
+        is_mla=is_mla,
+        num_heads=num_heads,
+        head_dim=d,
+        context_batch_size=context_batch_size,
+        dtype=q.dtype,
+        device=q.device,
+        compressed=True,
+    )
+    require_cuda_tensors(q, k, v, ctx.k_cache, ctx.v_cache, ctx.cu_seqlens_kv)
+    validate_packed_cache_shapes(
+        ctx.k_cache,
+        ctx.v_cache,
+        num_heads=num_heads,
+        total_context_len=int(ctx.total_context_len),
+        head_dim=d,
+        is_mla=is_mla,
+    )
+    validate_head_dim_supported(d, is_mla=is_mla)
+    validate_cu_seqlens_rank1_min2(cu_seqlens_q, ctx.cu_seqlens_kv)
+    cbs, c_strides = _packed_context(ctx, num_heads=num_heads, d=d, is_mla=is_mla, b=b, prefill=prefill)
+    num_q_tiles = int(q_tile_starts_q.numel())
+    if batch_ids_q.ndim != 1 or batch_ids_q.numel() != num_q_tiles:
+        raise ValueError("batch_ids_q must be rank-1 with exactly one entry per query tile")
+    if q_tile_starts_q.ndim != 1:
+        raise ValueError("q_tile_starts_q must be rank-1")
+    require_cuda_tensors(cu_seqlens_q, message="cu_seqlens_q must be a CUDA tensor")
+    _check_cache_dtype(ctx.k_cache, q)
+
+    q_, k_, v_ = make_contiguous(q, k, v)
+    k_cache, v_cache = make_contiguous(ctx.k_cache, ctx.v_cache)
+    out = torch.empty_like(q_)
+    if num_heads > 0 and total_q_len > 0 and b > 0:
+        kv_sh = 0 if is_mla else total_q_len * d
+        _launch(
+            q=q_,
+            out=out,
+            k=k_,
+            v=None if is_mla else v_,
+            B=b,
+            H=num_heads,
+            D=d,
+            N=0,
+            total_q=int(total_q_len),
+            cu_seqlens_q=cu_seqlens_q.to(torch.int32).contiguous(),
+            q_strides=(0, total_q_len * d, d),
+            q_layout=_lib.LAYOUT_PACKED,
+            o_strides=(0, total_q_len * d, d),
+            o_layout=_lib.LAYOUT_PACKED,
+            k_strides=(0, kv_sh, d),
+            v_strides=(0, kv_sh, d),
+            kv_layout=_lib.LAYOUT_PACKED,
+            k_ctx=k_cache,
+            v_ctx=None if is_mla else v_cache,
+            c_strides=c_strides,
+            cu_seqlens_kv=ctx.cu_seqlens_kv.to(torch.int32).contiguous(),
+            ctx_len=0,
+            ctx_batch=cbs,
+            ctx_rows=int(ctx.total_context_len),
+            scale=scale,
+            flags=(_lib.FLAG_MLA if is_mla else 0)
+            | (_lib.FLAG_PREFILL if prefill else 0)
+            | (_lib.FLAG_CAUSAL_SEQ if causal_query_seq_attn else 0),
+            inference_cache=inference_cache,
+        )
+
+    if prefill and inference_cache is not None:
+        inference_cache.prefill_kv_cache(
+            layer_id,
+            k_cache=k,
+            v_cache=None if is_mla else v,
+            total_context_len=int(total_q_len),
+            cu_seqlens_kv=cu_seqlens_q,
+            context_batch_size=b,
+            is_mla=is_mla,
+            num_heads=num_heads,
+            head_dim=d,
+        )
+    return out

@@ -1,0 +1,138 @@
+"""Numpy restatement of the reference's MLM attention -- test infrastructure only.
+
+The reference computes, per query tile, an online softmax over [cached context ||
+main keys] (src/flash_mlm/mlm_kernel_impl.py:10-62); mathematically that is plain
+softmax attention over the concatenated key set, which is what these functions
+compute, in float64, one (sequence, head) at a time.  Which keys a query sees and
+where they live follows the device bodies:
+  packed  _mlm_compressed_kernel_impl  mlm_kernel_impl.py:219-390
+  dense   _mlm_main_kernel_impl        mlm_kernel_impl.py:65-216
+and the reference's own test oracles (src/flash_mlm/host/test_host.py:30-145).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def attend(q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float) -> np.ndarray:
+    """softmax(scale * q K^T) V for q [L, D], K/V [M, D] (M >= 1), in float64."""
+    q = q.astype(np.float64)
+    K = K.astype(np.float64)
+    V = V.astype(np.float64)
+    s = (q @ K.T) * float(scale)
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=1, keepdims=True)
+    return p @ V
+
+
+def packed_key_rows(b: int, lengths, causal_query_seq_attn: bool) -> list[tuple[int, int]]:
+    """(sequence, position) of the main keys of sequence b in packed order:
+    sequence b's own tokens, or with causal_query_seq_attn all tokens of sequences
+    0..b (mlm_kernel_impl.py:288-293)."""
+    seqs = range(b + 1) if causal_query_seq_attn else (b,)
+    return [(s, p) for s in seqs for p in range(int(lengths[s]))]
+
+
+def mlm_attention_packed(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    lengths,
+    scale: float,
+    *,
+    is_mla: bool = False,
+    causal_query_seq_attn: bool = False,
+    prefill: bool = False,
+    k_cache: np.ndarray | None = None,
+    v_cache: np.ndarray | None = None,
+    cu_seqlens_kv=None,
+    total_context_len: int = 0,
+    context_batch_size: int = 1,
+) -> np.ndarray:
+    """Packed-path attention on padded q/k/v [B, H, N, D] -> [B, H, N, D] (float64),
+    zeros at padding positions.
+
+    Context of sequence b (skipped when ``prefill``): rows
+    ``h_off + cu_seqlens_kv[cb] .. h_off + cu_seqlens_kv[cb+1]`` of the head-major cache,
+    ``cb = b`` if context_batch_size > 1 else 0, ``h_off = h * total_context_len``
+    (0 for MLA).  MLA: main K = V = head 0 of k, context V = context K.
+    """
+    B, H, N, D = q.shape
+    out = np.zeros((B, H, N, D), dtype=np.float64)
+    cu_kv = None if cu_seqlens_kv is None else np.asarray(cu_seqlens_kv, dtype=np.int64)
+    for b in range(B):
+        Lq = int(lengths[b])
+        if Lq == 0:
+            continue
+        rows = packed_key_rows(b, lengths, causal_query_seq_attn)
+        sb = np.array([r[0] for r in rows])
+        pb = np.array([r[1] for r in rows])
+        c0 = c1 = 0
+        if not prefill and cu_kv is not None:
+            cb = b if context_batch_size > 1 else 0
+            c0, c1 = int(cu_kv[cb]), int(cu_kv[cb + 1])
+        for h in range(H):
+            kh = 0 if is_mla else h
+            K_main = k[sb, kh, pb]
+            V_main = K_main if is_mla else v[sb, h, pb]
+            if c1 > c0:
+                off = 0 if is_mla else h * total_context_len
+                K_ctx = k_cache[off + c0 : off + c1]
+                V_ctx = K_ctx if is_mla else v_cache[off + c0 : off + c1]
+                K_all = np.concatenate([K_ctx, K_main])
+                V_all = np.concatenate([V_ctx, V_main])
+            else:
+                K_all, V_all = K_main, V_main
+            out[b, h, :Lq] = attend(q[b, h, :Lq], K_all, V_all, scale)
+    return out
+
+
+def mlm_attention_dense(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    scale: float,
+    *,
+    is_mla: bool = False,
+    prefill: bool = False,
+    k_cache: np.ndarray | None = None,
+    v_cache: np.ndarray | None = None,
+    context_len: int = 0,
+    context_batch_size: int = 1,
+) -> np.ndarray:
+    """Dense-path attention q/k/v [B, H, N, D] -> [B, H, N, D] (float64).
+
+    Every query of (b, h) attends to [context || k[b, h, :N]].  Context rows (skipped
+    when ``prefill``): MLA ``cb*context_len + [0, context_len)``; otherwise
+    ``(cb*H + h)*context_len + [0, context_len)``, cb = b if context_batch_size > 1
+    else 0 (mlm_kernel_impl.py:132-141).  MLA keeps per-head main keys and V = K.
+    """
+    B, H, N, D = q.shape
+    out = np.zeros((B, H, N, D), dtype=np.float64)
+    for b in range(B):
+        cb = b if context_batch_size > 1 else 0
+        for h in range(H):
+            K_main = k[b, h]
+            V_main = K_main if is_mla else v[b, h]
+            if not prefill and context_len > 0:
+                start = cb * context_len if is_mla else (cb * H + h) * context_len
+                K_ctx = k_cache[start : start + context_len]
+                V_ctx = K_ctx if is_mla else v_cache[start : start + context_len]
+                K_all = np.concatenate([K_ctx, K_main])
+                V_all = np.concatenate([V_ctx, V_main])
+            else:
+                K_all, V_all = K_main, V_main
+            out[b, h] = attend(q[b, h], K_all, V_all, scale)
+    return out
+
+
+def effective_flops(lengths_q, lengths_ctx, num_heads: int, head_dim: int, *, causal_query_seq_attn=False, prefill=False) -> float:
+    """4 * H * D * sum_b Lq_b * (Lctx_b + Lmain_b), padding excluded; Lmain_b = Lq_b, or
+    cu_q[b+1] with causal_query_seq_attn; Lctx_b = 0 with prefill
+    (src/benchmark/common.py:39-57 counts Lmain_b = Lq_b)."""
+    lq = np.asarray(lengths_q, dtype=np.float64)
+    lc = np.zeros_like(lq) if prefill else np.broadcast_to(np.asarray(lengths_ctx, dtype=np.float64), lq.shape)
+    lm = np.cumsum(lq) if causal_query_seq_attn else lq
+    return float(4.0 * num_heads * head_dim * np.sum(lq * (lc + lm)))

@@ -1,0 +1,96 @@
+"""CPU baseline: the reference benchmark's per-sequence PyTorch SDPA attention path
+(src/benchmark/standard_kernel/utils.py:410-461 packed, :464-517 dense), restated and
+timed on the host's CPU cores in fp32 -- a reported baseline, not a checker, and test /
+bench infrastructure only.
+
+For every sequence b: K = [context rows of b || main keys of b], one
+torch.nn.functional.scaled_dot_product_attention call over all heads.  Main keys
+follow the kernel semantics (MLA: head 0 of k shared by all heads, V = K;
+causal_query_seq_attn: sequences 0..b).  A bounded prefix of the workload's sequences
+is timed so the run stays within `budget_s` seconds.
+"""
+
+from __future__ import annotations
+
+import time
+
+import torch
+import torch.nn.functional as F
+
+
+def _sequence_inputs(case, b: int):
+    """fp32 CPU tensors (q [H, Lq, D], K [H|1, M, D], V) for sequence b of a bench Case."""
+    t = case.tensors
+    H = case.H
+    Lq = case.lengths_q[b]
+    q = t["q"][b, :, :Lq].float().cpu()
+    seqs = range(b + 1) if case.causal else (b,)
+    if case.cfg in (1, 2):  # dense
+        K_main = t["k"][b].float().cpu()
+        V_main = t["v"][b].float().cpu()
+    elif case.is_mla:
+        K_main = torch.cat([t["k"][s, :1, : case.lengths_q[s]] for s in seqs], dim=1).float().cpu()
+        V_main = K_main
+    else:
+        K_main = torch.cat([t["k"][s, :, : case.lengths_q[s]] for s in seqs], dim=1).float().cpu()
+        V_main = torch.cat([t["v"][s, :, : case.lengths_q[s]] for s in seqs], dim=1).float().cpu()
+    if case.prefill:
+        return q, K_main, V_main
+    if case.cfg == 2:
+        C = case.config["context"]
+        kc = t["k0"][0].float().cpu()
+        vc = t["v0"][0].float().cpu()
+    elif case.cfg == 1:
+        return q, K_main, V_main
+    else:
+        cb = b if t["cbs"] > 1 else 0
+        cu = t["cu_kv"]
+        c0, c1 = int(cu[cb]), int(cu[cb + 1])
+        Tc = t["Tc"]
+        if case.is_mla:
+            kc = t["k_cache"][c0:c1].float().cpu()[None]
+            vc = kc
+        else:
+            kc = t["k_cache"].view(H, Tc, -1)[:, c0:c1].float().cpu()
+            vc = t["v_cache"].view(H, Tc, -1)[:, c0:c1].float().cpu()
+    K = torch.cat([kc, K_main], dim=1)
+    V = K if case.is_mla else torch.cat([vc, V_main], dim=1)
+    return q, K, V
+
+
+def _flops(case, b: int) -> float:
+    lq = case.lengths_q[b]
+    main = sum(case.lengths_q[: b + 1]) if case.causal else lq
+    ctx = 0 if case.prefill else case.lengths_ctx[b]
+    return 4.0 * case.H * case.D * lq * (ctx + main)
+
+
+def time_case(case, budget_s: float = 20.0) -> dict:
+    scale = case.tensors["scale"]
+    n_seq = len(case.lengths_q)
+    # warm-up on the first sequence
+    q, K, V = _sequence_inputs(case, 0)
+    F.scaled_dot_product_attention(q[None], K.expand(q.shape[0], -1, -1)[None], V.expand(q.shape[0], -1, -1)[None], scale=scale)
+    elapsed, flops, done = 0.0, 0.0, 0
+    for b in range(n_seq):
+        q, K, V = _sequence_inputs(case, b)
+        Kx = K.expand(q.shape[0], -1, -1)
+        Vx = V.expand(q.shape[0], -1, -1)
+        t0 = time.perf_counter()
+        F.scaled_dot_product_attention(q[None], Kx[None], Vx[None], scale=scale)
+        elapsed += time.perf_counter() - t0
+        flops += _flops(case, b)
+        done += 1
+        if elapsed > budget_s:
+            break
+    total = sum(_flops(case, b) for b in range(n_seq))
+    return {
+        "value": round(flops / elapsed / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"first {done} of {n_seq} sequences, all {case.H} heads, fp32 per-sequence "
+        f"torch SDPA (reference benchmark path); {flops / 1e9:.2f} of {total / 1e9:.2f} GFLOP, "
+        f"{elapsed:.2f} s",
+        "ms_per_step_extrapolated": round(elapsed / flops * total * 1e3, 3),
+    }

@@ -1,0 +1,60 @@
+"""The C ABI library (libflash_mlm_hip.so) loads on the host and exports exactly what
+include/flash_mlm_hip.h declares, with matching struct layouts (CPU only: no kernel
+launches; only argument-rejection paths that return before any HIP call)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import REPO
+from flash_mlm import _lib
+
+HEADER = REPO / "include" / "flash_mlm_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"FMLM_API\s+[\w\s\*]+?\b(fmlm_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert {"fmlm_pack_metadata", "fmlm_pack", "fmlm_unpack", "fmlm_attn_fwd", "fmlm_tile_map"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} missing from the ctypes binding"
+    assert set(_lib.SIGNATURES) == set(_declared())
+
+
+def test_struct_layouts_match():
+    lib = _lib.load()
+    assert lib.fmlm_abi_version() == _lib.ABI_VERSION
+    assert lib.fmlm_attn_params_size() == ctypes.sizeof(_lib.AttnParams)
+    assert lib.fmlm_pack_tensor_size() == ctypes.sizeof(_lib.PackTensor)
+
+
+def test_argument_rejection_without_launch():
+    lib = _lib.load()
+    # invalid arguments return negative codes before any HIP call
+    assert lib.fmlm_pack(None, 0, 2, 1, 1, 16, None, 1, 1, None) == -1
+    assert lib.fmlm_pack(None, 1, 3, 1, 1, 16, None, 1, 1, None) == -2  # bad element size
+    assert lib.fmlm_unpack(2, None, 0, None, 1, 1, 1, 16, None, None) == -1
+    assert lib.fmlm_pack_metadata(None, 0, 1, 4, 0, None, None, None, None, None, None) == -1
+    assert lib.fmlm_tile_map(None, 1, 4, 0, None, None, None, None) == -1
+    assert lib.fmlm_attn_fwd(None, None) == -1
+    p = _lib.AttnParams()
+    p.dtype, p.B, p.H, p.D, p.N = _lib.DTYPE_BF16, 1, 1, 48, 4
+    assert lib.fmlm_attn_workspace_bytes(p) == -3  # unsupported head dim
+    p.D = 64
+    assert lib.fmlm_attn_workspace_bytes(p) == 0  # dense: no schedule workspace
+    p.dtype = 7
+    assert lib.fmlm_attn_workspace_bytes(p) == -2
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.check(-1, "x")

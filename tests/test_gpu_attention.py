@@ -1,0 +1,448 @@
+"""GPU parity of the HIP attention path against the numpy oracle (fp64 math on the
+same bf16/fp16/fp32 inputs).  Tolerance: max-abs 1e-2 and rtol 1e-2 per element
+(assert_allclose(out, ref, atol=1e-2, rtol=1e-2)).
+
+The first group ports the reference's own integration tests
+(src/flash_mlm/host/test_host.py, same seeds, shapes and API calls, checked here
+against the oracle instead of torch fp16 math); the rest widens coverage (head dims,
+dtypes, context sharing, prefill round trips, odd shapes) and runs the BASELINE
+configs at full size with per-(sequence, head) oracle checks plus size-independent
+properties."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flash_mlm import (
+    InferenceCache,
+    build_pack_metadata,
+    flash_attn_mlm,
+    flash_attn_mlm_compressed,
+    flash_attn_mlm_precompressed,
+    unpack_from_kernel,
+)
+from flash_mlm.host.host_utils import pack_for_kernel
+from oracle import attention_ref as ar
+from oracle import pack_ref
+
+pytestmark = pytest.mark.gpu
+ATOL = RTOL = 1e-2
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _close(out, ref, atol=ATOL, rtol=RTOL):
+    np.testing.assert_allclose(_np(out) if isinstance(out, torch.Tensor) else out, ref, atol=atol, rtol=rtol)
+
+
+def _randn(shape, device, dtype=torch.float16, std=1.0):
+    return (torch.randn(shape, device=device) * std).to(dtype)
+
+
+def _packed_oracle(q, k, v, lengths, scale, *, is_mla=False, causal=False, prefill=False, k_cache=None, v_cache=None, cu_kv=None, cbs=1, Tc=0):
+    return ar.mlm_attention_packed(
+        _np(q), _np(k), _np(v), [int(x) for x in lengths], scale, is_mla=is_mla,
+        causal_query_seq_attn=causal, prefill=prefill,
+        k_cache=None if k_cache is None else _np(k_cache),
+        v_cache=None if v_cache is None else _np(v_cache),
+        cu_seqlens_kv=None if cu_kv is None else [int(x) for x in cu_kv],
+        total_context_len=Tc, context_batch_size=cbs,
+    )
+
+
+# ---------------------------------------------------------------------------
+# reference integration tests (test_host.py), ported
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_dense_prefill_requires_cache(is_mla, device):
+    torch.manual_seed(21)
+    q = _randn((2, 2, 16, 64), device)
+    with pytest.raises(ValueError, match="prefill=True requires inference_cache"):
+        flash_attn_mlm(q, q, q, scale=0.5, inference_cache=None, layer_id=None, is_mla=is_mla, block_m=32, block_n=32, prefill=True)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_dense_no_cache_matches_reference(is_mla, device):
+    torch.manual_seed(22)
+    B, H, N, D, scale = 2, 3, 24, 64, 0.6
+    q, k = _randn((B, H, N, D), device), _randn((B, H, N, D), device)
+    v = k if is_mla else _randn((B, H, N, D), device)
+    out = flash_attn_mlm(q, k, v, scale=scale, is_mla=is_mla, block_m=32, block_n=32)
+    _close(out, ar.mlm_attention_dense(_np(q), _np(k), _np(v), scale, is_mla=is_mla))
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_dense_prefill_then_use_cached_context_matches_reference(is_mla, device):
+    torch.manual_seed(23)
+    B, H, N, D, scale = 2, 2, 20, 64, 0.55
+    q1, k1 = _randn((B, H, N, D), device), _randn((B, H, N, D), device)
+    v1 = k1 if is_mla else _randn((B, H, N, D), device)
+    q2, k2 = _randn((B, H, N, D), device), _randn((B, H, N, D), device)
+    v2 = k2 if is_mla else _randn((B, H, N, D), device)
+    cache = InferenceCache()
+    out1 = flash_attn_mlm(q1, k1, v1, scale=scale, inference_cache=cache, layer_id=3, is_mla=is_mla, block_m=32, block_n=32, prefill=True)
+    _close(out1, ar.mlm_attention_dense(_np(q1), _np(k1), _np(v1), scale, is_mla=is_mla))
+    out = flash_attn_mlm(q2, k2, v2, scale=scale, inference_cache=cache, layer_id=3, is_mla=is_mla, context_batch_size=B, block_m=32, block_n=32)
+    entry = cache.get_kv_cache(3, is_mla=is_mla, num_heads=H, head_dim=D, dtype=q2.dtype, device=q2.device)
+    # the stored entry is this call's K/V (MLA: head 0 of k), bit-exact
+    if is_mla:
+        assert torch.equal(entry.k_cache, k1[:, 0].reshape(B * N, D)) and entry.v_cache is None
+    else:
+        assert torch.equal(entry.k_cache, k1.reshape(B * H * N, D)) and torch.equal(entry.v_cache, v1.reshape(B * H * N, D))
+    ctx_len = entry.total_context_len // entry.context_batch_size
+    ref = ar.mlm_attention_dense(
+        _np(q2), _np(k2), _np(v2), scale, is_mla=is_mla, k_cache=_np(entry.k_cache),
+        v_cache=None if is_mla else _np(entry.v_cache), context_len=ctx_len, context_batch_size=entry.context_batch_size,
+    )
+    _close(out, ref)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_compressed_prefill_requires_cache(is_mla, device):
+    torch.manual_seed(11)
+    q = _randn((2, 2, 16, 64), device)
+    meta = build_pack_metadata(torch.tensor([16, 9], device=device, dtype=torch.int32), 16, block_n=32)
+    with pytest.raises(ValueError, match="prefill=True requires inference_cache"):
+        flash_attn_mlm_compressed(q, q, q, num_heads=2, scale=0.5, q_meta=meta, is_mla=is_mla, block_m=32, block_n=32, prefill=True)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_compressed_no_prefill_empty_context_same_with_or_without_cache(is_mla, device):
+    torch.manual_seed(12)
+    B, H, N, D, scale = 2, 3, 24, 64, 0.6
+    lengths = torch.tensor([24, 15], device=device, dtype=torch.int32)
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    out_no = flash_attn_mlm_compressed(q, k, v, num_heads=H, scale=scale, q_meta=meta, is_mla=is_mla, block_m=32, block_n=32)
+    out_with = flash_attn_mlm_compressed(
+        q, k, v, num_heads=H, scale=scale, q_meta=meta, inference_cache=InferenceCache(), layer_id=0, is_mla=is_mla, block_m=32, block_n=32
+    )
+    assert torch.equal(out_no, out_with)
+    ref = _packed_oracle(q, k, v, lengths.tolist(), scale, is_mla=is_mla)
+    _close(unpack_from_kernel(out_no, meta, H=H), ref)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_compressed_prefill_with_cache_stores_entry(is_mla, device):
+    torch.manual_seed(13)
+    B, H, N, D = 2, 2, 20, 64
+    lengths = torch.tensor([20, 7], device=device, dtype=torch.int32)
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    cache = InferenceCache()
+    out = flash_attn_mlm_compressed(q, k, v, num_heads=H, scale=0.55, q_meta=meta, inference_cache=cache, layer_id=7, is_mla=is_mla, block_m=32, block_n=32, prefill=True)
+    stored = cache.get_kv_cache(7, is_mla=is_mla, num_heads=H, head_dim=D, dtype=q.dtype, device=q.device)
+    assert int(stored.cu_seqlens_kv[-1]) == 27
+    assert stored.total_context_len >= 27
+    assert stored.k_cache.shape[0] == (1 if is_mla else H) * stored.total_context_len
+    assert stored.context_batch_size == B
+    # exact layout: padded T_pad (host_utils.py:292-312) and zero tails, bit-exact
+    ref_meta = pack_ref.pack_metadata(np.array([20, 7]), N, 32)
+    T_pad = pack_ref.total_q_len_padded(27, ref_meta.cu_seqlens, 32, 32)
+    assert stored.total_context_len == T_pad
+    np.testing.assert_array_equal(_np(stored.k_cache), pack_ref.pack(_np(k[:, :1] if is_mla else k), ref_meta, T_pad))
+    if not is_mla:
+        np.testing.assert_array_equal(_np(stored.v_cache), pack_ref.pack(_np(v), ref_meta, T_pad))
+    # prefill skips the (absent) context; output is plain per-sequence attention
+    _close(unpack_from_kernel(out, meta, H), _packed_oracle(q, k, v, [20, 7], 0.55, is_mla=is_mla, prefill=True))
+
+
+def _empty_context_cache(B, H, D, is_mla, device):
+    k_cache = torch.empty((0, D), device=device, dtype=torch.float16)
+    cache = InferenceCache()
+    cache.prefill_kv_cache(
+        layer_id=0, k_cache=k_cache, v_cache=torch.empty_like(k_cache), total_context_len=0,
+        cu_seqlens_kv=torch.zeros(B + 1, device=device, dtype=torch.int32), context_batch_size=B,
+        is_mla=is_mla, num_heads=H, head_dim=D,
+    )
+    return cache
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_compressed_matches_reference(is_mla, device):
+    torch.manual_seed(0)
+    B, H, N, D, scale = 2, 3, 48, 64, 0.7
+    lengths = torch.tensor([48, 37], device=device, dtype=torch.int32)
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    out = flash_attn_mlm_compressed(q, k, v, num_heads=H, scale=scale, q_meta=meta, inference_cache=_empty_context_cache(B, H, D, is_mla, device), layer_id=0, is_mla=is_mla, block_m=32, block_n=32)
+    _close(unpack_from_kernel(out, meta, H=H), _packed_oracle(q, k, v, [48, 37], scale, is_mla=is_mla))
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_compressed_prev_subseq_attention_matches_reference(is_mla, device):
+    torch.manual_seed(2)
+    B, H, N, D, scale = 3, 2, 32, 64, 0.65
+    lengths = torch.tensor([9, 7, 5], device=device, dtype=torch.int32)
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    out = flash_attn_mlm_compressed(
+        q, k, v, num_heads=H, scale=scale, q_meta=meta, inference_cache=_empty_context_cache(B, H, D, is_mla, device),
+        layer_id=0, is_mla=is_mla, block_m=32, block_n=32, causal_query_seq_attn=True,
+    )
+    _close(unpack_from_kernel(out, meta, H=H), _packed_oracle(q, k, v, [9, 7, 5], scale, is_mla=is_mla, causal=True))
+
+
+def _context_cache(B, H, D, is_mla, ctx_lengths, device, dtype=torch.float16, cbs=None, std=1.0):
+    cu_kv = torch.zeros(len(ctx_lengths) + 1, dtype=torch.int32)
+    cu_kv[1:] = torch.cumsum(torch.tensor(ctx_lengths), 0)
+    Tc = int(cu_kv[-1])
+    k_cache = _randn(((1 if is_mla else H) * Tc, D), device, dtype, std)
+    v_cache = _randn(((1 if is_mla else H) * Tc, D), device, dtype, std)
+    cache = InferenceCache()
+    cache.prefill_kv_cache(
+        layer_id=0, k_cache=k_cache, v_cache=v_cache, total_context_len=Tc, cu_seqlens_kv=cu_kv.to(device),
+        context_batch_size=len(ctx_lengths) if cbs is None else cbs, is_mla=is_mla, num_heads=H, head_dim=D,
+    )
+    return cache, k_cache, v_cache, cu_kv, Tc
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_compressed_matches_reference_with_cache(is_mla, device):
+    torch.manual_seed(1)
+    B, H, N, D, scale = 2, 3, 48, 64, 0.5
+    lengths = torch.tensor([48, 37], device=device, dtype=torch.int32)
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, is_mla, [13, 9], device)
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    out = flash_attn_mlm_compressed(q, k, v, num_heads=H, scale=scale, q_meta=meta, inference_cache=cache, layer_id=0, is_mla=is_mla, block_m=32, block_n=32)
+    ref = _packed_oracle(q, k, v, [48, 37], scale, is_mla=is_mla, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=B, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H=H), ref)
+
+
+def _prepack(q, k, v, meta, is_mla):
+    q_p = pack_for_kernel(q, meta, flatten_for_kernel=True)
+    if is_mla:
+        k_p = pack_for_kernel(k[:, :1], meta, flatten_for_kernel=False).squeeze(0)
+        return q_p, k_p, k_p
+    return q_p, pack_for_kernel(k, meta, flatten_for_kernel=True), pack_for_kernel(v, meta, flatten_for_kernel=True)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+@pytest.mark.parametrize("with_cache", [False, True])
+@pytest.mark.parametrize("causal", [False, True])
+def test_precompressed_matches_compressed(is_mla, with_cache, causal, device):
+    torch.manual_seed(51 if with_cache else 50)
+    B, H, N, D, scale = 2, 3, 48, 64, 0.5
+    lengths = torch.tensor([48, 37], device=device, dtype=torch.int32)
+    q, k = _randn((B, H, N, D), device), _randn((B, H, N, D), device)
+    v = k if is_mla else _randn((B, H, N, D), device)
+    if with_cache:
+        make = lambda: _context_cache(B, H, D, is_mla, [13, 9], device)[0]  # noqa: E731
+        torch.manual_seed(5)
+        c1 = make()
+        torch.manual_seed(5)
+        c2 = make()
+    else:
+        c1, c2 = (_empty_context_cache(B, H, D, is_mla, device) for _ in range(2))
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    ref_out = flash_attn_mlm_compressed(q, k, v, num_heads=H, scale=scale, q_meta=meta, inference_cache=c1, layer_id=0, is_mla=is_mla, block_m=32, block_n=32, causal_query_seq_attn=causal)
+    q_p, k_p, v_p = _prepack(q, k, v, meta, is_mla)
+    pre = flash_attn_mlm_precompressed(
+        q_p, k_p, v_p, num_heads=H, total_q_len=q_p.shape[0] // H, cu_seqlens_q=meta.cu_seqlens,
+        batch_ids_q=meta.batch_ids_q, q_tile_starts_q=meta.q_tile_starts_q, scale=scale, inference_cache=c2,
+        layer_id=0, is_mla=is_mla, block_m=32, block_n=32, causal_query_seq_attn=causal,
+    )
+    torch.testing.assert_close(pre, ref_out, atol=1e-5, rtol=0)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_precompressed_prefill_stores_cache_entry(is_mla, device):
+    torch.manual_seed(52)
+    B, H, N, D = 2, 2, 20, 64
+    lengths = torch.tensor([20, 7], device=device, dtype=torch.int32)
+    q, k = _randn((B, H, N, D), device), _randn((B, H, N, D), device)
+    v = k if is_mla else _randn((B, H, N, D), device)
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    q_p, k_p, v_p = _prepack(q, k, v, meta, is_mla)
+    cache = InferenceCache()
+    out = flash_attn_mlm_precompressed(
+        q_p, k_p, v_p, num_heads=H, total_q_len=q_p.shape[0] // H, cu_seqlens_q=meta.cu_seqlens,
+        batch_ids_q=meta.batch_ids_q, q_tile_starts_q=meta.q_tile_starts_q, scale=0.55, inference_cache=cache,
+        layer_id=7, is_mla=is_mla, block_m=32, block_n=32, prefill=True,
+    )
+    stored = cache.get_kv_cache(7, is_mla=is_mla, num_heads=H, head_dim=D, dtype=q.dtype, device=q.device)
+    assert int(stored.cu_seqlens_kv[-1]) == 27 and stored.total_context_len >= 27
+    assert stored.k_cache.shape[0] == (1 if is_mla else H) * stored.total_context_len
+    assert stored.context_batch_size == B and stored.k_cache is k_p
+    _close(unpack_from_kernel(out, meta, H), _packed_oracle(q, k, v, [20, 7], 0.55, is_mla=is_mla, prefill=True))
+
+
+# ---------------------------------------------------------------------------
+# wider coverage
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("mode", ["ctx", "causal_ctx", "mla_ctx", "mla_causal_prefill"])
+def test_packed_head_dim_dtype_sweep(dtype, D, mode, device):
+    torch.manual_seed(1000 + D)
+    is_mla = mode.startswith("mla")
+    causal = "causal" in mode
+    prefill = "prefill" in mode
+    lengths = [70, 1, 0, 133, 64, 17]
+    B, H, N = len(lengths), 3, 140
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, dtype) for _ in range(3))
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, is_mla, [5, 0, 40, 129, 64, 3], device, dtype)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, is_mla=is_mla, block_n=64, causal_query_seq_attn=causal, prefill=prefill)
+    ref = _packed_oracle(q, k, v, lengths, scale, is_mla=is_mla, causal=causal, prefill=prefill, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=B, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [16, 64, 128, 256])
+@pytest.mark.parametrize("is_mla", [False, True])
+@pytest.mark.parametrize("cbs", [1, 3])
+def test_dense_sweep_with_context(dtype, D, is_mla, cbs, device):
+    torch.manual_seed(2000 + D + cbs)
+    B, H, N, C = 3, 2, 77, 45
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, dtype) for _ in range(3))
+    rows = cbs * C * (1 if is_mla else H)
+    kc, vc = _randn((rows, D), device, dtype), _randn((rows, D), device, dtype)
+    cache = InferenceCache()
+    cache.prefill_kv_cache(0, k_cache=kc, v_cache=None if is_mla else vc, context_batch_size=cbs, is_mla=is_mla, num_heads=H, head_dim=D,
+                           total_context_len=cbs * C)
+    out = flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0, is_mla=is_mla)
+    ref = ar.mlm_attention_dense(_np(q), _np(k), _np(v), scale, is_mla=is_mla, k_cache=_np(kc), v_cache=_np(vc), context_len=C, context_batch_size=cbs)
+    _close(out, ref)
+
+
+def test_shared_context_override_on_multi_batch_entry(device):
+    # context_batch_size=1 on a multi-batch entry -> cu_seqlens_kv = [0, total] (host_utils.py:232-237)
+    torch.manual_seed(31)
+    B, H, N, D = 3, 2, 40, 64
+    lengths = [40, 12, 33]
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, [7, 11, 5], device)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=32)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, 0.3, cache, 0, context_batch_size=1)
+    ref = _packed_oracle(q, k, v, lengths, 0.3, k_cache=kc, v_cache=vc, cu_kv=[0, Tc], cbs=1, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+    with pytest.raises(ValueError, match=r"context_batch_size \(2\) must match cached entry context_batch_size \(3\)"):
+        flash_attn_mlm_compressed(q, k, v, H, meta, 0.3, cache, 0, context_batch_size=2)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_prefill_then_attend_round_trip(is_mla, device):
+    # layer 0: prefill stores padded packed K/V; a second call attends to it as context
+    torch.manual_seed(41)
+    B, H, N, D = 3, 4, 50, 128
+    lengths1, lengths2 = [50, 20, 33], [17, 50, 8]
+    q1, k1, v1 = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    q2, k2, v2 = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    cache = InferenceCache()
+    m1 = cache.packing.get_pack_metadata(torch.tensor(lengths1, device=device), N=N, block_n=16)
+    m2 = cache.packing.get_pack_metadata(torch.tensor(lengths2, device=device), N=N, block_n=16)
+    flash_attn_mlm_compressed(q1, k1, v1, H, m1, 0.2, cache, "L", is_mla=is_mla, block_n=16, prefill=True, auto_tune_tiles=True)
+    entry = cache.get_kv_cache("L", is_mla=is_mla, num_heads=H, head_dim=D, dtype=torch.bfloat16, device=q1.device)
+    out = flash_attn_mlm_compressed(q2, k2, v2, H, m2, 0.2, cache, "L", is_mla=is_mla, block_n=16)
+    ref = _packed_oracle(q2, k2, v2, lengths2, 0.2, is_mla=is_mla, k_cache=entry.k_cache, v_cache=entry.v_cache,
+                         cu_kv=_np(entry.cu_seqlens_kv).astype(int), cbs=B, Tc=entry.total_context_len)
+    _close(unpack_from_kernel(out, m2, H), ref)
+    # the context a sequence sees is exactly its own prefilled tokens
+    ref_alt = ar.mlm_attention_packed(
+        _np(q2), _np(k2), _np(v2), lengths2, 0.2, is_mla=is_mla,
+    )
+    assert not np.allclose(ref, ref_alt, atol=1e-3)
+
+
+def test_non_contiguous_inputs(device):
+    torch.manual_seed(61)
+    B, H, N, D = 2, 4, 33, 64
+    base = _randn((B, N, H, D), device, torch.bfloat16)
+    q = base.permute(0, 2, 1, 3)  # strided [B, H, N, D]
+    k = _randn((B, H, N, D), device, torch.bfloat16)
+    v = _randn((B, H, N, D * 2), device, torch.bfloat16)[..., ::2]  # non-unit D stride
+    lengths = [33, 19]
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, block_n=32)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, 0.125)
+    _close(unpack_from_kernel(out, meta, H), _packed_oracle(q, k, v, lengths, 0.125))
+    dense = flash_attn_mlm(q, k, v, 0.125)
+    _close(dense, ar.mlm_attention_dense(_np(q), _np(k), _np(v), 0.125))
+
+
+def test_deterministic(device):
+    torch.manual_seed(71)
+    B, H, N, D = 4, 8, 300, 128
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor([300, 1, 257, 128], device=device), N, block_n=64)
+    a = flash_attn_mlm_compressed(q, k, v, H, meta, 0.1, causal_query_seq_attn=True, block_n=64)
+    b = flash_attn_mlm_compressed(q, k, v, H, meta, 0.1, causal_query_seq_attn=True, block_n=64)
+    assert torch.equal(a, b)
+
+
+def test_normalisation_and_extreme_logits(device):
+    # V constant -> output exactly that constant (weights sum to one) even with huge logits
+    torch.manual_seed(81)
+    B, H, N, D = 2, 2, 300, 64
+    q = _randn((B, H, N, D), device, torch.bfloat16, std=8.0)
+    k = _randn((B, H, N, D), device, torch.bfloat16, std=8.0)
+    v = torch.full((B, H, N, D), 0.75, device=device, dtype=torch.bfloat16)
+    meta = build_pack_metadata(torch.tensor([300, 299], device=device), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, 1.0, block_n=64)
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float(), torch.full_like(out, 0.75).float(), atol=4e-3, rtol=0)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs at full size
+# ---------------------------------------------------------------------------
+def _check_sampled(case, out_unpacked, pairs, rows=None):
+    t = case.tensors
+    for b, h in pairs:
+        Lq = case.lengths_q[b]
+        sel = np.arange(Lq) if rows is None else np.unique(np.linspace(0, Lq - 1, rows).astype(int))
+        if case.cfg in (1, 2):
+            qn = _np(t["q"][b, h, sel])
+            K = _np(t["k"][b, h])
+            V = K if case.is_mla else _np(t["v"][b, h])
+            if case.cfg == 2:
+                C = case.config["context"]
+                K = np.concatenate([_np(t["k0"][0, h]), K])
+                V = np.concatenate([_np(t["v0"][0, h]), V])
+        else:
+            keys = ar.packed_key_rows(b, case.lengths_q, case.causal)
+            sb = torch.tensor([r[0] for r in keys], device=t["q"].device)
+            pb = torch.tensor([r[1] for r in keys], device=t["q"].device)
+            kh = 0 if case.is_mla else h
+            K = _np(t["k"][sb, kh, pb])
+            V = K if case.is_mla else _np(t["v"][sb, h, pb])
+            if not case.prefill:
+                cb = b if t["cbs"] > 1 else 0
+                c0, c1 = int(t["cu_kv"][cb]), int(t["cu_kv"][cb + 1])
+                off = 0 if case.is_mla else h * t["Tc"]
+                Kc = _np(t["k_cache"][off + c0 : off + c1])
+                Vc = Kc if case.is_mla else _np(t["v_cache"][off + c0 : off + c1])
+                K, V = np.concatenate([Kc, K]), np.concatenate([Vc, V])
+            qn = _np(t["q"][b, h, torch.tensor(sel, device=t["q"].device)])
+        ref = ar.attend(qn, K, V, t["scale"])
+        _close(out_unpacked[b, h, torch.tensor(sel, device=out_unpacked.device)], ref)
+
+
+@pytest.mark.parametrize("cfg,variant", [(1, ""), (2, ""), (3, ""), (4, ""), (5, ""), (5, "prefill")])
+def test_baseline_config_full_size(cfg, variant, device):
+    import bench
+
+    case = bench.make_case(cfg, device, variant=variant)
+    out = case.step()
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    B = len(case.lengths_q)
+    H = case.H
+    if cfg in (3, 4, 5):
+        # padding positions are zeros after unpack
+        N = out.shape[2]
+        L = torch.tensor(case.lengths_q, device=device)
+        pad = torch.arange(N, device=device)[None, :] >= L[:, None]
+        assert bool((out.permute(0, 2, 1, 3)[pad] == 0).all())
+    rng = np.random.default_rng(cfg)
+    pairs = [(0, 0), (B - 1, H - 1)] + [(int(rng.integers(B)), int(rng.integers(H))) for _ in range(2)]
+    _check_sampled(case, out, pairs, rows=None if cfg in (1, 2, 4) else 64)
