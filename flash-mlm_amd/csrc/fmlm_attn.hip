@@ -27,43 +27,117 @@
 namespace fmlm {
 
 // ---------------------------------------------------------------------------
-// Work schedule: one item per (sequence b, query tile j) with tiles of BQ rows,
-// only over real (unpadded) rows.
+// Work schedule.  A work unit is (sequence b, head h, query tile j) with tiles of BQ
+// real (unpadded) rows.  Units of one (b, h) group share that group's K/V, so a group
+// is kept on one XCD: the dispatcher hands workgroup L to XCD L % 8, so group g goes
+// to XCD g % 8 and its units occupy consecutive slots x + 8*pos of that XCD.  Groups
+// are visited longest-first (estimated keys x tiles), which also balances the XCDs.
+// Slots past an XCD's share are idle (b = -1).  The list is built once per
+// cu_seqlens by schedule_kernel and cached by the host.
 // ---------------------------------------------------------------------------
-constexpr int kSchedThreads = 1024;
+constexpr int kXcds = 8;
+constexpr int kSchedThreads = 512;  // one wave per XCD
+constexpr int kSortMax = 2048;      // sequences ordered longest-first up to this many
 
-__global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* __restrict__ cu,
-                                                                 int B, int BQ, int capacity,
-                                                                 int2* __restrict__ items,
-                                                                 int32_t* __restrict__ n_items) {
-  __shared__ int s_til[kSchedThreads];
+struct SeqInfo {
+  int q0, len;       // packed start and clamped length of sequence b
+  int ctx, mainlen;  // context keys and main keys it attends to
+};
+
+FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
+  const int32_t* cu = p.cu_seqlens_q;
+  SeqInfo s;
+  s.q0 = seq_start(cu, b, p.N);
+  int L = p.N;
+  if (cu) {
+    L = cu[b + 1] - s.q0;
+    if (p.N > 0) L = min(L, p.N);
+    L = max(min(L, p.total_q - s.q0), 0);
+  }
+  s.len = L;
+  s.ctx = 0;
+  if (!(p.flags & FMLM_FLAG_PREFILL)) {
+    const int cb = p.ctx_batch > 1 ? b : 0;
+    int c0 = 0, c1 = p.ctx_len;
+    if (p.cu_seqlens_kv) {
+      c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
+      c1 = min(max(p.cu_seqlens_kv[cb + 1], c0), p.ctx_rows);
+    }
+    s.ctx = max(c1 - c0, 0);
+  }
+  s.mainlen = ((p.flags & FMLM_FLAG_CAUSAL_SEQ) && cu) ? s.q0 + L : L;
+  return s;
+}
+
+__global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn_params p, int BQ,
+                                                                 int capacity,
+                                                                 int4* __restrict__ units,
+                                                                 int32_t* __restrict__ n_units) {
+  __shared__ int s_tiles[kSortMax];
+  __shared__ float s_work[kSortMax];
+  __shared__ int s_order[kSortMax];
+  __shared__ int s_len[kXcds];
   const int tid = threadIdx.x;
-  int carry = 0;
-  for (int base = 0; base < B; base += kSchedThreads) {
-    const int b = base + tid;
-    int tiles = 0;
-    if (b < B) {
-      const int len = cu[b + 1] - cu[b];
-      tiles = len > 0 ? (len + BQ - 1) / BQ : 0;
+  const int B = p.B, H = p.H;
+  const bool sorted = B <= kSortMax;
+  if (sorted) {
+    for (int b = tid; b < B; b += kSchedThreads) {
+      const SeqInfo si = seq_info(p, b);
+      const int tiles = (si.len + BQ - 1) / BQ;
+      s_tiles[b] = tiles;
+      s_work[b] = (float)tiles * (float)(si.ctx + si.mainlen + BQ);
     }
-    s_til[tid] = tiles;
     __syncthreads();
-    for (int off = 1; off < kSchedThreads; off <<= 1) {
-      int t = tid >= off ? s_til[tid - off] : 0;
-      __syncthreads();
-      s_til[tid] += t;
-      __syncthreads();
+    for (int b = tid; b < B; b += kSchedThreads) {
+      const float wb = s_work[b];
+      int rank = 0;
+      for (int o = 0; o < B; ++o) {
+        const float wo = s_work[o];
+        rank += (wo > wb) || (wo == wb && o < b);
+      }
+      s_order[rank] = b;
     }
-    const int first = carry + s_til[tid] - tiles;
-    for (int j = 0; j < tiles && first + j < capacity; ++j) items[first + j] = make_int2(b, j);
-    carry += s_til[kSchedThreads - 1];
     __syncthreads();
   }
-  if (tid == 0) *n_items = min(carry, capacity);
+  const int x = tid >> 6, lane = tid & 63;
+  const int G = B * H;
+  int carry = 0;
+  for (int i0 = 0; x + kXcds * i0 < G; i0 += 64) {
+    const int g = x + kXcds * (i0 + lane);
+    int b = 0, h = 0, tiles = 0;
+    if (g < G) {
+      const int r = g / H;
+      h = g - r * H;
+      b = sorted ? s_order[r] : r;
+      tiles = sorted ? s_tiles[b] : (seq_info(p, b).len + BQ - 1) / BQ;
+    }
+    // inclusive wave scan of tiles
+    int incl = tiles;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off);
+      if (lane >= off) incl += v;
+    }
+    const int pos = carry + incl - tiles;
+    for (int j = 0; j < tiles; ++j) {
+      const int64_t slot = (int64_t)x + (int64_t)kXcds * (pos + j);
+      if (slot < capacity) units[slot] = make_int4(b, h, j, 0);
+    }
+    carry += __shfl(incl, 63);
+  }
+  if (lane == 0) s_len[x] = carry;
+  __syncthreads();
+  int maxlen = 0;
+  for (int i = 0; i < kXcds; ++i) maxlen = max(maxlen, s_len[i]);
+  for (int q = carry + lane; q < maxlen; q += 64) {
+    const int64_t slot = (int64_t)x + (int64_t)kXcds * q;
+    if (slot < capacity) units[slot] = make_int4(-1, 0, 0, 0);
+  }
+  if (tid == 0) *n_units = (int)min((int64_t)kXcds * maxlen, (int64_t)capacity);
 }
 
 // ---------------------------------------------------------------------------
-// Per-workgroup problem description resolved from (item, head).
+// Per-workgroup problem description resolved from its work unit.
 // ---------------------------------------------------------------------------
 struct KvSeg {
   const char* k;
@@ -92,29 +166,31 @@ FMLM_DEV int64_t seg_row(const KvSeg& s, int i, bool is_v, const int32_t* cu, in
   return base + (int64_t)bb * sb + (int64_t)(i - cu[bb]) * sn;
 }
 
-// Resolve the workgroup's item.  Returns false for an idle workgroup.
-FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int2* items, const int32_t* n_items,
-                           int BQ, int esz, WorkItem& w) {
-  int b, tile;
+// Resolve the workgroup's unit.  Returns false for an idle workgroup.
+FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const int32_t* n_units,
+                           int BQ, WorkItem& w) {
+  int b, h, tile;
   if (p.cu_seqlens_q) {
-    if ((int)blockIdx.x >= *n_items) return false;
-    const int2 it = items[blockIdx.x];
-    b = it.x;
-    tile = it.y;
+    if ((int)blockIdx.x >= *n_units) return false;
+    const int4 u = units[blockIdx.x];
+    b = u.x;
+    h = u.y;
+    tile = u.z;
+    if (b < 0) return false;
   } else {
+    // dense: group g = (b, h) on XCD g % 8, its ceil(N/BQ) tiles on consecutive slots
     const int nt = (p.N + BQ - 1) / BQ;
-    b = blockIdx.x / nt;
-    tile = blockIdx.x % nt;
+    const int x = blockIdx.x % kXcds, pos = blockIdx.x / kXcds;
+    const int g = (pos / nt) * kXcds + x;
+    tile = pos % nt;
+    if (g >= p.B * p.H) return false;
+    b = g / p.H;
+    h = g - b * p.H;
   }
-  const int h = blockIdx.y;
   const int32_t* cu = p.cu_seqlens_q;
-  const int q0 = seq_start(cu, b, p.N);
-  int L = p.N;
-  if (cu) {
-    L = cu[b + 1] - q0;
-    if (p.N > 0) L = min(L, p.N);
-    L = max(min(L, p.total_q - q0), 0);
-  }
+  const SeqInfo si = seq_info(p, b);
+  const int q0 = si.q0;
+  const int L = si.len;
   w.b = b;
   w.h = h;
   w.qpos0 = tile * BQ;
@@ -176,7 +252,6 @@ FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int2* items, const i
       m.vbase = (int64_t)b * v_sb + (int64_t)h * v_sh;
     }
   }
-  (void)esz;
   return true;
 }
 
@@ -204,48 +279,52 @@ struct Mfma<f16> {
   }
 };
 
-// Position of key k (within a BK tile) in the transposed V tile.  Within each
-// 32-key block, key 16*hf + 4*g + r goes to 8*g + 4*hf + r so that lane group g
-// reads its eight P.V keys (the S^T rows 4g..4g+3 of two adjacent 16-key blocks)
-// as one 16-byte row segment.
-FMLM_DEV int vt_pos(int k) {
-  const int blk = k >> 5, kk = k & 31;
-  const int hf = kk >> 4, g = (kk >> 2) & 3, r = kk & 3;
-  return (blk << 5) + (g << 3) + (hf << 2) + r;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define FMLM_LDS __attribute__((address_space(3)))
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane j supplies the address of
+// four consecutive 16-bit elements M[j][0..3]; lane i receives M[4e + i/4][i%4], e=0..3.
+FMLM_DEV s16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLM_LDS s16x4*)(p));
 }
 
 template <typename T, int D, int QB, int NW, int BK>
 struct MfmaCfg {
   static constexpr int NT = NW * 64;
   static constexpr int BQ = NW * QB * 16;
-  static constexpr int KS = D + 8;   // LDS K row stride (elements)
-  static constexpr int VS = BK + 8;  // LDS V^T row stride (elements)
+  static constexpr int KS = D + 8;    // LDS K row stride: 16 rows of a b128 read hit distinct banks
+  static constexpr int VS = D + 16;   // LDS V row stride: 8 rows of a tr16 read hit distinct banks
   static constexpr int KTILE = BK * KS;
-  static constexpr int VTILE = D * VS;
-  static constexpr int LDS_BYTES = (KTILE + VTILE) * 2;
+  static constexpr int VTILE = BK * VS;
+  static constexpr int STAGE = KTILE + VTILE;          // elements per pipeline stage
+  static constexpr int LDS_BYTES = 2 * STAGE * 2;      // two stages
   static constexpr int KC = (D + 31) / 32;   // 32-wide contraction steps over D
   static constexpr int NDB = D / 16;         // 16-wide output column blocks
   static constexpr int NKB = BK / 16;        // 16-key S^T blocks per tile
   static constexpr int NKS = BK / 32;        // 32-key P.V steps per tile
   static constexpr int C8 = D / 8;           // 16-byte chunks per row
-  static constexpr int LITEMS = (BK / 4) * C8;  // loader items (4 keys x 8 columns)
-  static constexpr int LPT = (LITEMS + NT - 1) / NT;  // loader items per thread
+  static constexpr int CHUNKS = BK * C8;     // 16-byte chunks per K (or V) tile
+  static constexpr int LPT = (CHUNKS + NT - 1) / NT;  // chunks per thread per tensor
   static_assert(D % 16 == 0 && D >= 16, "head dim");
   static_assert(BK % 32 == 0, "key tile");
 };
 
+// Lazy rescaling: the running max used for exp2 only moves when a new row max
+// exceeds it by more than this (log2 units), so P <= 2^kRescaleSlack and most tiles
+// skip the O / l rescale.  Exact after the final O / l.
+constexpr float kRescaleSlack = 8.0f;
+
 template <typename T, int D, int QB, int NW, int BK>
-__global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(const fmlm_attn_params p,
-                                                            const int2* __restrict__ items,
-                                                            const int32_t* __restrict__ n_items) {
+__global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(const fmlm_attn_params p,
+                                                               const int4* __restrict__ units,
+                                                               const int32_t* __restrict__ n_units) {
   typedef MfmaCfg<T, D, QB, NW, BK> C;
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
-  T* Ks = (T*)smem_raw;
-  T* Vt = Ks + C::KTILE;
+  T* const lds = (T*)smem_raw;
 
   WorkItem w;
-  if (!resolve_work(p, items, n_items, C::BQ, 2, w)) return;
+  if (!resolve_work(p, units, n_units, C::BQ, w)) return;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -254,6 +333,10 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(const fmlm_attn_para
   const int g = lane >> 4;
   const int32_t* cu = p.cu_seqlens_q;
   const int B = p.B;
+  // softmax(scale * s): a negative scale is folded into Q's sign so the exponent
+  // scale c is positive; a tiny floor keeps -inf * c == -inf for masked keys.
+  const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
+  const float c = fmaxf(fabsf(p.scale) * kLog2e, 1e-30f);
 
   // ---- Q fragments: lane (q + 16g), block qb, step kc holds Q[row][kc*32 + 8g .. +8]
   v8 qf[QB][C::KC];
@@ -266,10 +349,10 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(const fmlm_attn_para
 #pragma unroll
     for (int kc = 0; kc < C::KC; ++kc) {
       const int col = kc * 32 + g * 8;
-      if (ok && col < D)
-        qf[qb][kc] = *(const v8*)(qbase + (off + col) * 2);
-      else
-        qf[qb][kc] = v8{};
+      u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+      if (ok && col < D) raw = *(const u32x4*)(qbase + (off + col) * 2);
+      raw ^= qsign;
+      qf[qb][kc] = __builtin_bit_cast(v8, raw);
     }
   }
 
@@ -284,70 +367,58 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(const fmlm_attn_para
     m_i[qb] = -INFINITY;
     l_i[qb] = 0.f;
   }
-  const float c = p.scale * kLog2e;
 
   // ---- tile sequence: context tiles then main tiles
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
   const int ntiles = nt0 + nt1;
 
-  u32x4 kreg[C::LPT][4], vreg[C::LPT][4];
+  // global -> register prefetch of one K and one V tile (16-byte chunks, row-major)
+  u32x4 kreg[C::LPT], vreg[C::LPT];
   auto issue_loads = [&](int t) {
     const KvSeg& s = t < nt0 ? w.seg[0] : w.seg[1];
     const int j0 = (t < nt0 ? t : t - nt0) * BK;
 #pragma unroll
     for (int li = 0; li < C::LPT; ++li) {
       const int it = tid + li * C::NT;
-      const int kq = it / C::C8, c8 = it % C::C8;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = j0 + kq * 4 + r;
-        if (it < C::LITEMS && key < s.n) {
-          const int64_t kr = seg_row(s, key, false, cu, B);
-          const int64_t vr = seg_row(s, key, true, cu, B);
-          kreg[li][r] = *(const u32x4*)(s.k + (kr + c8 * 8) * 2);
-          vreg[li][r] = *(const u32x4*)(s.v + (vr + c8 * 8) * 2);
-        } else {
-          kreg[li][r] = u32x4{0u, 0u, 0u, 0u};
-          vreg[li][r] = u32x4{0u, 0u, 0u, 0u};
-        }
+      const int row = it / C::C8, c8 = it % C::C8;
+      const int key = j0 + row;
+      kreg[li] = u32x4{0u, 0u, 0u, 0u};
+      vreg[li] = u32x4{0u, 0u, 0u, 0u};
+      if ((C::CHUNKS % C::NT == 0 || it < C::CHUNKS) && key < s.n) {
+        const int64_t kr = seg_row(s, key, false, cu, B);
+        const int64_t vr = seg_row(s, key, true, cu, B);
+        kreg[li] = *(const u32x4*)(s.k + (kr + c8 * 8) * 2);
+        vreg[li] = *(const u32x4*)(s.v + (vr + c8 * 8) * 2);
       }
     }
   };
-  auto store_lds = [&]() {
+  auto store_lds = [&](int stage) {
+    T* Ks = lds + stage * C::STAGE;
+    T* Vs = Ks + C::KTILE;
 #pragma unroll
     for (int li = 0; li < C::LPT; ++li) {
       const int it = tid + li * C::NT;
-      if (it >= C::LITEMS) continue;
-      const int kq = it / C::C8, c8 = it % C::C8;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) *(u32x4*)(Ks + (kq * 4 + r) * C::KS + c8 * 8) = kreg[li][r];
-      // transpose 4 keys x 8 columns into 8 rows of V^T (4 keys each)
-      const int pos = vt_pos(kq * 4);
-#pragma unroll
-      for (int dw = 0; dw < 4; ++dw) {
-        const uint32_t a0 = vreg[li][0][dw], a1 = vreg[li][1][dw];
-        const uint32_t a2 = vreg[li][2][dw], a3 = vreg[li][3][dw];
-        u32x2 lo, hi;
-        lo[0] = (a0 & 0xffffu) | (a1 << 16);
-        lo[1] = (a2 & 0xffffu) | (a3 << 16);
-        hi[0] = (a0 >> 16) | (a1 & 0xffff0000u);
-        hi[1] = (a2 >> 16) | (a3 & 0xffff0000u);
-        *(u32x2*)(Vt + (c8 * 8 + dw * 2) * C::VS + pos) = lo;
-        *(u32x2*)(Vt + (c8 * 8 + dw * 2 + 1) * C::VS + pos) = hi;
-      }
+      if (C::CHUNKS % C::NT != 0 && it >= C::CHUNKS) continue;
+      const int row = it / C::C8, c8 = it % C::C8;
+      *(u32x4*)(Ks + row * C::KS + c8 * 8) = kreg[li];
+      *(u32x4*)(Vs + row * C::VS + c8 * 8) = vreg[li];
     }
   };
 
-  if (ntiles > 0) issue_loads(0);
+  if (ntiles > 0) {
+    issue_loads(0);
+    store_lds(0);
+    if (ntiles > 1) issue_loads(1);
+  }
+  __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
+    const int stage = t & 1;
+    const T* Ks = lds + stage * C::STAGE;
+    const T* Vs = Ks + C::KTILE;
     const int nk = t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
-    __syncthreads();  // previous tile's LDS reads are done
-    store_lds();
-    __syncthreads();
-    if (t + 1 < ntiles) issue_loads(t + 1);
 
-    // ---- S^T = K Q^T
+    // ---- S^T = K Q^T: accumulator lane (q + 16g) reg r = S[query q][key 16kb + 4g + r]
     f32x4 s[C::NKB][QB];
 #pragma unroll
     for (int kb = 0; kb < C::NKB; ++kb)
@@ -364,67 +435,81 @@ __global__ __launch_bounds__(NW * 64) void attn_mfma_kernel(const fmlm_attn_para
       }
     }
 
+    // the other stage is free: land the prefetched tile there and fetch the next
+    if (t + 1 < ntiles) {
+      store_lds(stage ^ 1);
+      if (t + 2 < ntiles) issue_loads(t + 2);
+    }
+
     // ---- online softmax (mlm_kernel_impl.py:42-60); lane owns query l16 of each block
-    const bool partial = nk < BK;
-    typename Mfma<T>::v8 pf[C::NKS][QB];
+    if (nk < BK) {
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kb * 16 + g * 4 + r >= nk)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) s[kb][qb][r] = -INFINITY;
+    }
+    v8 pf[C::NKS][QB];
+    bool need_rescale = false;
+    float m_new[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      if (partial) {
+      float mx = s[0][qb][0];
 #pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb)
+      for (int kb = 0; kb < C::NKB; ++kb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (kb * 16 + g * 4 + r >= nk) s[kb][qb][r] = -INFINITY;
+        for (int r = (kb == 0 ? 1 : 0); r < 4; ++r) mx = fmaxf(mx, s[kb][qb][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx *= c;
+      const bool grow = mx > m_i[qb] + kRescaleSlack;
+      m_new[qb] = grow ? mx : m_i[qb];
+      need_rescale = need_rescale || grow;
+    }
+    if (__builtin_amdgcn_ballot_w64(need_rescale)) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const float alpha = fast_exp2(m_i[qb] - m_new[qb]);  // 1 where unchanged, 0 on the first tile
+        m_i[qb] = m_new[qb];
+        l_i[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) o[db][qb] *= alpha;
       }
-      float mx = -INFINITY;
-      if (c >= 0.f) {
+    }
 #pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][qb][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        mx *= c;
-      } else {
-        float mn = INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            mn = s[kb][qb][r] == -INFINITY ? mn : fminf(mn, s[kb][qb][r]);
-        mn = fminf(mn, __shfl_xor(mn, 16));
-        mn = fminf(mn, __shfl_xor(mn, 32));
-        mx = mn * c;
-      }
-      const float m_new = fmaxf(m_i[qb], mx);
-      const float alpha = fast_exp2(m_i[qb] - m_new);
-      m_i[qb] = m_new;
+    for (int qb = 0; qb < QB; ++qb) {
+      const float mneg = -m_i[qb];
       float rs = 0.f;
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float x = s[kb][qb][r];
-          const float pv = x == -INFINITY ? 0.f : fast_exp2(x * c - m_new);
+          const float pv = fast_exp2(fmaf(s[kb][qb][r], c, mneg));
           rs += pv;
           pf[kb >> 1][qb][(kb & 1) * 4 + r] = (T)pv;
         }
       }
-      l_i[qb] = l_i[qb] * alpha + rs;
-#pragma unroll
-      for (int db = 0; db < C::NDB; ++db) o[db][qb] *= alpha;
+      l_i[qb] += rs;
     }
 
-    // ---- O^T += V^T P^T
+    // ---- O^T += V^T P^T; the V^T fragment comes from row-major V via two tr16 reads:
+    // lane (j + 16g) addresses V[32ks + 16h + 4g + j/4][16db + 4(j%4)], h = 0, 1, so lane
+    // (i + 16g) receives V[32ks + 16h + 4g + e][16db + i] -- the keys of its P^T elements.
 #pragma unroll
     for (int ks = 0; ks < C::NKS; ++ks) {
 #pragma unroll
       for (int db = 0; db < C::NDB; ++db) {
-        const v8 a = *(const v8*)(Vt + (db * 16 + l16) * C::VS + ks * 32 + g * 8);
+        const T* base = Vs + (ks * 32 + g * 4 + (l16 >> 2)) * C::VS + db * 16 + (l16 & 3) * 4;
+        const s16x4 lo = lds_read_tr16(base);
+        const s16x4 hi = lds_read_tr16(base + 16 * C::VS);
+        const v8 a = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) o[db][qb] = Mfma<T>::run(a, pf[ks][qb], o[db][qb]);
       }
     }
+    __syncthreads();  // this stage is consumed; the next one is complete
   }
 
   // ---- epilogue: O /= l (l == 0 -> 1), store valid rows (mlm_kernel_impl.py:381-390)
@@ -470,14 +555,14 @@ FMLM_DEV float to_f(T x) {
 
 template <typename T, int D>
 __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
-    const fmlm_attn_params p, const int2* __restrict__ items, const int32_t* __restrict__ n_items) {
+    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
   typedef SimtCfg<D> C;
   extern __shared__ __align__(16) char smem_raw[];
   float* Kf = (float*)smem_raw;
   float* Vf = Kf + C::BKS * D;
 
   WorkItem w;
-  if (!resolve_work(p, items, n_items, C::RPW, (int)sizeof(T), w)) return;
+  if (!resolve_work(p, units, n_units, C::RPW, w)) return;
   const int tid = threadIdx.x;
   const int row = tid / C::TPR;
   const int part = tid % C::TPR;
@@ -607,14 +692,21 @@ static int pick_launch(int dtype, int D, Launch& L) {
   return ok ? 0 : FMLM_E_HEAD_DIM;
 }
 
-static int64_t max_items(const fmlm_attn_params& p, int bq) {
-  if (!p.cu_seqlens_q) return (int64_t)p.B * ((p.N + bq - 1) / bq);
-  return (int64_t)p.B + p.total_q / bq + 1;
+// Grid size (1-D): dense units are laid out arithmetically, packed units by the
+// schedule, whose XCD slots are bounded by ceil(total/8) + the largest group.
+static int64_t grid_units(const fmlm_attn_params& p, int bq) {
+  if (!p.cu_seqlens_q) {
+    const int64_t groups = (int64_t)p.B * p.H;
+    return kXcds * ((groups + kXcds - 1) / kXcds) * ((p.N + bq - 1) / bq);
+  }
+  const int64_t total = (int64_t)p.H * (p.B + p.total_q / bq + 1);
+  const int64_t max_group = (p.N > 0 ? (p.N + bq - 1) / bq : p.total_q / bq + 1) + 1;
+  return kXcds * ((total + kXcds - 1) / kXcds + max_group);
 }
 
 static int64_t workspace_for(const fmlm_attn_params& p, int bq) {
   if (!p.cu_seqlens_q) return 0;
-  return 256 + max_items(p, bq) * (int64_t)sizeof(int2);
+  return 256 + grid_units(p, bq) * (int64_t)sizeof(int4);
 }
 
 static int check_params(const fmlm_attn_params& p) {
@@ -630,10 +722,10 @@ static int check_params(const fmlm_attn_params& p) {
 }
 
 static int launch_schedule(const fmlm_attn_params& p, int bq, char* sched, hipStream_t s) {
-  const int64_t cap = max_items(p, bq);
+  const int64_t cap = grid_units(p, bq);
   if (cap > 0x7fffffff) return FMLM_E_ARG;
-  hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, s, p.cu_seqlens_q, p.B, bq,
-                     (int)cap, (int2*)(sched + 256), (int32_t*)sched);
+  hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, s, p, bq, (int)cap,
+                     (int4*)(sched + 256), (int32_t*)sched);
   return launch_status();
 }
 
@@ -672,7 +764,6 @@ extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
   if (p.B == 0 || p.H == 0) return 0;
   const int64_t need = workspace_for(p, L.bq);
   if (need > 0 && !p.schedule && (!p.workspace || p.workspace_bytes < need)) return FMLM_E_WORKSPACE;
-  if (p.H > 65535) return FMLM_E_ARG;
   hipStream_t s = (hipStream_t)stream;
 
   // allow > 64 KiB of dynamic LDS once per kernel
@@ -690,24 +781,23 @@ extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
     }
   }
 
-  int2* items = nullptr;
-  int32_t* n_items = nullptr;
+  int4* units = nullptr;
+  int32_t* n_units = nullptr;
   if (p.cu_seqlens_q) {
     char* sched = (char*)(p.schedule ? p.schedule : p.workspace);
-    n_items = (int32_t*)sched;
-    items = (int2*)(sched + 256);
+    n_units = (int32_t*)sched;
+    units = (int4*)(sched + 256);
     if (!p.schedule) {
       rc = launch_schedule(p, L.bq, sched, s);
       if (rc) return rc;
     }
   }
-  const int64_t gx = max_items(p, L.bq);
+  const int64_t gx = grid_units(p, L.bq);
   if (gx <= 0) return 0;
   if (gx > 0x7fffffff) return FMLM_E_ARG;
   fmlm_attn_params pc = p;
-  void* args[] = {(void*)&pc, (void*)&items, (void*)&n_items};
-  hipError_t e = hipLaunchKernel(L.fn, dim3((unsigned)gx, (unsigned)p.H), dim3(L.threads), args,
-                                 (size_t)L.lds, s);
+  void* args[] = {(void*)&pc, (void*)&units, (void*)&n_units};
+  hipError_t e = hipLaunchKernel(L.fn, dim3((unsigned)gx), dim3(L.threads), args, (size_t)L.lds, s);
   if (e != hipSuccess) return (int)e;
   return launch_status();
 }

@@ -390,6 +390,7 @@ def _compressed_impl(
         raise ValueError("q_tile_starts_q must be rank-1")
     _check_cache_dtype(ctx.k_cache, q)
 
+    packed_kv = None  # (k, v, rows per head) of a packed copy of this call's K/V
     if prefill and inference_cache is not None:
         # packed, zero-padded K/V written straight into the layer's named workspace and
         # stored (as views) before the launch (host.py:326-364)
@@ -427,6 +428,7 @@ def _compressed_impl(
             num_heads=num_heads,
             head_dim=d,
         )
+        packed_kv = (k_entry, v_entry, T_pad)
 
     out = torch.empty((num_heads * T, d), dtype=q.dtype, device=q.device)
     if T == 0 or num_heads == 0:
@@ -435,7 +437,28 @@ def _compressed_impl(
     k_cache, v_cache = make_contiguous(ctx.k_cache, ctx.v_cache)
     cu_q = cu_seqlens_q.to(torch.int32).contiguous()
     cu_kv = ctx.cu_seqlens_kv.to(torch.int32).contiguous()
-    if is_mla:
+    kv_layout = _lib.LAYOUT_PADDED
+    if causal_query_seq_attn:
+        # the causal key range [0, cu[b+1]) spans sequences: pack K/V once (or reuse the
+        # prefill entry) so the kernel streams it linearly
+        if packed_kv is None:
+            kv_heads = 1 if is_mla else num_heads
+
+            def alloc(name: str) -> torch.Tensor:
+                if inference_cache is None:
+                    return torch.empty((kv_heads * T, d), dtype=k.dtype, device=k.device)
+                return inference_cache.packing.get_2d(name, kv_heads * T, d, dtype=k.dtype, device=k.device)
+
+            k_pk = alloc("k")
+            v_pk = k_pk if is_mla else alloc("v")
+            sources = [(k_[:, :1], 1)] if is_mla else [(k_, num_heads), (v_, num_heads)]
+            outs = [k_pk] if is_mla else [k_pk, v_pk]
+            _pack_rows(sources, outs, cu_seqlens=cu_q, B=b, N=n, D=d, total=T, total_padded=T)
+            packed_kv = (k_pk, v_pk, T)
+        k_, v_, rows = packed_kv
+        k_strides = v_strides = (0, 0 if is_mla else rows * d, d)
+        kv_layout = _lib.LAYOUT_PACKED
+    elif is_mla:
         k_strides = (k_.stride(0), 0, k_.stride(2))  # every head reads head 0
         v_strides = k_strides
     else:
@@ -464,7 +487,7 @@ def _compressed_impl(
         o_layout=_lib.LAYOUT_PACKED,
         k_strides=k_strides,
         v_strides=v_strides,
-        kv_layout=_lib.LAYOUT_PADDED,
+        kv_layout=kv_layout,
         k_ctx=k_cache,
         v_ctx=None if is_mla else v_cache,
         c_strides=c_strides,

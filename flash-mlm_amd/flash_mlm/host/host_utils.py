@@ -82,6 +82,10 @@ def build_pack_metadata(lengths: torch.Tensor, N: int, block_n: int) -> PackMeta
         raise ValueError("block_n must be >= 1")
     _require_device(lengths, what="build_pack_metadata")
 
+    if lengths.numel() == 0:
+        # the reference's tile map rejects a one-element cu_seqlens (host_utils.py:78-79)
+        raise ValueError("cu_seqlens_q must have at least 2 elements")
+
     lib = _lib.load()
     device = lengths.device
     if lengths.dtype not in (torch.int32, torch.int64):

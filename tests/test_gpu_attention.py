@@ -446,3 +446,28 @@ def test_baseline_config_full_size(cfg, variant, device):
     rng = np.random.default_rng(cfg)
     pairs = [(0, 0), (B - 1, H - 1)] + [(int(rng.integers(B)), int(rng.integers(H))) for _ in range(2)]
     _check_sampled(case, out, pairs, rows=None if cfg in (1, 2, 4) else 64)
+
+
+def test_abi_causal_over_padded_kv(device):
+    # the C ABI also accepts causal_query_seq_attn over padded K/V (per-row sequence
+    # lookup); the Python launchers pack first, so exercise that kernel path directly
+    from flash_mlm import _lib
+    from flash_mlm.host import host as hh
+
+    torch.manual_seed(91)
+    B, H, N, D = 4, 3, 70, 64
+    lengths = [70, 5, 33, 64]
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    T = meta.total_tokens
+    out = torch.empty((H * T, D), dtype=q.dtype, device=device)
+    empty = torch.empty((0, D), dtype=q.dtype, device=device)
+    hh._launch(
+        q=q, out=out, k=k, v=v, B=B, H=H, D=D, N=N, total_q=T, cu_seqlens_q=meta.cu_seqlens,
+        q_strides=(q.stride(0), q.stride(1), q.stride(2)), q_layout=_lib.LAYOUT_PADDED,
+        o_strides=(0, T * D, D), o_layout=_lib.LAYOUT_PACKED,
+        k_strides=(k.stride(0), k.stride(1), k.stride(2)), v_strides=(v.stride(0), v.stride(1), v.stride(2)),
+        kv_layout=_lib.LAYOUT_PADDED, k_ctx=empty, v_ctx=empty, c_strides=(0, 0, D), cu_seqlens_kv=None,
+        ctx_len=0, ctx_batch=1, ctx_rows=0, scale=0.3, flags=_lib.FLAG_CAUSAL_SEQ, inference_cache=None,
+    )
+    _close(unpack_from_kernel(out, meta, H), _packed_oracle(q, k, v, lengths, 0.3, causal=True))

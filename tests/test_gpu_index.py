@@ -78,8 +78,11 @@ def test_metadata_random_vs_oracle(seed, device):
 
 
 def test_metadata_empty_batch(device):
-    meta = build_pack_metadata(torch.zeros(0, dtype=torch.int32, device=device), 16, 4)
-    _check_meta(meta, pack_ref.pack_metadata(np.zeros(0, dtype=np.int32), 16, 4))
+    # B = 0: the reference's tile map rejects cu_seqlens = [0] (host_utils.py:78-79)
+    with pytest.raises(ValueError, match="cu_seqlens_q must have at least 2 elements"):
+        build_pack_metadata(torch.zeros(0, dtype=torch.int32, device=device), 16, 4)
+    with pytest.raises(ValueError, match="cu_seqlens_q must have at least 2 elements"):
+        pack_ref.pack_metadata(np.zeros(0, dtype=np.int32), 16, 4)
     meta = build_pack_metadata(torch.zeros(3, dtype=torch.int32, device=device), 0, 4)
     _check_meta(meta, pack_ref.pack_metadata(np.zeros(3, dtype=np.int32), 0, 4))
 

@@ -36,6 +36,11 @@ def test_metadata_errors_match_reference(case):
         pack_ref.pack_metadata(np.array(case["lengths"]), case["N"], case["block_n"])
 
 
+def test_metadata_rejects_empty_batch():
+    with pytest.raises(ValueError, match="cu_seqlens_q must have at least 2 elements"):
+        pack_ref.pack_metadata(np.zeros(0, dtype=np.int32), 16, 4)
+
+
 def test_metadata_rejects_out_of_range_lengths():
     with pytest.raises(ValueError, match=r"lengths values must be in \[0, N\]"):
         pack_ref.pack_metadata(np.array([3, 5]), 4, 2)
