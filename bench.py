@@ -255,6 +255,12 @@ def main() -> None:
     ap.add_argument("--variant", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument(
+        "--profile",
+        action="store_true",
+        help="profiling driver for rocprofv3: one 256 MiB device copy (calibrates the HBM byte "
+        "counters) then --steps bare attention launches; prints no JSON line",
+    )
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -272,6 +278,18 @@ def main() -> None:
     torch.cuda.set_device(device)
     case = make_case(args.config, device, variant=args.variant)
     print(f"[bench] {case.workload}: built inputs", file=sys.stderr, flush=True)
+
+    if args.profile:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # 256 MiB read + 256 MiB write
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            case.attention()
+        torch.cuda.synchronize()
+        print(f"[bench] profiled {args.steps} attention launches", file=sys.stderr, flush=True)
+        return
 
     ms = _time_steps(case.step, args.steps, args.warmup)
     print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step", file=sys.stderr, flush=True)

@@ -378,6 +378,26 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(const fmlm_attn_p
   auto issue_loads = [&](int t) {
     const KvSeg& s = t < nt0 ? w.seg[0] : w.seg[1];
     const int j0 = (t < nt0 ? t : t - nt0) * BK;
+    if (!s.lookup) {
+      // tile base is workgroup-uniform; each chunk adds a 32-bit element offset
+      const char* kt = s.k + (s.kbase + (int64_t)j0 * s.ksn) * 2;
+      const char* vt = s.v + (s.vbase + (int64_t)j0 * s.vsn) * 2;
+      const int ksn = (int)s.ksn, vsn = (int)s.vsn;
+      const bool full = j0 + BK <= s.n;
+#pragma unroll
+      for (int li = 0; li < C::LPT; ++li) {
+        const int it = tid + li * C::NT;
+        const int row = it / C::C8, c8 = it % C::C8;
+        const bool ok = (C::CHUNKS % C::NT == 0 || it < C::CHUNKS) && (full || j0 + row < s.n);
+        kreg[li] = u32x4{0u, 0u, 0u, 0u};
+        vreg[li] = u32x4{0u, 0u, 0u, 0u};
+        if (ok) {
+          kreg[li] = *(const u32x4*)(kt + (int64_t)(row * ksn + c8 * 8) * 2);
+          vreg[li] = *(const u32x4*)(vt + (int64_t)(row * vsn + c8 * 8) * 2);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int li = 0; li < C::LPT; ++li) {
       const int it = tid + li * C::NT;
@@ -711,6 +731,10 @@ static int64_t workspace_for(const fmlm_attn_params& p, int bq) {
 
 static int check_params(const fmlm_attn_params& p) {
   if (p.B < 0 || p.H < 0 || p.N < 0 || p.D < 1 || p.total_q < 0 || p.ctx_len < 0) return FMLM_E_ARG;
+  // row strides are applied as 32-bit offsets within a key tile
+  const int64_t kMaxRowStride = 1 << 22;
+  for (int64_t sn : {p.k_sn, p.v_sn, p.c_sn, p.q_sn, p.o_sn})
+    if (sn < 0 || sn >= kMaxRowStride) return FMLM_E_ARG;
   if (!p.q || !p.o || !p.k || (!(p.flags & FMLM_FLAG_MLA) && !p.v)) return FMLM_E_ARG;
   if ((p.flags & FMLM_FLAG_CAUSAL_SEQ) && !p.cu_seqlens_q) return FMLM_E_ARG;
   if (!(p.flags & FMLM_FLAG_PREFILL)) {
