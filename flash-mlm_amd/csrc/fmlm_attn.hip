@@ -554,6 +554,246 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(const fmlm_attn_p
 }
 
 // ---------------------------------------------------------------------------
+// MLA kernel for a 512-wide latent (K = V = one latent row shared by all heads).
+//
+// Q and O of 16+ rows x 512 columns do not fit one wave's registers next to each
+// other, so a workgroup of 8 waves covers 64 query rows of one head as 2 row groups
+// x 4 slices.  Per 64-key tile, wave (rg, s):
+//   S^T for the 16 keys [16s, 16s+16) x its group's 32 rows (Q in registers, full D),
+//   row max and P exchanged with the group's other slices through LDS,
+//   O^T for the 128 columns [128s, 128s+128) x 32 rows over all 64 keys.
+// The latent tile (64 rows x 1 KiB) is fetched with direct-to-LDS loads into a
+// double-buffered, XOR-swizzled layout (16-byte chunk c of row r lives at c ^ swz(r)),
+// which keeps both the b128 K reads and the tr16 V reads free of bank conflicts.
+// ---------------------------------------------------------------------------
+struct MlaCfg {
+  static constexpr int D = 512;
+  static constexpr int NT = 512;         // 8 waves
+  static constexpr int BQ = 64;          // query rows per workgroup
+  static constexpr int BK = 64;          // keys per tile
+  static constexpr int ROW_BYTES = D * 2;
+  static constexpr int TILE_BYTES = BK * ROW_BYTES;          // 64 KiB
+  static constexpr int PS = BK + 8;                          // P row stride (elements)
+  static constexpr int P_BYTES = 2 * 32 * PS * 2;            // [rg][32 rows][PS] 16-bit
+  static constexpr int RED_BYTES = 2 * 4 * 32 * 4;           // [rg][slice][32 rows] fp32
+  static constexpr int LDS_BYTES = 2 * TILE_BYTES + P_BYTES + RED_BYTES;
+};
+
+FMLM_DEV int mla_swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
+
+template <typename T>
+__global__ __launch_bounds__(MlaCfg::NT, 1) void attn_mla512_kernel(const fmlm_attn_params p,
+                                                                   const int4* __restrict__ units,
+                                                                   const int32_t* __restrict__ n_units) {
+  typedef MlaCfg C;
+  typedef typename Mfma<T>::v8 v8;
+  constexpr int D = C::D, BK = C::BK;
+  extern __shared__ __align__(16) char smem_raw[];
+  char* const tiles = smem_raw;                                    // 2 stages
+  T* const Ps = (T*)(smem_raw + 2 * C::TILE_BYTES);                // [rg][32][PS]
+  float* const red = (float*)(smem_raw + 2 * C::TILE_BYTES + C::P_BYTES);  // [rg][4][32]
+
+  WorkItem w;
+  if (!resolve_work(p, units, n_units, C::BQ, w)) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int rg = wave >> 2, sl = wave & 3;  // row group, slice
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
+  const float c = fmaxf(fabsf(p.scale) * kLog2e, 1e-30f);
+
+  // ---- Q fragments of this row group's 32 rows (2 blocks of 16), full D
+  v8 qf[2][D / 32];
+  const char* qbase = (const char*)p.q;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = rg * 32 + qb * 16 + l16;
+    const bool ok = row < w.qcount;
+    const int64_t off = w.q_row0 + (int64_t)row * w.q_sn;
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc) {
+      u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+      if (ok) raw = *(const u32x4*)(qbase + (off + kc * 32 + g * 8) * 2);
+      raw ^= qsign;
+      qf[qb][kc] = __builtin_bit_cast(v8, raw);
+    }
+  }
+  f32x4 o[8][2];
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_i[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.f, 0.f};
+
+  const int nt0 = (w.seg[0].n + BK - 1) / BK;
+  const int nt1 = (w.seg[1].n + BK - 1) / BK;
+  const int ntiles = nt0 + nt1;
+
+  // direct-to-LDS fetch of tile t into stage st: wave w loads rows 8w..8w+7, lane l
+  // brings the logical chunk l ^ swz(row) so that physical chunk l holds it
+  auto fetch = [&](int t, int st) {
+    const KvSeg& s = t < nt0 ? w.seg[0] : w.seg[1];
+    const int j0 = (t < nt0 ? t : t - nt0) * BK;
+    const char* base = s.k + s.kbase * 2;
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int row = wave * 8 + rr;
+      const int key = min(j0 + row, s.n - 1);  // rows past the end repeat a valid row (masked)
+      const char* src = base + ((int64_t)key * s.ksn) * 2 + ((lane ^ mla_swz(row)) << 4);
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (FMLM_LDS void*)(tiles + st * C::TILE_BYTES + row * C::ROW_BYTES),
+                                       16, 0, 0);
+    }
+  };
+
+  // Per-lane byte offsets inside a tile (see mla_swz).  K: row 16 sl + l16, 16-byte
+  // chunk 4(4a + b) + g lives at koff[b] + 256 a.  V: rows 8g + l16/4 (+4), columns
+  // 128 sl + 16 db + 4 (l16 % 4) live at voff[db] (and voff[db ^ 4] + 4 rows).
+  int koff[4], voff[8];
+  {
+    const int krow = sl * 16 + l16;
+    const int sw = mla_swz(krow);
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      koff[b] = krow * C::ROW_BYTES + 64 * (b ^ (sw >> 2)) + 16 * (g ^ (sw & 3));
+    const int r7 = l16 >> 2;  // swz of row 8g + r7 is 2 r7 + (g & 1)
+    const int low = ((l16 & 3) >> 1) ^ (g & 1);
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+      voff[db] = (8 * g + r7) * C::ROW_BYTES + 256 * sl + 32 * (db ^ r7) + 16 * low + (l16 & 1) * 8;
+  }
+
+  if (ntiles > 0) fetch(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int st = t & 1;
+    const char* tile = tiles + st * C::TILE_BYTES;
+    if (t + 1 < ntiles) fetch(t + 1, st ^ 1);
+    const int nk = t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
+
+    // ---- S^T for keys [16 sl, 16 sl + 16) x 32 rows
+    f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int a = 0; a < D / 128; ++a) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int kc = a * 4 + b;
+        const v8 kf = *(const v8*)(tile + koff[b] + a * 256);
+        s[0] = Mfma<T>::run(kf, qf[0][kc], s[0]);
+        s[1] = Mfma<T>::run(kf, qf[1][kc], s[1]);
+      }
+    }
+    if (nk < BK) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (sl * 16 + g * 4 + r >= nk) {
+          s[0][r] = -INFINITY;
+          s[1][r] = -INFINITY;
+        }
+    }
+    // ---- row max across the 4 slices of the row group
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float mx = fmaxf(fmaxf(s[qb][0], s[qb][1]), fmaxf(s[qb][2], s[qb][3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (g == 0) red[(rg * 4 + sl) * 32 + qb * 16 + l16] = mx;
+    }
+    __syncthreads();
+    bool need_rescale = false;
+    float m_new[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = qb * 16 + l16;
+      float mx = fmaxf(fmaxf(red[(rg * 4 + 0) * 32 + r], red[(rg * 4 + 1) * 32 + r]),
+                       fmaxf(red[(rg * 4 + 2) * 32 + r], red[(rg * 4 + 3) * 32 + r]));
+      mx *= c;
+      const bool grow = mx > m_i[qb] + kRescaleSlack;
+      m_new[qb] = grow ? mx : m_i[qb];
+      need_rescale = need_rescale || grow;
+    }
+    if (__builtin_amdgcn_ballot_w64(need_rescale)) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float alpha = fast_exp2(m_i[qb] - m_new[qb]);
+        m_i[qb] = m_new[qb];
+        l_i[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[db][qb] *= alpha;
+      }
+    }
+    // ---- P for this slice's keys -> LDS as P[row][key]
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const float mneg = -m_i[qb];
+      T pv4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = fast_exp2(fmaf(s[qb][r], c, mneg));
+        l_i[qb] += pv;
+        pv4[r] = (T)pv;
+      }
+      *(u32x2*)(Ps + (rg * 32 + qb * 16 + l16) * C::PS + sl * 16 + g * 4) = *(const u32x2*)pv4;
+    }
+    __syncthreads();
+
+    // ---- O^T[128 sl + 16 db + i][row] += V^T P^T over the 64 keys; key order within a
+    // 32-key step: lane group g owns keys 8g..8g+7 (P: one b128 read, V: two tr16 reads,
+    // rows 8g + j/4 and 8g + 4 + j/4, the second at voff[db ^ 4] + 4 rows)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      v8 pb[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+        pb[qb] = *(const v8*)(Ps + (rg * 32 + qb * 16 + l16) * C::PS + ks * 32 + g * 8);
+      const char* vt = tile + ks * 32 * C::ROW_BYTES;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        const s16x4 lo = lds_read_tr16(vt + voff[db]);
+        const s16x4 hi = lds_read_tr16(vt + voff[db ^ 4] + 4 * C::ROW_BYTES);
+        const v8 a = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[db][0] = Mfma<T>::run(a, pb[0], o[db][0]);
+        o[db][1] = Mfma<T>::run(a, pb[1], o[db][1]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // next stage landed
+    __syncthreads();                // this stage, P and the max slots are free
+  }
+
+  // ---- epilogue: l summed over the 4 slices, O /= l, store this slice's columns
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float l = l_i[qb];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (g == 0) red[(rg * 4 + sl) * 32 + qb * 16 + l16] = l;
+  }
+  __syncthreads();
+  char* obase = (char*)p.o;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int r = qb * 16 + l16;
+    const float l = red[(rg * 4 + 0) * 32 + r] + red[(rg * 4 + 1) * 32 + r] +
+                    red[(rg * 4 + 2) * 32 + r] + red[(rg * 4 + 3) * 32 + r];
+    const float inv = l > 0.f ? 1.f / l : 1.f;
+    const int row = rg * 32 + r;
+    if (row >= w.qcount) continue;
+    const int64_t off = w.o_row0 + (int64_t)row * w.o_sn;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      T v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = (T)(o[db][qb][e] * inv);
+      *(u32x2*)(obase + (off + sl * 128 + db * 16 + g * 4) * 2) = *(const u32x2*)v4;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // SIMT kernel: one query row per TPR threads (each holding D/TPR dims), K/V tiles
 // staged in LDS as fp32.  Used for fp32 inputs and head dims without an MFMA
 // instantiation.  Probabilities are rounded to T before P.V like the MFMA path.
@@ -677,13 +917,28 @@ static Launch simt_launch() {
 }
 
 template <typename T>
-static bool pick_mfma(int D, Launch& L) {
-  switch (D) {
+static Launch mla512_launch() {
+  return Launch{MlaCfg::BQ, MlaCfg::NT, MlaCfg::LDS_BYTES, (const void*)&attn_mla512_kernel<T>};
+}
+
+// MFMA kernels by head dim; the 512-wide latent kernel needs K = V (MLA) and linear
+// main-key addressing (no per-row sequence lookup).
+template <typename T>
+static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
+  switch (p.D) {
     case 16: L = mfma_launch<T, 16, 2, 4, 64>(); return true;
     case 32: L = mfma_launch<T, 32, 2, 4, 64>(); return true;
     case 64: L = mfma_launch<T, 64, 2, 4, 64>(); return true;
     case 128: L = mfma_launch<T, 128, 2, 4, 64>(); return true;
     case 256: L = mfma_launch<T, 256, 1, 4, 64>(); return true;
+    case 512: {
+      const bool mla = p.flags & FMLM_FLAG_MLA;
+      const bool lookup = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q &&
+                          p.kv_layout != FMLM_LAYOUT_PACKED;
+      if (!mla || lookup) return false;
+      L = mla512_launch<T>();
+      return true;
+    }
     default: return false;
   }
 }
@@ -701,12 +956,12 @@ static bool pick_simt(int D, Launch& L) {
   }
 }
 
-static int pick_launch(int dtype, int D, Launch& L) {
+static int pick_launch(const fmlm_attn_params& p, Launch& L) {
   bool ok = false;
-  switch (dtype) {
-    case FMLM_DTYPE_BF16: ok = pick_mfma<bf16>(D, L) || pick_simt<bf16>(D, L); break;
-    case FMLM_DTYPE_F16: ok = pick_mfma<f16>(D, L) || pick_simt<f16>(D, L); break;
-    case FMLM_DTYPE_F32: ok = pick_simt<float>(D, L); break;
+  switch (p.dtype) {
+    case FMLM_DTYPE_BF16: ok = pick_mfma<bf16>(p, L) || pick_simt<bf16>(p.D, L); break;
+    case FMLM_DTYPE_F16: ok = pick_mfma<f16>(p, L) || pick_simt<f16>(p.D, L); break;
+    case FMLM_DTYPE_F32: ok = pick_simt<float>(p.D, L); break;
     default: return FMLM_E_DTYPE;
   }
   return ok ? 0 : FMLM_E_HEAD_DIM;
@@ -761,7 +1016,7 @@ extern "C" int fmlm_attn_schedule(const fmlm_attn_params* pp, void* schedule,
                                   int64_t schedule_bytes, void* stream) {
   if (!pp || !schedule || !pp->cu_seqlens_q || pp->B < 1) return FMLM_E_ARG;
   Launch L;
-  const int rc = pick_launch(pp->dtype, pp->D, L);
+  const int rc = pick_launch(*pp, L);
   if (rc) return rc;
   if (schedule_bytes < workspace_for(*pp, L.bq)) return FMLM_E_WORKSPACE;
   return launch_schedule(*pp, L.bq, (char*)schedule, (hipStream_t)stream);
@@ -772,7 +1027,7 @@ extern "C" int fmlm_attn_params_size(void) { return (int)sizeof(fmlm_attn_params
 extern "C" int64_t fmlm_attn_workspace_bytes(const fmlm_attn_params* p) {
   if (!p) return FMLM_E_ARG;
   Launch L;
-  const int rc = pick_launch(p->dtype, p->D, L);
+  const int rc = pick_launch(*p, L);
   if (rc) return rc;
   return workspace_for(*p, L.bq);
 }
@@ -783,7 +1038,7 @@ extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
   int rc = check_params(p);
   if (rc) return rc;
   Launch L;
-  rc = pick_launch(p.dtype, p.D, L);
+  rc = pick_launch(p, L);
   if (rc) return rc;
   if (p.B == 0 || p.H == 0) return 0;
   const int64_t need = workspace_for(p, L.bq);

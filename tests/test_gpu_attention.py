@@ -471,3 +471,44 @@ def test_abi_causal_over_padded_kv(device):
         ctx_len=0, ctx_batch=1, ctx_rows=0, scale=0.3, flags=_lib.FLAG_CAUSAL_SEQ, inference_cache=None,
     )
     _close(unpack_from_kernel(out, meta, H), _packed_oracle(q, k, v, lengths, 0.3, causal=True))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["ctx", "causal_ctx", "prefill", "shared_ctx"])
+def test_mla_latent512_packed(dtype, mode, device):
+    # MLA with a 512-wide latent (BASELINE config 5 shape class), odd lengths and tails
+    torch.manual_seed(3000 + len(mode))
+    lengths = [130, 1, 64, 97, 200]
+    B, H, N, D = len(lengths), 6, 200, 512
+    causal, prefill = "causal" in mode, mode == "prefill"
+    q = _randn((B, H, N, D), device, dtype, std=0.5)
+    k = _randn((B, H, N, D), device, dtype, std=0.5)
+    ctx_lengths = [70, 0, 5, 129, 64]
+    # shared_ctx: a per-sequence entry requested with context_batch_size=1 attends to all
+    # cached rows [0, total) (host_utils.py:232-237)
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, True, ctx_lengths, device, dtype, std=0.5)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    scale = 1.0 / math.sqrt(D)
+    cbs = 1 if mode == "shared_ctx" else B
+    out = flash_attn_mlm_compressed(q, k, k, H, meta, scale, cache, 0, is_mla=True, block_n=64,
+                                    causal_query_seq_attn=causal, prefill=prefill,
+                                    context_batch_size=1 if mode == "shared_ctx" else None)
+    cu_ref = [0, Tc] if mode == "shared_ctx" else cu_kv
+    ref = _packed_oracle(q, k, k, lengths, scale, is_mla=True, causal=causal, prefill=prefill,
+                         k_cache=kc, cu_kv=cu_ref, cbs=cbs, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+
+
+@pytest.mark.parametrize("cbs", [1, 2])
+def test_mla_latent512_dense(cbs, device):
+    torch.manual_seed(3100 + cbs)
+    B, H, N, D, C = 2, 4, 150, 512, 77
+    q = _randn((B, H, N, D), device, torch.bfloat16, std=0.5)
+    k = _randn((B, H, N, D), device, torch.bfloat16, std=0.5)
+    kc = _randn((cbs * C, D), device, torch.bfloat16, std=0.5)
+    cache = InferenceCache()
+    cache.prefill_kv_cache(0, k_cache=kc, context_batch_size=cbs, is_mla=True, num_heads=H, head_dim=D)
+    out = flash_attn_mlm(q, k, k, 1.0 / math.sqrt(D), inference_cache=cache, layer_id=0, is_mla=True)
+    ref = ar.mlm_attention_dense(_np(q), _np(k), _np(k), 1.0 / math.sqrt(D), is_mla=True, k_cache=_np(kc),
+                                 context_len=C, context_batch_size=cbs)
+    _close(out, ref)
