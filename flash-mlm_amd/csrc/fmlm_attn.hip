@@ -315,7 +315,7 @@ struct MfmaCfg {
 constexpr float kRescaleSlack = 8.0f;
 
 template <typename T, int D, int QB, int NW, int BK>
-__global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(const fmlm_attn_params p,
+__global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(const fmlm_attn_params p,
                                                                const int4* __restrict__ units,
                                                                const int32_t* __restrict__ n_units) {
   typedef MfmaCfg<T, D, QB, NW, BK> C;
@@ -539,6 +539,419 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(const fmlm_attn_p
     float l = l_i[qb];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    const float inv = l > 0.f ? 1.f / l : 1.f;
+    const int row = (wave * QB + qb) * 16 + l16;
+    if (row >= w.qcount) continue;
+    const int64_t off = w.o_row0 + (int64_t)row * w.o_sn;
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) {
+      T v4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = (T)(o[db][qb][r] * inv);
+      *(u32x2*)(obase + (off + db * 16 + g * 4) * 2) = *(const u32x2*)v4;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Software-pipelined MFMA kernel (v3) for head dims 16..256.
+//
+// The LDS holds two K tiles and two V tiles, filled by direct global->LDS loads (no
+// staging registers) with 16-byte chunks XOR-swizzled per row by kv_swz, so both the
+// b128 K reads and the tr16 V reads are bank-conflict free.  Iteration t of a wave:
+//   1. issues the loads of K(t+2) (into K(t)'s buffer) and V(t+1) (into V(t-1)'s);
+//   2. row max of S(t) (lane-local + two permlane swaps) and the lazy-rescale decision;
+//   3. one basic block that runs S(t+1) = K(t+1) Q^T on the MFMA pipe while the VALU
+//      computes P(t) = exp2(S(t) c - m), then O += V(t)^T P(t) and l += 1^T P(t) (the row
+//      sums as an MFMA against a ones operand);
+//   4. waits for its loads and meets the other waves at a barrier.
+// The loads are issued with inline asm: the compiler cannot tell the LDS writes of a
+// global_load_lds builtin from the V reads of the same iteration and would otherwise
+// wait for every outstanding load before the first V read; ordering is enforced here
+// by the explicit wait + barrier of step 4 instead.
+// ---------------------------------------------------------------------------
+template <int D>
+FMLM_DEV int kv_swz(int r) {
+  if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else if constexpr (D == 64) return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+  else if constexpr (D == 32) return (r >> 2) & 3;
+  else return (r >> 3) & 1;
+}
+
+// NaN-propagating max (v_maximum3_f32): no operand canonicalisation, unlike fmaxf
+FMLM_DEV float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// max over lanes l, l^16, l^32, l^48: permlane16/32_swap(x, x) return {x[l], x[l^16]}
+// resp. {x[l], x[l^32]} in some order
+FMLM_DEV float lane_max_xor16_32(float x) {
+  const int xi = __builtin_bit_cast(int, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+  x = vmax(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
+  const int yi = __builtin_bit_cast(int, x);
+  const auto b = __builtin_amdgcn_permlane32_swap(yi, yi, false, false);
+  return vmax(__builtin_bit_cast(float, (int)b[0]), __builtin_bit_cast(float, (int)b[1]));
+}
+
+// An empty asm that claims to rewrite x: arithmetic producing x stays before this point
+// and arithmetic consuming it stays after, in the order of the surrounding side effects.
+template <typename X>
+FMLM_DEV void pin(X& x) { asm volatile("" : "+v"(x)); }
+
+FMLM_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const FMLM_LDS char*)p;
+}
+
+FMLM_DEV const char* uniform_ptr(const char* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const char*)(((uint64_t)hi << 32) | lo);
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 64 lanes x 16 bytes from base + off (per lane) to LDS [lds, lds + 1024), lane l at
+// lds + 16 l.  base and lds are wave-uniform.
+FMLM_DEV void dma16_sbase(const char* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+constexpr int kLdsLead = 3;  // LDS reads issued before the first MFMA of a step
+
+template <typename T>
+struct Pair;
+template <>
+struct Pair<bf16> {
+  typedef __bf16 type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct Pair<f16> {
+  typedef _Float16 type __attribute__((ext_vector_type(2)));
+};
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T, int D, int QB, int NW, int BK>
+struct Mfma3Cfg {
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = NW * QB * 16;
+  static constexpr int ROWB = D * 2;          // bytes per K / V row (unpadded)
+  static constexpr int TILEB = BK * ROWB;
+  static constexpr int CPR = D / 8;           // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;        // rows per wave-wide direct load
+  static constexpr int NINST = BK / RPI;      // wave-wide loads per tile per tensor
+  static constexpr int NPW = (NINST + NW - 1) / NW;  // ... per wave
+  static constexpr int LDS_BYTES = 4 * TILEB;  // K[2], V[2]
+  static constexpr int KC = (D + 31) / 32;
+  static constexpr int NDB = D / 16;
+  static constexpr int NKB = BK / 16;
+  static constexpr int NKS = BK / 32;
+  static constexpr int NKF = KC * NKB;    // K fragment reads per step
+  static constexpr int NVF = NKS * NDB;   // V fragment (tr16 pair) reads per step
+  static_assert(D % 16 == 0 && D >= 16 && D <= 256, "head dim");
+  static_assert(BK % 32 == 0 && BK % RPI == 0, "key tile");
+};
+
+template <typename T, int D, int QB, int NW, int BK>
+__global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
+    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
+  typedef Mfma3Cfg<T, D, QB, NW, BK> C;
+  typedef typename Mfma<T>::v8 v8;
+  extern __shared__ __align__(16) char smem_raw[];
+  char* const kbuf = smem_raw;                   // [2][TILEB]
+  char* const vbuf = smem_raw + 2 * C::TILEB;    // [2][TILEB]
+
+  WorkItem w;
+  if (!resolve_work(p, units, n_units, C::BQ, w)) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int32_t* cu = p.cu_seqlens_q;
+  const int B = p.B;
+  // ---- Q fragments (B operand of S^T): lane (q + 16g), block qb, step kc, pre-scaled by
+  // scale*log2(e) (one rounding to the input type) so that S comes out of the MFMAs in
+  // log2 units
+  const float cs = p.scale * kLog2e;
+  v8 qf[QB][C::KC];
+  {
+    const char* qbase = (const char*)p.q;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int row = (wave * QB + qb) * 16 + l16;
+      const bool ok = row < w.qcount;
+      const int64_t off = w.q_row0 + (int64_t)row * w.q_sn;
+#pragma unroll
+      for (int kc = 0; kc < C::KC; ++kc) {
+        const int col = kc * 32 + g * 8;
+        v8 raw = v8{};
+        if (ok && col < D) raw = *(const v8*)(qbase + (off + col) * 2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) raw[e] = (T)((float)raw[e] * cs);
+        qf[qb][kc] = raw;
+      }
+    }
+  }
+
+  // ---- per-lane LDS byte offsets (see kv_swz): the K fragment of block kb, step kc is
+  // at kb*16*ROWB + 256*(kc/4) + koff[kc%4]; the V tr16 fragment of step ks, column
+  // block db, half h is at (32 ks + 16 h)*ROWB + 256*(db/8) + voff[db%8]
+  int koff[4], voff[8];
+  {
+    const int ksw = kv_swz<D>(l16);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) koff[b] = l16 * C::ROWB + 16 * ((4 * b + g) ^ ksw);
+    const int vr = 4 * g + (l16 >> 2);
+    const int vsw = kv_swz<D>(vr);
+    const int x = (l16 & 3) >> 1;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) voff[db] = vr * C::ROWB + 16 * ((2 * db + x) ^ vsw) + 8 * (l16 & 1);
+  }
+  // ---- per-lane direct-load layout: wave-wide load i = wave + j*NW brings rows
+  // [i*RPI, (i+1)*RPI); lane l fetches logical chunk (l % CPR) ^ kv_swz(row) of row
+  // i*RPI + l/CPR, which lands in physical chunk l % CPR
+  const int drow0 = wave * C::RPI + lane / C::CPR;  // + j*NW*RPI for load j
+
+  f32x4 o[C::NDB][QB];
+  f32x4 lsum[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    lsum[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // m_i: running row maximum (log2 units); sbase: the maximum the current S tile was
+  // computed against (its accumulators start at -sb)
+  float m_i[QB], sbase[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_i[qb] = -INFINITY;
+    sbase[qb] = 0.f;
+  }
+
+  const int nt0 = (w.seg[0].n + BK - 1) / BK;
+  const int nt1 = (w.seg[1].n + BK - 1) / BK;
+  const int ntiles = nt0 + nt1;
+
+  // Fetch K (is_v false) or V of tile t into LDS dst.  Rows past the segment end repeat
+  // its last row (their scores are masked to -inf, so P = 0 multiplies finite values).
+  // Segments here are linear (no per-row sequence lookup; the dispatcher guarantees it).
+  auto fetch = [&](int t, char* dst, bool is_v) {
+    const KvSeg& s = t < nt0 ? w.seg[0] : w.seg[1];
+    const int j0 = (t < nt0 ? t : t - nt0) * BK;
+    const int last = s.n - 1 - j0;
+    const uint32_t lds0 = lds_addr(dst);
+    const int64_t sn = is_v ? s.vsn : s.ksn;
+    const char* base = uniform_ptr((is_v ? s.v : s.k) + ((is_v ? s.vbase : s.kbase) + (int64_t)j0 * sn) * 2);
+    const uint32_t rowb = (uint32_t)sn * 2u;
+#pragma unroll
+    for (int j = 0; j < C::NPW; ++j) {
+      const int i = wave + j * NW;
+      const int row = drow0 + j * NW * C::RPI;
+      const int col = 16 * ((lane % C::CPR) ^ kv_swz<D>(row));
+      if (C::NINST % NW == 0 || i < C::NINST)
+        dma16_sbase(base, (uint32_t)min(row, last) * rowb + col,
+                    __builtin_amdgcn_readfirstlane(lds0 + i * 1024));
+    }
+  };
+  auto tile_keys = [&](int t) {
+    return t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
+  };
+  // S^T = K Q^T from the K tile at kt (prologue only; the steps interleave it)
+  auto qk = [&](const char* kt, f32x4 (&s)[C::NKB][QB]) {
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc) {
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb) {
+        v8 a;
+        if (kc * 32 + g * 8 < D)
+          a = *(const v8*)(kt + kb * 16 * C::ROWB + 256 * (kc >> 2) + koff[kc & 3]);
+        else
+          a = v8{};
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          s[kb][qb] = Mfma<T>::run(a, qf[qb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[kb][qb]);
+      }
+    }
+  };
+  v8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
+  pin(ones);  // keep in registers rather than rematerialised per use
+
+  // One pipeline step: sc holds S(t); computes sn = S(t+1) from kn, consumes V(t) at vt,
+  // refills kdst with K(t+2) and vdst with V(t+1).
+  // raw row maxima of a score tile (before the scale); rows past a segment end repeat
+  // its last valid row, so they never change a maximum
+  auto row_max = [&](const f32x4 (&sx)[C::NKB][QB], float (&mx)[QB]) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float m = vmax(vmax(sx[0][qb][0], sx[0][qb][1]), vmax(sx[0][qb][2], sx[0][qb][3]));
+#pragma unroll
+      for (int kb = 1; kb < C::NKB; ++kb)
+        m = vmax(vmax(m, vmax(sx[kb][qb][0], sx[kb][qb][1])), vmax(sx[kb][qb][2], sx[kb][qb][3]));
+      mx[qb] = lane_max_xor16_32(m);
+    }
+  };
+
+  // One pipeline step: sc holds S(t) and mx its row maxima; computes sn = S(t+1) from kn
+  // and its maxima, consumes V(t) at vt, refills kdst with K(t+2) and vdst with V(t+1).
+  auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
+                  const char* kn, const char* vt, char* kdst, char* vdst) {
+    if (t + 2 < ntiles) fetch(t + 2, kdst, false);
+    if (t + 1 < ntiles) fetch(t + 1, vdst, true);
+
+    bool need_rescale = false;
+    float m_new[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float m = mx[qb] + sbase[qb];
+      const bool grow = m > m_i[qb] + kRescaleSlack;
+      m_new[qb] = grow ? m : m_i[qb];
+      need_rescale = need_rescale || grow;
+    }
+    if (__builtin_amdgcn_ballot_w64(need_rescale)) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const float alpha = fast_exp2(m_i[qb] - m_new[qb]);  // 1 where unchanged, 0 on the first tile
+        const float shift = sbase[qb] - m_new[qb];               // 0 where unchanged
+        m_i[qb] = m_new[qb];
+        lsum[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) o[db][qb] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < C::NKB; ++kb) sc[kb][qb] += shift;
+      }
+    }
+    const int nk = tile_keys(t);
+    if (nk < BK) {
+      const int lim = nk - 4 * g;  // key kb*16 + 4g + r is valid iff kb*16 + r < lim
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kb * 16 + r >= lim)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) sc[kb][qb][r] = -INFINITY;
+    }
+
+    // ---- one basic block from here to the barrier, written as a sequence of slots
+    // fenced by sched_barrier so the order below is the issue order.  Slot s runs the
+    // MFMAs of operand fragment s: fragments [0, NKF) are K(t+1) fragments (S(t+1),
+    // beside a share of the exp work of P(t)), fragments [NKF, NKF+NVF) are V(t)
+    // fragments (O += V^T P, beside a share of the row-max work of S(t+1)).  The LDS
+    // read of fragment s + kLdsLead is issued at the top of slot s.
+    constexpr int NF = C::NKF + C::NVF;
+    f32x4 minit[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) minit[qb] = f32x4{-m_i[qb], -m_i[qb], -m_i[qb], -m_i[qb]};
+    constexpr int NP = C::NKB * QB * 2;    // exp pairs
+    constexpr int NMS = C::NKB * QB + QB;  // row-max steps
+    v8 fr[kLdsLead + 1];
+    u32x4 pf[C::NKS][QB];  // P(t) as packed pairs, the B operand of P V
+    float mpart[QB];
+    auto issue = [&](int r) {
+      if (r < C::NKF) {
+        const int kc = r / C::NKB, kb = r % C::NKB;
+        fr[r % (kLdsLead + 1)] = kc * 32 + g * 8 < D
+            ? *(const v8*)(kn + kb * 16 * C::ROWB + 256 * (kc >> 2) + koff[kc & 3]) : v8{};
+      } else {
+        const int j = r - C::NKF, ks = j / C::NDB, db = j % C::NDB;
+        const char* va = vt + ks * 32 * C::ROWB + 256 * (db >> 3) + voff[db & 7];
+        const s16x4 lo = lds_read_tr16(va);
+        const s16x4 hi = lds_read_tr16(va + 16 * C::ROWB);
+        fr[r % (kLdsLead + 1)] = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    // exp of S^T elements (kb, r), (kb, r+1) of block qb; keys kb*16 + 4g + r (+1) are
+    // elements (kb&1)*4 + r (+1) of the P fragment of key step kb/2.  pin() keeps the
+    // work inside its slot (pure arithmetic would otherwise be moved to its first use).
+    auto exp_pair = [&](int pi) {
+      const int qb = pi / (C::NKB * 2), kb = (pi >> 1) % C::NKB, r = (pi & 1) * 2;
+      f32x2 x = f32x2{sc[kb][qb][r], sc[kb][qb][r + 1]};
+      pin(x);
+      x[0] = fast_exp2(x[0]);
+      x[1] = fast_exp2(x[1]);
+      uint32_t wv = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
+      pin(wv);
+      pf[kb >> 1][qb][(kb & 1) * 2 + (pi & 1)] = wv;
+    };
+    auto max_step = [&](int k) {
+      if (k < C::NKB * QB) {
+        const int qb = k / C::NKB, kb = k % C::NKB;
+        f32x4 x = sn[kb][qb];
+        pin(x);
+        const float m4 = vmax(vmax(x[0], x[1]), vmax(x[2], x[3]));
+        mpart[qb] = kb == 0 ? m4 : vmax(mpart[qb], m4);
+        pin(mpart[qb]);
+      } else {
+        const int qb = k - C::NKB * QB;
+        mx[qb] = lane_max_xor16_32(mpart[qb]);
+        pin(mx[qb]);
+      }
+    };
+#pragma unroll
+    for (int r = 0; r < kLdsLead; ++r) issue(r);
+#pragma unroll
+    for (int sl = 0; sl < NF; ++sl) {
+      if (sl + kLdsLead < NF) issue(sl + kLdsLead);
+      const v8 a = fr[sl % (kLdsLead + 1)];
+      if (sl < C::NKF) {
+        const int kc = sl / C::NKB, kb = sl % C::NKB;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          sn[kb][qb] = Mfma<T>::run(a, qf[qb][kc], kc == 0 ? minit[qb] : sn[kb][qb]);
+#pragma unroll
+        for (int pi = sl * NP / C::NKF; pi < (sl + 1) * NP / C::NKF; ++pi) exp_pair(pi);
+      } else {
+        const int j = sl - C::NKF, ks = j / C::NDB, db = j % C::NDB;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          o[db][qb] = Mfma<T>::run(a, __builtin_bit_cast(v8, pf[ks][qb]), o[db][qb]);
+        if (db == C::NDB - 1)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            lsum[qb] = Mfma<T>::run(ones, __builtin_bit_cast(v8, pf[ks][qb]), lsum[qb]);
+#pragma unroll
+        for (int k = j * NMS / C::NVF; k < (j + 1) * NMS / C::NVF; ++k) max_step(k);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) sbase[qb] = m_i[qb];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  };
+
+  f32x4 sa[C::NKB][QB], sb[C::NKB][QB];
+  float mx[QB];
+  if (ntiles > 0) {
+    fetch(0, kbuf, false);
+    fetch(0, vbuf, true);
+    if (ntiles > 1) fetch(1, kbuf + C::TILEB, false);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    qk(kbuf, sa);
+    row_max(sa, mx);
+    __syncthreads();  // every wave is done with K(0): its buffer may be refilled
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    const int cur = (t & 1) * C::TILEB, nxt = C::TILEB - cur;
+    step(t, sa, sb, mx, kbuf + nxt, vbuf + cur, kbuf + cur, vbuf + nxt);
+#pragma unroll
+    for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) sa[kb][qb] = sb[kb][qb];
+  }
+
+  // ---- epilogue: O /= l (l == 0 -> 1), store valid rows
+  char* obase = (char*)p.o;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l = lsum[qb][0];
     const float inv = l > 0.f ? 1.f / l : 1.f;
     const int row = (wave * QB + qb) * 16 + l16;
     if (row >= w.qcount) continue;
@@ -916,29 +1329,44 @@ static Launch simt_launch() {
   return Launch{C::RPW, C::NT, C::LDS_BYTES, (const void*)&attn_simt_kernel<T, D>};
 }
 
+template <typename T, int D, int QB, int NW, int BK>
+static Launch mfma3_launch() {
+  typedef Mfma3Cfg<T, D, QB, NW, BK> C;
+  return Launch{C::BQ, C::NT, C::LDS_BYTES, (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK>};
+}
+
 template <typename T>
 static Launch mla512_launch() {
   return Launch{MlaCfg::BQ, MlaCfg::NT, MlaCfg::LDS_BYTES, (const void*)&attn_mla512_kernel<T>};
 }
 
-// MFMA kernels by head dim; the 512-wide latent kernel needs K = V (MLA) and linear
-// main-key addressing (no per-row sequence lookup).
+// MFMA kernels by head dim.  The pipelined kernel and the 512-wide latent kernel need
+// linear main-key addressing; causal_query_seq_attn over padded K/V (a per-row sequence
+// lookup) takes the register-staged kernel.  The latent kernel also needs K = V (MLA).
 template <typename T>
 static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
+  const bool lookup = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q &&
+                      p.kv_layout != FMLM_LAYOUT_PACKED;
+  if (lookup) {
+    switch (p.D) {
+      case 16: L = mfma_launch<T, 16, 2, 4, 64>(); return true;
+      case 32: L = mfma_launch<T, 32, 2, 4, 64>(); return true;
+      case 64: L = mfma_launch<T, 64, 2, 4, 64>(); return true;
+      case 128: L = mfma_launch<T, 128, 2, 4, 64>(); return true;
+      case 256: L = mfma_launch<T, 256, 1, 4, 64>(); return true;
+      default: return false;
+    }
+  }
   switch (p.D) {
-    case 16: L = mfma_launch<T, 16, 2, 4, 64>(); return true;
-    case 32: L = mfma_launch<T, 32, 2, 4, 64>(); return true;
-    case 64: L = mfma_launch<T, 64, 2, 4, 64>(); return true;
-    case 128: L = mfma_launch<T, 128, 2, 4, 64>(); return true;
-    case 256: L = mfma_launch<T, 256, 1, 4, 64>(); return true;
-    case 512: {
-      const bool mla = p.flags & FMLM_FLAG_MLA;
-      const bool lookup = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q &&
-                          p.kv_layout != FMLM_LAYOUT_PACKED;
-      if (!mla || lookup) return false;
+    case 16: L = mfma3_launch<T, 16, 2, 4, 64>(); return true;
+    case 32: L = mfma3_launch<T, 32, 2, 4, 64>(); return true;
+    case 64: L = mfma3_launch<T, 64, 2, 4, 64>(); return true;
+    case 128: L = mfma3_launch<T, 128, 2, 4, 64>(); return true;
+    case 256: L = mfma3_launch<T, 256, 1, 4, 64>(); return true;
+    case 512:
+      if (!(p.flags & FMLM_FLAG_MLA)) return false;
       L = mla512_launch<T>();
       return true;
-    }
     default: return false;
   }
 }
