@@ -632,6 +632,13 @@ struct Pair<f16> {
 };
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+// walks the key tiles of a work item for the direct loads (see attn_mfma3_kernel)
+struct KeyCursor {
+  const char* p;
+  uint32_t rowb;
+  int left, seg;
+};
+
 template <typename T, int D, int QB, int NW, int BK>
 struct Mfma3Cfg {
   static constexpr int NT = NW * 64;
@@ -731,31 +738,48 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     m_i[qb] = -INFINITY;
     sbase[qb] = 0.f;
   }
+  const bool wave_active = wave * QB * 16 < w.qcount;
+  KeyCursor kcur, vcur;
 
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
   const int ntiles = nt0 + nt1;
 
-  // Fetch K (is_v false) or V of tile t into LDS dst.  Rows past the segment end repeat
-  // its last row (their scores are masked to -inf, so P = 0 multiplies finite values).
-  // Segments here are linear (no per-row sequence lookup; the dispatcher guarantees it).
-  auto fetch = [&](int t, char* dst, bool is_v) {
-    const KvSeg& s = t < nt0 ? w.seg[0] : w.seg[1];
-    const int j0 = (t < nt0 ? t : t - nt0) * BK;
-    const int last = s.n - 1 - j0;
+  // ---- direct loads.  A cursor walks the key tiles of the context then the main segment
+  // (linear addressing: the dispatcher routes per-row lookups elsewhere): p is the
+  // wave-uniform byte address of the current tile's row 0, left the keys left in the
+  // segment from there.  Rows past a segment end repeat its last row (their scores are
+  // masked to -inf, so P = 0 multiplies finite values).
+  typedef KeyCursor Cursor;
+  auto lane_offsets = [&](uint32_t rowb, int last, uint32_t (&ofs)[C::NPW]) {
+#pragma unroll
+    for (int j = 0; j < C::NPW; ++j) {
+      const int row = drow0 + j * NW * C::RPI;
+      ofs[j] = (uint32_t)min(row, last) * rowb + 16 * ((lane % C::CPR) ^ kv_swz<D>(row));
+    }
+  };
+  auto cursor_seg = [&](Cursor& cr, int sg, bool is_v) {
+    const KvSeg& sgm = w.seg[sg];
+    cr.seg = sg;
+    cr.left = __builtin_amdgcn_readfirstlane(sgm.n);
+    cr.rowb = __builtin_amdgcn_readfirstlane((uint32_t)(is_v ? sgm.vsn : sgm.ksn) * 2u);
+    cr.p = uniform_ptr((is_v ? sgm.v : sgm.k) + (is_v ? sgm.vbase : sgm.kbase) * 2);
+  };
+  auto cursor_init = [&](Cursor& cr, bool is_v) { cursor_seg(cr, w.seg[0].n > 0 ? 0 : 1, is_v); };
+  // load the cursor's tile into LDS dst and advance to the next tile
+  auto fetch = [&](Cursor& cr, char* dst, bool is_v) {
     const uint32_t lds0 = lds_addr(dst);
-    const int64_t sn = is_v ? s.vsn : s.ksn;
-    const char* base = uniform_ptr((is_v ? s.v : s.k) + ((is_v ? s.vbase : s.kbase) + (int64_t)j0 * sn) * 2);
-    const uint32_t rowb = (uint32_t)sn * 2u;
+    uint32_t ofs[C::NPW];
+    lane_offsets(cr.rowb, cr.left - 1, ofs);
 #pragma unroll
     for (int j = 0; j < C::NPW; ++j) {
       const int i = wave + j * NW;
-      const int row = drow0 + j * NW * C::RPI;
-      const int col = 16 * ((lane % C::CPR) ^ kv_swz<D>(row));
       if (C::NINST % NW == 0 || i < C::NINST)
-        dma16_sbase(base, (uint32_t)min(row, last) * rowb + col,
-                    __builtin_amdgcn_readfirstlane(lds0 + i * 1024));
+        dma16_sbase(uniform_ptr(cr.p), ofs[j], __builtin_amdgcn_readfirstlane(lds0 + i * 1024));
     }
+    cr.left -= BK;
+    cr.p += (size_t)BK * cr.rowb;
+    if (cr.left <= 0 && cr.seg == 0 && w.seg[1].n > 0) cursor_seg(cr, 1, is_v);
   };
   auto tile_keys = [&](int t) {
     return t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
@@ -801,8 +825,13 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   // and its maxima, consumes V(t) at vt, refills kdst with K(t+2) and vdst with V(t+1).
   auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
                   const char* kn, const char* vt, char* kdst, char* vdst) {
-    if (t + 2 < ntiles) fetch(t + 2, kdst, false);
-    if (t + 1 < ntiles) fetch(t + 1, vdst, true);
+    if (t + 2 < ntiles) fetch(kcur, kdst, false);
+    if (t + 1 < ntiles) fetch(vcur, vdst, true);
+    if (!wave_active) {  // every query row of this wave is padding: loads and barriers only
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      return;
+    }
 
     bool need_rescale = false;
     float m_new[QB];
@@ -845,7 +874,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     // fragments (O += V^T P, beside a share of the row-max work of S(t+1)).  The LDS
     // read of fragment s + kLdsLead is issued at the top of slot s.
     constexpr int NF = C::NKF + C::NVF;
-    f32x4 minit[QB];
+    f32x4 minit[QB];  // -m_i splat: the initial S accumulators
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) minit[qb] = f32x4{-m_i[qb], -m_i[qb], -m_i[qb], -m_i[qb]};
     constexpr int NP = C::NKB * QB * 2;    // exp pairs
@@ -871,8 +900,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     // work inside its slot (pure arithmetic would otherwise be moved to its first use).
     auto exp_pair = [&](int pi) {
       const int qb = pi / (C::NKB * 2), kb = (pi >> 1) % C::NKB, r = (pi & 1) * 2;
+      if (r == 0) pin(sc[kb][qb]);
       f32x2 x = f32x2{sc[kb][qb][r], sc[kb][qb][r + 1]};
-      pin(x);
       x[0] = fast_exp2(x[0]);
       x[1] = fast_exp2(x[1]);
       uint32_t wv = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
@@ -882,8 +911,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     auto max_step = [&](int k) {
       if (k < C::NKB * QB) {
         const int qb = k / C::NKB, kb = k % C::NKB;
-        f32x4 x = sn[kb][qb];
-        pin(x);
+        pin(sn[kb][qb]);
+        const f32x4 x = sn[kb][qb];
         const float m4 = vmax(vmax(x[0], x[1]), vmax(x[2], x[3]));
         mpart[qb] = kb == 0 ? m4 : vmax(mpart[qb], m4);
         pin(mpart[qb]);
@@ -929,13 +958,17 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   f32x4 sa[C::NKB][QB], sb[C::NKB][QB];
   float mx[QB];
   if (ntiles > 0) {
-    fetch(0, kbuf, false);
-    fetch(0, vbuf, true);
-    if (ntiles > 1) fetch(1, kbuf + C::TILEB, false);
+    cursor_init(kcur, false);
+    cursor_init(vcur, true);
+    fetch(kcur, kbuf, false);
+    fetch(vcur, vbuf, true);
+    if (ntiles > 1) fetch(kcur, kbuf + C::TILEB, false);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    qk(kbuf, sa);
-    row_max(sa, mx);
+    if (wave_active) {
+      qk(kbuf, sa);
+      row_max(sa, mx);
+    }
     __syncthreads();  // every wave is done with K(0): its buffer may be refilled
   }
   for (int t = 0; t < ntiles; ++t) {
