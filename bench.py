@@ -10,8 +10,11 @@ full-batch cached context) that is flash_attn_mlm_compressed + unpack_from_kerne
 Prints one JSON line: effective attention TFLOP/s (padding excluded, formula
 4*H*D*sum_b Lq_b*(Lctx_b + Lmain_b)), ms per step, the attention kernel's roofline
 fraction against the MI355X dense fp16/bf16 MFMA peak (kernel time from HIP events
-around back-to-back launches on its stream), and the reference's per-sequence
-PyTorch SDPA path timed on this host's CPU cores as a reported baseline.
+around back-to-back launches on its stream), the kernel's HBM bytes per launch from two
+rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE) run as child processes before this
+process touches the GPU, each scaled by the counter's reading for a 256 MiB copy, and
+the reference's per-sequence PyTorch SDPA path timed on this host's CPU cores as a
+reported baseline.
 
 The configs (BASELINE.json "configs") are built by `make_case`, which the GPU tests
 reuse for parity checks.
@@ -237,6 +240,68 @@ def _kernel_ms(attention, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+COPY_KIB = (256 << 20) / 1024  # the --profile driver's calibration copy
+
+
+def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s: float) -> dict:
+    """One `rocprofv3 --pmc <counter>` run of this script's --profile driver in a child
+    process.  Returns {"attn": mean KiB per attention dispatch, "copy": KiB of the
+    256 MiB calibration copy}."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        raise RuntimeError("rocprofv3 not on PATH")
+    out = Path(tempfile.mkdtemp(prefix="fmlm_pmc_", dir="/tmp"))
+    cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(out), "-o", "pmc", "--",
+           sys.executable, str(REPO / "bench.py"), "--config", str(cfg), "--profile",
+           "--steps", str(launches)]
+    if variant:
+        cmd += ["--variant", variant]
+    env = dict(os.environ, TMPDIR="/tmp")
+    try:
+        # rocprofv3 may exit non-zero after writing complete results; the CSV decides
+        subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, stdout=subprocess.DEVNULL,
+                       stderr=subprocess.DEVNULL, check=False)
+        files = list(out.rglob("*counter_collection.csv"))
+        if not files:
+            raise RuntimeError(f"rocprofv3 --pmc {counter} wrote no counter file")
+        attn, copies = [], []
+        for f in files:
+            with open(f, newline="") as fh:
+                for row in csv.DictReader(fh):
+                    if row["Counter_Name"] != counter:
+                        continue
+                    name, v = row["Kernel_Name"], float(row["Counter_Value"])
+                    if "attn_" in name and "schedule" not in name:
+                        attn.append(v)
+                    elif "copyBuffer" in name:
+                        copies.append(v)
+        if len(attn) < launches or not copies:
+            raise RuntimeError(f"rocprofv3 --pmc {counter}: {len(attn)} attention dispatches, "
+                               f"{len(copies)} copies")
+        return {"attn": sum(attn[-launches:]) / launches, "copy": max(copies)}
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+def hbm_traffic(cfg: int, variant: str, launches: int = 3, timeout_s: float = 120.0) -> dict:
+    """HBM bytes per attention launch from two counter passes (FETCH_SIZE, WRITE_SIZE),
+    each scaled by what the same counter reads for a copy of known size (256 MiB read +
+    256 MiB written) in the same run."""
+    f = _counter_pass("FETCH_SIZE", cfg, variant, launches, timeout_s)
+    w = _counter_pass("WRITE_SIZE", cfg, variant, launches, timeout_s)
+    ff, fw = COPY_KIB / f["copy"], COPY_KIB / w["copy"]
+    return {
+        "bytes": 1024.0 * (f["attn"] * ff + w["attn"] * fw),
+        "fetch_kib": f["attn"], "write_kib": w["attn"],
+        "fetch_scale": round(ff, 4), "write_scale": round(fw, 4),
+    }
+
+
 def cpu_baseline(case: Case, budget_s: float = 20.0) -> dict:
     """The reference's per-sequence PyTorch SDPA path (oracle/cpu_baseline.py) on this
     host's CPU cores, fp32, over a bounded prefix of the workload's sequences."""
@@ -255,6 +320,8 @@ def main() -> None:
     ap.add_argument("--variant", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes that measure HBM traffic")
     ap.add_argument(
         "--profile",
         action="store_true",
@@ -270,6 +337,16 @@ def main() -> None:
             file=sys.stderr,
         )
         sys.exit(2)
+    # counter passes run as child processes before this process touches the GPU
+    traffic, traffic_note = None, None
+    if not args.profile and not args.no_traffic:
+        try:
+            traffic = hbm_traffic(args.config, args.variant)
+            print(f"[bench] HBM traffic per launch: {traffic}", file=sys.stderr, flush=True)
+        except Exception as e:  # counters unavailable: report null, say why
+            traffic_note = f"counter passes failed: {e}"
+            print(f"[bench] {traffic_note}", file=sys.stderr, flush=True)
+
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
@@ -306,10 +383,16 @@ def main() -> None:
         "peak": peak,
         "unit": "TFLOP/s",
         "frac": round(k_tflops / peak, 5),
-        "traffic": None,
+        "traffic": None if traffic is None else round(traffic["bytes"]),
         "kernel_ms": round(kms, 5),
         "algorithmic_bytes": case.attention_bytes,
     }
+    if traffic is not None:
+        roofline["traffic_detail"] = {k: v for k, v in traffic.items() if k != "bytes"}
+        roofline["traffic_over_algorithmic"] = round(traffic["bytes"] / case.attention_bytes, 3)
+        roofline["hbm_gbs"] = round(traffic["bytes"] / (kms * 1e-3) / 1e9, 1)
+    elif traffic_note:
+        roofline["traffic_note"] = traffic_note
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(case)
