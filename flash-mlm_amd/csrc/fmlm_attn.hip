@@ -924,9 +924,13 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     };
 #pragma unroll
     for (int r = 0; r < kLdsLead; ++r) issue(r);
+    // wave priority: a wave in its MFMA-dense block issues ahead of the other waves on its
+    // SIMD (their loads, branches and softmax VALU fill the gaps), the P V phase highest
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int sl = 0; sl < NF; ++sl) {
       if (sl + kLdsLead < NF) issue(sl + kLdsLead);
+      if (sl == C::NKF) __builtin_amdgcn_s_setprio(2);
       const v8 a = fr[sl % (kLdsLead + 1)];
       if (sl < C::NKF) {
         const int kc = sl / C::NKB, kb = sl % C::NKB;
@@ -949,6 +953,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) sbase[qb] = m_i[qb];
     __builtin_amdgcn_s_waitcnt(0);
