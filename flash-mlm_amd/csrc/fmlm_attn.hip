@@ -1126,7 +1126,9 @@ __global__ __launch_bounds__(MlaCfg::NT, 1) void attn_mla512_kernel(const fmlm_a
     if (t + 1 < ntiles) fetch(t + 1, st ^ 1);
     const int nk = t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
 
-    // ---- S^T for keys [16 sl, 16 sl + 16) x 32 rows
+    // ---- S^T for keys [16 sl, 16 sl + 16) x 32 rows (MFMA phases run at raised wave
+    // priority so the other waves' exchanges and softmax fill the gaps)
+    __builtin_amdgcn_s_setprio(1);
     f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int a = 0; a < D / 128; ++a) {
@@ -1138,6 +1140,7 @@ __global__ __launch_bounds__(MlaCfg::NT, 1) void attn_mla512_kernel(const fmlm_a
         s[1] = Mfma<T>::run(kf, qf[1][kc], s[1]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if (nk < BK) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -1195,6 +1198,7 @@ __global__ __launch_bounds__(MlaCfg::NT, 1) void attn_mla512_kernel(const fmlm_a
     // ---- O^T[128 sl + 16 db + i][row] += V^T P^T over the 64 keys; key order within a
     // 32-key step: lane group g owns keys 8g..8g+7 (P: one b128 read, V: two tr16 reads,
     // rows 8g + j/4 and 8g + 4 + j/4, the second at voff[db ^ 4] + 4 rows)
+    __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       v8 pb[2];
@@ -1211,6 +1215,7 @@ __global__ __launch_bounds__(MlaCfg::NT, 1) void attn_mla512_kernel(const fmlm_a
         o[db][1] = Mfma<T>::run(a, pb[1], o[db][1]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_s_waitcnt(0);  // next stage landed
     __syncthreads();                // this stage, P and the max slots are free
   }
