@@ -13,9 +13,10 @@ fraction against the MI355X dense fp16/bf16 MFMA peak (kernel time: median of HI
 timings on its launch stream, L2/MALL flushed before each launch), the kernel's HBM bytes
 per launch from two
 rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE) run as child processes before this
-process touches the GPU, each scaled by the counter's reading for a 256 MiB copy, and
-the reference's per-sequence PyTorch SDPA path timed on this host's CPU cores as a
-reported baseline.
+process touches the GPU, each scaled by the counter's reading for a 256 MiB copy, the
+HBM rate of the pack and unpack kernels on the same tensors ("hbm_kernels"), and the
+reference's per-sequence PyTorch SDPA path timed on this host's CPU cores as a reported
+baseline.
 
 The configs (BASELINE.json "configs") are built by `make_case`, which the GPU tests
 reuse for parity checks.
@@ -311,6 +312,61 @@ def hbm_traffic(cfg: int, variant: str, launches: int = 3, timeout_s: float = 12
     }
 
 
+def _event_ms(fn, reps: int) -> float:
+    """Median duration of fn() from HIP events on the current stream, L2/MALL flushed
+    (512 MiB write) before each call."""
+    stream = torch.cuda.current_stream()
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        fn()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in events:
+        flush.fill_(0)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    times = sorted(e0.elapsed_time(e1) for e0, e1 in events)
+    return times[len(times) // 2]
+
+
+def hbm_kernels(case: Case, reps: int = 30) -> dict:
+    """HBM rate of the path's copy kernels on this workload's tensors: unpack_from_kernel
+    (read H*T*D, write B*H*N*D) and pack_and_pad_main_tensors_for_mlm_compressed (per
+    tensor: read heads*T*D, write heads*T_pad*D; MLA packs q and one latent head).
+    Algorithmic bytes / median time, against the 8 TB/s HBM peak."""
+    import flash_mlm as fm
+    from flash_mlm.host import host_utils as hu
+
+    t = case.tensors
+    if "meta" not in t:
+        return {}
+    meta = t["meta"]
+    esz = torch.finfo(case.dtype).bits // 8
+    B, H, N, D = (int(x) for x in t["q"].shape)
+    T = int(meta.total_tokens)
+    out = {}
+
+    packed = torch.randn((H * T, D), device="cuda").to(case.dtype)
+    ms = _event_ms(lambda: fm.unpack_from_kernel(packed, meta, H), reps)
+    nbytes = esz * D * (H * T + B * H * N)
+    out["unpack"] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                     "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+
+    pc = fm.PackingCache()
+    pack = lambda: hu.pack_and_pad_main_tensors_for_mlm_compressed(  # noqa: E731
+        t["q"], t["k"], t["v"], q_meta=meta, num_heads=H, is_mla=case.is_mla, block_m=64,
+        block_n=int(case.config.get("block_n", 64)), packing_cache=pc)
+    T_pad = pack()[3]
+    ms = _event_ms(pack, reps)
+    heads = H + (1 if case.is_mla else 2 * H)
+    nbytes = esz * D * heads * (T + T_pad)
+    out["pack"] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                   "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                   "tensors": "q + latent head" if case.is_mla else "q, k, v"}
+    return out
+
+
 def cpu_baseline(case: Case, budget_s: float = 20.0) -> dict:
     """The reference's per-sequence PyTorch SDPA path (oracle/cpu_baseline.py) on this
     host's CPU cores, fp32, over a bounded prefix of the workload's sequences."""
@@ -406,6 +462,9 @@ def main() -> None:
         roofline["hbm_gbs"] = round(traffic["bytes"] / (kms * 1e-3) / 1e9, 1)
     elif traffic_note:
         roofline["traffic_note"] = traffic_note
+    hbm = hbm_kernels(case)
+    if hbm:
+        print(f"[bench] copy kernels: {hbm}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(case)
@@ -429,6 +488,7 @@ def main() -> None:
                    "reference_formula_gflop": round(case.flops_reference_formula / 1e9, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "hbm_kernels": hbm or None,
     }
     print(json.dumps(line), flush=True)
 

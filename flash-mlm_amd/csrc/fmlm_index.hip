@@ -165,42 +165,54 @@ struct PackArgs {
   fmlm_pack_tensor t[3];
 };
 
+// ---------------------------------------------------------------------------
+// Pack: block (TX chunk lanes x TY rows) over grid (row block, tensor*heads, sequence),
+// so the sequence and head come from the block index and no thread divides or searches.
+// Sequence b's rows p < min(L_b, N) go to dst row h*T_pad + cu[b] + p (rows outside
+// [0, T) are skipped); the last grid slice (z = B) zero-fills the rows of [0, T_pad) not
+// covered by [cu[0], cu[B]) (the packed tail [T, T_pad) for consistent metadata).
+// Without cu_seqlens, sequence b covers rows [b*N, (b+1)*N).
+// ---------------------------------------------------------------------------
 template <int VB>
-__global__ __launch_bounds__(256) void pack_kernel(PackArgs args, int esz, int B, int N, int D,
+__global__ __launch_bounds__(256) void pack_kernel(PackArgs args, int n_tensors, int hmax, int esz,
+                                                   int B, int N, int D,
                                                    const int32_t* __restrict__ cu, int T,
                                                    int T_pad) {
   typedef typename VecOf<VB>::type V;
-  const fmlm_pack_tensor& tt = args.t[blockIdx.y];
+  const int ti = blockIdx.y / hmax, h = blockIdx.y % hmax;
+  if (ti >= n_tensors) return;
+  const fmlm_pack_tensor& tt = args.t[ti];
+  if (h >= tt.heads) return;
   const int cpr = D * esz / VB;  // chunks per row
-  const int64_t total = (int64_t)tt.heads * T_pad * cpr;
-  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
-       c += (int64_t)gridDim.x * blockDim.x) {
-    const int chunk = (int)(c % cpr);
-    const int64_t row = c / cpr;  // h*T_pad + t
-    const int t = (int)(row % T_pad);
-    const int h = (int)(row / T_pad);
-    V val = V{};
-    int b = 0, p = N;
-    if (t < T) {
-      if (cu) {
-        b = find_seq(cu, B, t);
-        p = t - cu[b];
-      } else {
-        b = t / N;
-        p = t - b * N;
-      }
+  const int64_t row_bytes = (int64_t)D * esz;
+  char* const dst = (char*)tt.dst + (int64_t)h * T_pad * row_bytes;
+  const int b = blockIdx.z;
+  if (b < B) {
+    const int start = cu ? cu[b] : b * N;
+    const int len = min(cu ? cu[b + 1] - start : N, N);
+    const int p = blockIdx.x * blockDim.y + threadIdx.y;
+    if (p >= len) return;
+    const int t = start + p;
+    if (t < 0 || t >= T) return;
+    const char* src = (const char*)tt.src +
+                      ((int64_t)b * tt.s_sb + (int64_t)h * tt.s_sh + (int64_t)p * tt.s_sn) * esz;
+    for (int c = threadIdx.x; c < cpr; c += blockDim.x)
+      *(V*)(dst + (int64_t)t * row_bytes + (int64_t)c * VB) = *(const V*)(src + (int64_t)c * VB);
+  } else {  // zero rows outside [c0, c1)
+    const int c0 = cu ? min(max(cu[0], 0), T) : 0;
+    const int c1 = cu ? min(max(cu[B], c0), T) : T;
+    const int nz = c0 + (T_pad - c1);
+    for (int r = blockIdx.x * blockDim.y + threadIdx.y; r < nz; r += gridDim.x * blockDim.y) {
+      const int t = r < c0 ? r : c1 + (r - c0);
+      for (int c = threadIdx.x; c < cpr; c += blockDim.x)
+        *(V*)(dst + (int64_t)t * row_bytes + (int64_t)c * VB) = V{};
     }
-    if (p < N) {  // p >= N only for t >= T or an inconsistent cu: leave the row zero
-      const char* src = (const char*)tt.src +
-                        ((int64_t)b * tt.s_sb + (int64_t)h * tt.s_sh + (int64_t)p * tt.s_sn) * esz;
-      val = *(const V*)(src + (int64_t)chunk * VB);
-    }
-    *(V*)((char*)tt.dst + row * D * esz + (int64_t)chunk * VB) = val;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Unpack: one thread per VB-byte chunk of a padded output row (b, h, n).
+// Unpack: block (TX chunk lanes x TY rows) over grid (row block of N, head, sequence):
+// dst row (b, h, n) = packed row h*p_sh/D + cu[b] + n for n < L_b, zeros otherwise.
 // ---------------------------------------------------------------------------
 template <int VB>
 __global__ __launch_bounds__(256) void unpack_kernel(const char* __restrict__ packed, int64_t p_sh,
@@ -209,25 +221,26 @@ __global__ __launch_bounds__(256) void unpack_kernel(const char* __restrict__ pa
                                                      const int32_t* __restrict__ cu) {
   typedef typename VecOf<VB>::type V;
   const int cpr = D * esz / VB;
-  const int64_t total = (int64_t)B * H * N * cpr;
-  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
-       c += (int64_t)gridDim.x * blockDim.x) {
-    const int chunk = (int)(c % cpr);
-    const int64_t row = c / cpr;  // (b*H + h)*N + n
-    const int n = (int)(row % N);
-    const int64_t bh = row / N;
-    const int h = (int)(bh % H);
-    const int b = (int)(bh / H);
-    const int start = cu[b];
-    const int len = cu[b + 1] - start;
-    V val;
-    if (n < len)
-      val = *(const V*)(packed + ((int64_t)h * p_sh + (int64_t)(start + n) * D) * esz +
-                        (int64_t)chunk * VB);
-    else
-      val = V{};
-    *(V*)(dst + row * D * esz + (int64_t)chunk * VB) = val;
+  const int64_t row_bytes = (int64_t)D * esz;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int start = cu[b];
+  const int len = cu[b + 1] - start;
+  const int n = blockIdx.x * blockDim.y + threadIdx.y;
+  if (n >= N) return;
+  char* const out = dst + (((int64_t)b * H + h) * N + n) * row_bytes;
+  if (n < len) {
+    const char* in = packed + ((int64_t)h * p_sh + (int64_t)(start + n) * D) * esz;
+    for (int c = threadIdx.x; c < cpr; c += blockDim.x)
+      *(V*)(out + (int64_t)c * VB) = *(const V*)(in + (int64_t)c * VB);
+  } else {
+    for (int c = threadIdx.x; c < cpr; c += blockDim.x) *(V*)(out + (int64_t)c * VB) = V{};
   }
+}
+
+// Block shape for a row-copy kernel: TX lanes across a row's chunks, TY rows.
+static dim3 row_block(int cpr) {
+  const int tx = cpr < 256 ? cpr : 256;
+  return dim3(tx, 256 / tx);
 }
 
 // Widest vector width (bytes) that divides the row size and every address.
@@ -239,13 +252,6 @@ static int pick_vec(int64_t row_bytes, std::initializer_list<uint64_t> addrs_byt
     if (ok) return vb;
   }
   return 0;
-}
-
-static int grid_for(int64_t work, int threads) {
-  int64_t g = (work + threads - 1) / threads;
-  const int64_t cap = 256 * 64;  // grid-stride beyond 64 workgroups per CU
-  if (g > cap) g = cap;
-  return (int)(g < 1 ? 1 : g);
 }
 
 }  // namespace fmlm
@@ -302,7 +308,6 @@ extern "C" int fmlm_pack(const fmlm_pack_tensor* tensors, int32_t n_tensors, int
     return FMLM_E_ARG;
   if (!cu_seqlens && T != B * N) return FMLM_E_ARG;
   PackArgs args = {};
-  int64_t max_work = 0;
   int vb = 16;
   for (int i = 0; i < n_tensors; ++i) {
     const fmlm_pack_tensor& t = tensors[i];
@@ -313,16 +318,19 @@ extern "C" int fmlm_pack(const fmlm_pack_tensor* tensors, int32_t n_tensors, int
                             (uint64_t)(t.s_sh * esz), (uint64_t)(t.s_sn * esz)});
     if (!v) return FMLM_E_ALIGN;
     vb = v < vb ? v : vb;
-    const int64_t w = (int64_t)t.heads * T_pad * D * esz;
-    max_work = w > max_work ? w : max_work;
   }
   if (T_pad == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(grid_for(max_work / vb, 256), n_tensors);
-#define FMLM_PACK_CASE(VB)                                                                       \
-  case VB:                                                                                       \
-    hipLaunchKernelGGL(pack_kernel<VB>, grid, dim3(256), 0, s, args, esz, B, N, D, cu_seqlens, \
-                       T, T_pad);                                                                \
+  int hmax = 0;
+  for (int i = 0; i < n_tensors; ++i) hmax = tensors[i].heads > hmax ? tensors[i].heads : hmax;
+  const dim3 blk = row_block((int)((int64_t)D * esz / vb));
+  const int64_t gx = ((int64_t)(N > 0 ? N : 1) + blk.y - 1) / blk.y;
+  if ((int64_t)hmax * n_tensors > 65535 || B + 1 > 65535 || gx > (1 << 30)) return FMLM_E_ARG;
+  const dim3 grid((unsigned)gx, hmax * n_tensors, B + 1);
+#define FMLM_PACK_CASE(VB)                                                                     \
+  case VB:                                                                                     \
+    hipLaunchKernelGGL(pack_kernel<VB>, grid, blk, 0, s, args, n_tensors, hmax, esz, B, N, D, \
+                       cu_seqlens, T, T_pad);                                                  \
     break;
   switch (vb) {
     FMLM_PACK_CASE(16)
@@ -348,13 +356,16 @@ extern "C" int fmlm_unpack(int32_t elem_bytes, const void* packed, int64_t p_sh,
                           {(uint64_t)packed, (uint64_t)dst, (uint64_t)(p_sh * esz)});
   if (!vb) return FMLM_E_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(grid_for(rows * D * esz / vb, 256));
+  const dim3 blk = row_block((int)((int64_t)D * esz / vb));
+  const int64_t gx = ((int64_t)N + blk.y - 1) / blk.y;
+  if (H > 65535 || B > 65535 || gx > (1 << 30)) return FMLM_E_ARG;
+  const dim3 grid((unsigned)gx, H, B);
   const char* pk = (const char*)packed;
   char* out = (char*)dst;
-#define FMLM_UNPACK_CASE(VB)                                                                    \
-  case VB:                                                                                      \
-    hipLaunchKernelGGL(unpack_kernel<VB>, grid, dim3(256), 0, s, pk, p_sh, out, B, H, N, D, esz, \
-                       cu_seqlens);                                                             \
+#define FMLM_UNPACK_CASE(VB)                                                                 \
+  case VB:                                                                                   \
+    hipLaunchKernelGGL(unpack_kernel<VB>, grid, blk, 0, s, pk, p_sh, out, B, H, N, D, esz, \
+                       cu_seqlens);                                                          \
     break;
   switch (vb) {
     FMLM_UNPACK_CASE(16)
