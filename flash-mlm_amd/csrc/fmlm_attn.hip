@@ -34,10 +34,27 @@ namespace fmlm {
 // are visited longest-first (estimated keys x tiles), which also balances the XCDs.
 // Slots past an XCD's share are idle (b = -1).  The list is built once per
 // cu_seqlens by schedule_kernel and cached by the host.
+//
+// Split-KV: when the units would fill the GPU's workgroup slots for fewer than
+// kSplitRounds rounds, each query tile's key range is cut into S parts (a split group);
+// every part is a unit that writes a partial record (O / l, m, l per row) and a second
+// kernel, merge_kernel, combines each group's records into the output.  (Merging inside
+// the attention kernel would need device-scope release/acquire between workgroups,
+// which writes back and invalidates an XCD's whole L2 each time.)
+//
+// Unit encoding (int4): x = b (-1: idle), y = h | tile << 16, z = first record of the
+// split group, w = -1 (no split) or group | s << 20 | (S - 1) << 25.
+// Schedule buffer: [0, 256) header (n_units, n_groups, groups / records offsets, record
+// bytes), units at 256, then the group list (int4: b, h | tile << 16, first record, S),
+// then the records.
 // ---------------------------------------------------------------------------
 constexpr int kXcds = 8;
 constexpr int kSchedThreads = 512;  // one wave per XCD
 constexpr int kSortMax = 2048;      // sequences ordered longest-first up to this many
+constexpr int kSplitBK = 64;        // key tile of the split-capable kernel
+constexpr int kMaxSplits = 16;
+constexpr int kMinSplitTiles = 8;   // key tiles per part at least
+constexpr float kSplitRounds = 1.5f;
 
 struct SeqInfo {
   int q0, len;       // packed start and clamped length of sequence b
@@ -70,22 +87,65 @@ FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
 }
 
 __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn_params p, int BQ,
-                                                                 int capacity,
+                                                                 int capacity, int slots,
+                                                                 int rec_cap,
                                                                  int4* __restrict__ units,
-                                                                 int32_t* __restrict__ n_units) {
+                                                                 int32_t* __restrict__ header,
+                                                                 int4* __restrict__ groups,
+                                                                 int groups_off, int records_off,
+                                                                 int rec_bytes) {
   __shared__ int s_tiles[kSortMax];
   __shared__ float s_work[kSortMax];
   __shared__ int s_order[kSortMax];
+  __shared__ unsigned char s_split[kSortMax];
   __shared__ int s_len[kXcds];
+  __shared__ float s_sum[2];
+  __shared__ int s_chunk, s_groups, s_recs;
   const int tid = threadIdx.x;
   const int B = p.B, H = p.H;
   const bool sorted = B <= kSortMax;
+  if (tid < 2) s_sum[tid] = 0.f;
+  if (tid == 0) {
+    s_chunk = 0;
+    s_groups = 0;
+    s_recs = 0;
+  }
+  __syncthreads();
   if (sorted) {
+    // per sequence: query tiles and key tiles; totals of units and key-tile work
     for (int b = tid; b < B; b += kSchedThreads) {
       const SeqInfo si = seq_info(p, b);
       const int tiles = (si.len + BQ - 1) / BQ;
+      const int ktiles = (si.ctx + kSplitBK - 1) / kSplitBK + (si.mainlen + kSplitBK - 1) / kSplitBK;
       s_tiles[b] = tiles;
-      s_work[b] = (float)tiles * (float)(si.ctx + si.mainlen + BQ);
+      s_work[b] = (float)ktiles;
+      atomicAdd(&s_sum[0], (float)tiles * H);
+      atomicAdd(&s_sum[1], (float)tiles * H * ktiles);
+    }
+    __syncthreads();
+    // split only when the units are too few to fill the slots for kSplitRounds rounds;
+    // parts of about total / (kSplitRounds * slots) key tiles, at least kMinSplitTiles,
+    // the part size doubling until the records fit
+    if (tid == 0 && rec_cap > 0 && s_sum[0] < kSplitRounds * slots) {
+      int chunk = max(kMinSplitTiles, (int)ceilf(s_sum[1] / (kSplitRounds * slots)));
+      for (int it = 0; it < 24; ++it, chunk *= 2) {
+        float recs = 0.f;
+        for (int b = 0; b < B; ++b) {
+          const int S = min(kMaxSplits, max(1, (int)ceilf(s_work[b] / chunk)));
+          if (S > 1) recs += (float)s_tiles[b] * H * S;
+        }
+        if (recs <= (float)rec_cap) {
+          s_chunk = chunk;
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    for (int b = tid; b < B; b += kSchedThreads) {
+      const int S = s_chunk > 0 ? min(kMaxSplits, max(1, (int)ceilf(s_work[b] / s_chunk))) : 1;
+      s_split[b] = (unsigned char)S;
+      // longest unit first (key tiles per part), then more tiles first
+      s_work[b] = ceilf(s_work[b] / S) * 65536.f + (float)s_tiles[b];
     }
     __syncthreads();
     for (int b = tid; b < B; b += kSchedThreads) {
@@ -104,24 +164,35 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
   int carry = 0;
   for (int i0 = 0; x + kXcds * i0 < G; i0 += 64) {
     const int g = x + kXcds * (i0 + lane);
-    int b = 0, h = 0, tiles = 0;
+    int b = 0, h = 0, tiles = 0, S = 1;
     if (g < G) {
       const int r = g / H;
       h = g - r * H;
       b = sorted ? s_order[r] : r;
       tiles = sorted ? s_tiles[b] : (seq_info(p, b).len + BQ - 1) / BQ;
+      S = sorted ? s_split[b] : 1;
     }
-    // inclusive wave scan of tiles
-    int incl = tiles;
+    const int n = tiles * S;
+    // inclusive wave scan of units
+    int incl = n;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const int v = __shfl_up(incl, off);
       if (lane >= off) incl += v;
     }
-    const int pos = carry + incl - tiles;
+    const int pos = carry + incl - n;
+    int gid0 = 0, rec0 = 0;
+    if (S > 1) {
+      gid0 = atomicAdd(&s_groups, tiles);
+      rec0 = atomicAdd(&s_recs, tiles * S);
+      for (int j = 0; j < tiles; ++j) groups[gid0 + j] = make_int4(b, h | (j << 16), rec0 + j * S, S);
+    }
     for (int j = 0; j < tiles; ++j) {
-      const int64_t slot = (int64_t)x + (int64_t)kXcds * (pos + j);
-      if (slot < capacity) units[slot] = make_int4(b, h, j, 0);
+      for (int sp = 0; sp < S; ++sp) {
+        const int64_t slot = (int64_t)x + (int64_t)kXcds * (pos + j * S + sp);
+        const int wv = S > 1 ? (gid0 + j) | (sp << 20) | ((S - 1) << 25) : -1;
+        if (slot < capacity) units[slot] = make_int4(b, h | (j << 16), rec0 + j * S, wv);
+      }
     }
     carry += __shfl(incl, 63);
   }
@@ -133,7 +204,13 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
     const int64_t slot = (int64_t)x + (int64_t)kXcds * q;
     if (slot < capacity) units[slot] = make_int4(-1, 0, 0, 0);
   }
-  if (tid == 0) *n_units = (int)min((int64_t)kXcds * maxlen, (int64_t)capacity);
+  if (tid == 0) {
+    header[0] = (int)min((int64_t)kXcds * maxlen, (int64_t)capacity);
+    header[1] = s_groups;
+    header[2] = groups_off;
+    header[3] = records_off;
+    header[4] = rec_bytes;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -151,6 +228,8 @@ struct KvSeg {
 
 struct WorkItem {
   int b, h;
+  int split_s, split_n;  // part s of S of the key range (S = 1: whole range)
+  int split_group, rec0; // split group and its first record
   int qpos0, qcount;     // query positions [qpos0, qpos0+qcount) of sequence b
   int64_t q_row0, o_row0;  // element offset of row qpos0
   int64_t q_sn, o_sn;
@@ -170,13 +249,23 @@ FMLM_DEV int64_t seg_row(const KvSeg& s, int i, bool is_v, const int32_t* cu, in
 FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const int32_t* n_units,
                            int BQ, WorkItem& w) {
   int b, h, tile;
+  w.split_s = 0;
+  w.split_n = 1;
+  w.split_group = 0;
+  w.rec0 = 0;
   if (p.cu_seqlens_q) {
     if ((int)blockIdx.x >= *n_units) return false;
     const int4 u = units[blockIdx.x];
     b = u.x;
-    h = u.y;
-    tile = u.z;
+    h = u.y & 0xffff;
+    tile = (int)((uint32_t)u.y >> 16);
     if (b < 0) return false;
+    if (u.w >= 0) {
+      w.split_group = u.w & 0xfffff;
+      w.split_s = (u.w >> 20) & 31;
+      w.split_n = ((u.w >> 25) & 15) + 1;
+      w.rec0 = u.z;
+    }
   } else {
     // dense: group g = (b, h) on XCD g % 8, its ceil(N/BQ) tiles on consecutive slots
     const int nt = (p.N + BQ - 1) / BQ;
@@ -618,7 +707,6 @@ FMLM_DEV void dma16_sbase(const char* base, uint32_t off, uint32_t lds) {
 }
 #pragma clang diagnostic pop
 
-constexpr int kLdsLead = 3;  // LDS reads issued before the first MFMA of a step
 
 template <typename T>
 struct Pair;
@@ -654,6 +742,7 @@ struct Mfma3Cfg {
   static constexpr int NDB = D / 16;
   static constexpr int NKB = BK / 16;
   static constexpr int NKS = BK / 32;
+  static constexpr int LEAD = D <= 64 ? 2 : 3;  // LDS fragment reads in flight ahead of use
   static constexpr int NKF = KC * NKB;    // K fragment reads per step
   static constexpr int NVF = NKS * NDB;   // V fragment (tr16 pair) reads per step
   static_assert(D % 16 == 0 && D >= 16 && D <= 256, "head dim");
@@ -744,6 +833,9 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
   const int ntiles = nt0 + nt1;
+  // key tiles [tb, te) of this unit: all of them, or part s of S of a split group
+  const int tb = (int)((int64_t)w.split_s * ntiles / w.split_n);
+  const int te = (int)((int64_t)(w.split_s + 1) * ntiles / w.split_n);
 
   // ---- direct loads.  A cursor walks the key tiles of the context then the main segment
   // (linear addressing: the dispatcher routes per-row lookups elsewhere): p is the
@@ -765,7 +857,14 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     cr.rowb = __builtin_amdgcn_readfirstlane((uint32_t)(is_v ? sgm.vsn : sgm.ksn) * 2u);
     cr.p = uniform_ptr((is_v ? sgm.v : sgm.k) + (is_v ? sgm.vbase : sgm.kbase) * 2);
   };
-  auto cursor_init = [&](Cursor& cr, bool is_v) { cursor_seg(cr, w.seg[0].n > 0 ? 0 : 1, is_v); };
+  // position a cursor on key tile t
+  auto cursor_seek = [&](Cursor& cr, int t, bool is_v) {
+    const int sg = t < nt0 ? 0 : 1;
+    cursor_seg(cr, sg, is_v);
+    const int skip = (sg == 0 ? t : t - nt0) * BK;
+    cr.left -= skip;
+    cr.p += (size_t)skip * cr.rowb;
+  };
   // load the cursor's tile into LDS dst and advance to the next tile
   auto fetch = [&](Cursor& cr, char* dst, bool is_v) {
     const uint32_t lds0 = lds_addr(dst);
@@ -825,8 +924,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   // and its maxima, consumes V(t) at vt, refills kdst with K(t+2) and vdst with V(t+1).
   auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
                   const char* kn, const char* vt, char* kdst, char* vdst) {
-    if (t + 2 < ntiles) fetch(kcur, kdst, false);
-    if (t + 1 < ntiles) fetch(vcur, vdst, true);
+    if (t + 2 < te) fetch(kcur, kdst, false);
+    if (t + 1 < te) fetch(vcur, vdst, true);
     if (!wave_active) {  // every query row of this wave is padding: loads and barriers only
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
@@ -872,27 +971,27 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     // MFMAs of operand fragment s: fragments [0, NKF) are K(t+1) fragments (S(t+1),
     // beside a share of the exp work of P(t)), fragments [NKF, NKF+NVF) are V(t)
     // fragments (O += V^T P, beside a share of the row-max work of S(t+1)).  The LDS
-    // read of fragment s + kLdsLead is issued at the top of slot s.
+    // read of fragment s + C::LEAD is issued at the top of slot s.
     constexpr int NF = C::NKF + C::NVF;
     f32x4 minit[QB];  // -m_i splat: the initial S accumulators
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) minit[qb] = f32x4{-m_i[qb], -m_i[qb], -m_i[qb], -m_i[qb]};
     constexpr int NP = C::NKB * QB * 2;    // exp pairs
     constexpr int NMS = C::NKB * QB + QB;  // row-max steps
-    v8 fr[kLdsLead + 1];
+    v8 fr[C::LEAD + 1];
     u32x4 pf[C::NKS][QB];  // P(t) as packed pairs, the B operand of P V
     float mpart[QB];
     auto issue = [&](int r) {
       if (r < C::NKF) {
         const int kc = r / C::NKB, kb = r % C::NKB;
-        fr[r % (kLdsLead + 1)] = kc * 32 + g * 8 < D
+        fr[r % (C::LEAD + 1)] = kc * 32 + g * 8 < D
             ? *(const v8*)(kn + kb * 16 * C::ROWB + 256 * (kc >> 2) + koff[kc & 3]) : v8{};
       } else {
         const int j = r - C::NKF, ks = j / C::NDB, db = j % C::NDB;
         const char* va = vt + ks * 32 * C::ROWB + 256 * (db >> 3) + voff[db & 7];
         const s16x4 lo = lds_read_tr16(va);
         const s16x4 hi = lds_read_tr16(va + 16 * C::ROWB);
-        fr[r % (kLdsLead + 1)] = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        fr[r % (C::LEAD + 1)] = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     };
     // exp of S^T elements (kb, r), (kb, r+1) of block qb; keys kb*16 + 4g + r (+1) are
@@ -923,15 +1022,15 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       }
     };
 #pragma unroll
-    for (int r = 0; r < kLdsLead; ++r) issue(r);
+    for (int r = 0; r < C::LEAD; ++r) issue(r);
     // wave priority: a wave in its MFMA-dense block issues ahead of the other waves on its
     // SIMD (their loads, branches and softmax VALU fill the gaps), the P V phase highest
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int sl = 0; sl < NF; ++sl) {
-      if (sl + kLdsLead < NF) issue(sl + kLdsLead);
+      if (sl + C::LEAD < NF) issue(sl + C::LEAD);
       if (sl == C::NKF) __builtin_amdgcn_s_setprio(2);
-      const v8 a = fr[sl % (kLdsLead + 1)];
+      const v8 a = fr[sl % (C::LEAD + 1)];
       if (sl < C::NKF) {
         const int kc = sl / C::NKB, kb = sl % C::NKB;
 #pragma unroll
@@ -962,12 +1061,12 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
 
   f32x4 sa[C::NKB][QB], sb[C::NKB][QB];
   float mx[QB];
-  if (ntiles > 0) {
-    cursor_init(kcur, false);
-    cursor_init(vcur, true);
+  if (te > tb) {
+    cursor_seek(kcur, tb, false);
+    cursor_seek(vcur, tb, true);
     fetch(kcur, kbuf, false);
     fetch(vcur, vbuf, true);
-    if (ntiles > 1) fetch(kcur, kbuf + C::TILEB, false);
+    if (te - tb > 1) fetch(kcur, kbuf + C::TILEB, false);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (wave_active) {
@@ -976,13 +1075,42 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     }
     __syncthreads();  // every wave is done with K(0): its buffer may be refilled
   }
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = (t & 1) * C::TILEB, nxt = C::TILEB - cur;
+  for (int t = tb; t < te; ++t) {
+    const int cur = ((t - tb) & 1) * C::TILEB, nxt = C::TILEB - cur;
     step(t, sa, sb, mx, kbuf + nxt, vbuf + cur, kbuf + cur, vbuf + nxt);
 #pragma unroll
     for (int kb = 0; kb < C::NKB; ++kb)
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) sa[kb][qb] = sb[kb][qb];
+  }
+
+  // ---- split part: this part's record (O / l as T, then m and l per row) for
+  // merge_kernel
+  if (w.split_n > 1) {
+    const int32_t* hdr = n_units;
+    char* const records = (char*)hdr + hdr[3];
+    const int64_t rec_bytes = hdr[4];
+    const int64_t ml_off = (int64_t)C::BQ * D * 2;  // m [BQ] then l [BQ] (fp32)
+    char* const mine = records + (int64_t)(w.rec0 + w.split_s) * rec_bytes;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int row = (wave * QB + qb) * 16 + l16;
+      if (row >= w.qcount) continue;
+      const float l = lsum[qb][0];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db) {
+        T v4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = (T)(o[db][qb][r] * inv);
+        *(u32x2*)(mine + ((int64_t)row * D + db * 16 + g * 4) * 2) = *(const u32x2*)v4;
+      }
+      if (g == 0) {
+        ((float*)(mine + ml_off))[row] = m_i[qb];
+        ((float*)(mine + ml_off))[C::BQ + row] = l;
+      }
+    }
+    return;
   }
 
   // ---- epilogue: O /= l (l == 0 -> 1), store valid rows
@@ -1353,11 +1481,84 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
 // ---------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// Split-KV merge: for every split group (query tile (b, h, tile) whose key range was
+// cut into S parts), O = sum_s 2^(m_s - M) l_s O_s / sum_s 2^(m_s - M) l_s with
+// M = max_s m_s, over the parts' records (O_s = part output / l_s as T, m_s in log2
+// units, l_s its row sum).  Grid-stride over groups; 8 columns of a row per thread.
+// ---------------------------------------------------------------------------
+constexpr int kMergeRows = 128;  // largest split-capable query tile
+
+template <typename T>
+__global__ __launch_bounds__(256) void merge_kernel(const fmlm_attn_params p, int BQ,
+                                                    const int32_t* __restrict__ header) {
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ float s_w[kMergeRows][kMaxSplits];  // per row: part weights / their sum
+  const int n_groups = header[1];
+  const int4* groups = (const int4*)((const char*)header + header[2]);
+  const char* records = (const char*)header + header[3];
+  const int64_t rec_bytes = header[4];
+  const int D = p.D;
+  const int64_t ml_off = (int64_t)BQ * D * 2;
+  for (int gi = blockIdx.x; gi < n_groups; gi += gridDim.x) {
+    const int4 gr = groups[gi];
+    const int b = gr.x, h = gr.y & 0xffff, tile = (int)((uint32_t)gr.y >> 16), S = gr.w;
+    const SeqInfo si = seq_info(p, b);
+    const int qcount = min(BQ, si.len - tile * BQ);
+    const int64_t ob = p.o_layout == FMLM_LAYOUT_PACKED
+                           ? (int64_t)h * p.o_sh + (int64_t)si.q0 * p.o_sn
+                           : (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
+    const int64_t o_row0 = ob + (int64_t)tile * BQ * p.o_sn;
+    const char* rec0 = records + (int64_t)gr.z * rec_bytes;
+    // weights of row r: 2^(m_s - M) l_s / sum, all parts' (m, l) loaded at once
+    for (int r = threadIdx.x; r < qcount; r += blockDim.x) {
+      float m[kMaxSplits], l[kMaxSplits];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp) {
+        const float* ml = (const float*)(rec0 + (sp < S ? sp : 0) * rec_bytes + ml_off);
+        m[sp] = sp < S ? ml[r] : -INFINITY;
+        l[sp] = sp < S ? ml[BQ + r] : 0.f;
+      }
+      float M = -INFINITY;
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp) M = fmaxf(M, m[sp]);
+      float L = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp) {
+        l[sp] = M == -INFINITY ? 0.f : fast_exp2(m[sp] - M) * l[sp];
+        L += l[sp];
+      }
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp) s_w[r][sp] = l[sp] * inv;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < qcount * (D / 8); idx += blockDim.x) {
+      const int row = idx / (D / 8), c8 = idx - row * (D / 8);
+      const char* src = rec0 + ((int64_t)row * D + c8 * 8) * 2;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int sp = 0; sp < S; ++sp) {
+        const v8 ov = *(const v8*)(src + sp * rec_bytes);
+        const float ws = s_w[row][sp];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += ws * (float)ov[e];
+      }
+      v8 res;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) res[e] = (T)acc[e];
+      *(v8*)((char*)p.o + (o_row0 + (int64_t)row * p.o_sn + c8 * 8) * 2) = res;
+    }
+    __syncthreads();  // s_w is rewritten for the next group
+  }
+}
+
 struct Launch {
   int bq;         // query rows per workgroup
   int threads;
   int lds;
   const void* fn;
+  bool split = false;  // kernel can run split-KV units
 };
 
 template <typename T, int D, int QB, int NW, int BK>
@@ -1375,7 +1576,8 @@ static Launch simt_launch() {
 template <typename T, int D, int QB, int NW, int BK>
 static Launch mfma3_launch() {
   typedef Mfma3Cfg<T, D, QB, NW, BK> C;
-  return Launch{C::BQ, C::NT, C::LDS_BYTES, (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK>};
+  static_assert(BK == kSplitBK, "split planning assumes the kernel's key tile");
+  return Launch{C::BQ, C::NT, C::LDS_BYTES, (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK>, true};
 }
 
 template <typename T>
@@ -1438,21 +1640,102 @@ static int pick_launch(const fmlm_attn_params& p, Launch& L) {
   return ok ? 0 : FMLM_E_HEAD_DIM;
 }
 
+// Allow the kernel's dynamic LDS (> 64 KiB for some tiles), once per kernel.
+static int allow_lds(const Launch& L) {
+  static std::mutex mu;
+  static const void* raised[64];
+  static int n_raised = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_raised; ++i)
+    if (raised[i] == L.fn) return 0;
+  hipError_t e = hipFuncSetAttribute(L.fn, hipFuncAttributeMaxDynamicSharedMemorySize, L.lds);
+  if (e != hipSuccess) return (int)e;
+  if (n_raised < 64) raised[n_raised++] = L.fn;
+  return 0;
+}
+
+// Split-KV sizing: the GPU's workgroup slots for this kernel (CUs x resident
+// workgroups), the record capacity and the record size.
+struct SplitCfg {
+  int slots = 0;
+  int rec_cap = 0;        // 0: no split
+  int64_t rec_bytes = 0;  // per record: rows x (D elements + m + l)
+};
+
+static SplitCfg split_cfg(const fmlm_attn_params& p, const Launch& L) {
+  SplitCfg sc;
+  if (!L.split || !p.cu_seqlens_q) return sc;
+  static std::mutex mu;
+  static const void* fns[64];
+  static int slots_of[64];
+  static int n_fns = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_fns; ++i)
+      if (fns[i] == L.fn) sc.slots = slots_of[i];
+    if (sc.slots == 0) {
+      int dev = 0, cus = 0, per_cu = 0;
+      if (allow_lds(L) != 0 || hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, L.fn, L.threads, L.lds) != hipSuccess)
+        return sc;
+      sc.slots = cus * (per_cu > 0 ? per_cu : 1);
+      if (n_fns < 64) {
+        fns[n_fns] = L.fn;
+        slots_of[n_fns++] = sc.slots;
+      }
+    }
+  }
+  // every sequence's tiles but its last are full, so there are at least
+  // H * (total_q - B*bq) / bq units: when that already fills kSplitRounds rounds, the
+  // schedule cannot split (and no records or merge launch are needed)
+  const int64_t min_units = (int64_t)p.H * (((int64_t)p.total_q - (int64_t)p.B * L.bq) / L.bq);
+  if (min_units >= (int64_t)(kSplitRounds * sc.slots) || L.bq > kMergeRows) return SplitCfg{};
+  sc.rec_cap = 3 * sc.slots;
+  const int esz = elem_size(p.dtype);
+  sc.rec_bytes = ((int64_t)L.bq * (p.D * esz + 8) + 15) / 16 * 16;
+  return sc;
+}
+
 // Grid size (1-D): dense units are laid out arithmetically, packed units by the
-// schedule, whose XCD slots are bounded by ceil(total/8) + the largest group.
-static int64_t grid_units(const fmlm_attn_params& p, int bq) {
+// schedule, whose XCD slots are bounded by ceil(total/8) + the largest group (with
+// splits: at most kSplitRounds*slots unsplit units plus rec_cap split parts, a group
+// growing by up to kMaxSplits).
+static int64_t grid_units(const fmlm_attn_params& p, int bq, const SplitCfg& sc) {
   if (!p.cu_seqlens_q) {
     const int64_t groups = (int64_t)p.B * p.H;
     return kXcds * ((groups + kXcds - 1) / kXcds) * ((p.N + bq - 1) / bq);
   }
   const int64_t total = (int64_t)p.H * (p.B + p.total_q / bq + 1);
   const int64_t max_group = (p.N > 0 ? (p.N + bq - 1) / bq : p.total_q / bq + 1) + 1;
-  return kXcds * ((total + kXcds - 1) / kXcds + max_group);
+  int64_t g = kXcds * ((total + kXcds - 1) / kXcds + max_group);
+  if (sc.rec_cap > 0) {
+    const int64_t split_total = (int64_t)(kSplitRounds * sc.slots) + sc.rec_cap;
+    const int64_t gs = kXcds * ((split_total + kXcds - 1) / kXcds + kMaxSplits * max_group);
+    g = gs > g ? gs : g;
+  }
+  return g;
 }
 
-static int64_t workspace_for(const fmlm_attn_params& p, int bq) {
+// Schedule buffer layout (see schedule_kernel): header, units, groups, records.
+struct SchedLayout {
+  int64_t units_off, groups_off, records_off, bytes;
+};
+
+static SchedLayout sched_layout(const fmlm_attn_params& p, int bq, const SplitCfg& sc) {
+  SchedLayout l;
+  l.units_off = 256;
+  l.groups_off = l.units_off + grid_units(p, bq, sc) * (int64_t)sizeof(int4);
+  l.groups_off = (l.groups_off + 255) / 256 * 256;
+  l.records_off = l.groups_off + (int64_t)sc.rec_cap * (int64_t)sizeof(int4);
+  l.records_off = (l.records_off + 255) / 256 * 256;
+  l.bytes = l.records_off + (int64_t)sc.rec_cap * sc.rec_bytes;
+  return l;
+}
+
+static int64_t workspace_for(const fmlm_attn_params& p, const Launch& L) {
   if (!p.cu_seqlens_q) return 0;
-  return 256 + grid_units(p, bq) * (int64_t)sizeof(int4);
+  return sched_layout(p, L.bq, split_cfg(p, L)).bytes;
 }
 
 static int check_params(const fmlm_attn_params& p) {
@@ -1471,11 +1754,16 @@ static int check_params(const fmlm_attn_params& p) {
   return 0;
 }
 
-static int launch_schedule(const fmlm_attn_params& p, int bq, char* sched, hipStream_t s) {
-  const int64_t cap = grid_units(p, bq);
-  if (cap > 0x7fffffff) return FMLM_E_ARG;
-  hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, s, p, bq, (int)cap,
-                     (int4*)(sched + 256), (int32_t*)sched);
+static int launch_schedule(const fmlm_attn_params& p, const Launch& L, char* sched, hipStream_t s) {
+  const SplitCfg sc = split_cfg(p, L);
+  const SchedLayout l = sched_layout(p, L.bq, sc);
+  const int64_t cap = grid_units(p, L.bq, sc);
+  if (cap > 0x7fffffff || p.H > 0xffff || (p.N + L.bq - 1) / L.bq > 0xffff) return FMLM_E_ARG;
+  int32_t* header = (int32_t*)sched;
+  hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, s, p, L.bq, (int)cap,
+                     sc.slots, sc.rec_cap, (int4*)(sched + l.units_off), header,
+                     (int4*)(sched + l.groups_off), (int)l.groups_off, (int)l.records_off,
+                     (int)sc.rec_bytes);
   return launch_status();
 }
 
@@ -1489,8 +1777,8 @@ extern "C" int fmlm_attn_schedule(const fmlm_attn_params* pp, void* schedule,
   Launch L;
   const int rc = pick_launch(*pp, L);
   if (rc) return rc;
-  if (schedule_bytes < workspace_for(*pp, L.bq)) return FMLM_E_WORKSPACE;
-  return launch_schedule(*pp, L.bq, (char*)schedule, (hipStream_t)stream);
+  if (schedule_bytes < workspace_for(*pp, L)) return FMLM_E_WORKSPACE;
+  return launch_schedule(*pp, L, (char*)schedule, (hipStream_t)stream);
 }
 
 extern "C" int fmlm_attn_params_size(void) { return (int)sizeof(fmlm_attn_params); }
@@ -1500,7 +1788,7 @@ extern "C" int64_t fmlm_attn_workspace_bytes(const fmlm_attn_params* p) {
   Launch L;
   const int rc = pick_launch(*p, L);
   if (rc) return rc;
-  return workspace_for(*p, L.bq);
+  return workspace_for(*p, L);
 }
 
 extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
@@ -1512,24 +1800,12 @@ extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
   rc = pick_launch(p, L);
   if (rc) return rc;
   if (p.B == 0 || p.H == 0) return 0;
-  const int64_t need = workspace_for(p, L.bq);
+  const int64_t need = workspace_for(p, L);
   if (need > 0 && !p.schedule && (!p.workspace || p.workspace_bytes < need)) return FMLM_E_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
 
-  // allow > 64 KiB of dynamic LDS once per kernel
-  {
-    static std::mutex mu;
-    static const void* raised[64];
-    static int n_raised = 0;
-    std::lock_guard<std::mutex> lock(mu);
-    bool done = false;
-    for (int i = 0; i < n_raised; ++i) done = done || raised[i] == L.fn;
-    if (!done) {
-      hipError_t e = hipFuncSetAttribute(L.fn, hipFuncAttributeMaxDynamicSharedMemorySize, L.lds);
-      if (e != hipSuccess) return (int)e;
-      if (n_raised < 64) raised[n_raised++] = L.fn;
-    }
-  }
+  rc = allow_lds(L);
+  if (rc) return rc;
 
   int4* units = nullptr;
   int32_t* n_units = nullptr;
@@ -1538,16 +1814,24 @@ extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
     n_units = (int32_t*)sched;
     units = (int4*)(sched + 256);
     if (!p.schedule) {
-      rc = launch_schedule(p, L.bq, sched, s);
+      rc = launch_schedule(p, L, sched, s);
       if (rc) return rc;
     }
   }
-  const int64_t gx = grid_units(p, L.bq);
+  const int64_t gx = grid_units(p, L.bq, split_cfg(p, L));
   if (gx <= 0) return 0;
   if (gx > 0x7fffffff) return FMLM_E_ARG;
   fmlm_attn_params pc = p;
   void* args[] = {(void*)&pc, (void*)&units, (void*)&n_units};
   hipError_t e = hipLaunchKernel(L.fn, dim3((unsigned)gx), dim3(L.threads), args, (size_t)L.lds, s);
   if (e != hipSuccess) return (int)e;
+  const SplitCfg sc = split_cfg(p, L);
+  if (sc.rec_cap > 0) {  // split groups (if the schedule made any) are merged here
+    const dim3 mg((unsigned)(sc.rec_cap < 1024 ? sc.rec_cap : 1024));
+    if (p.dtype == FMLM_DTYPE_BF16)
+      hipLaunchKernelGGL(merge_kernel<bf16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
+    else
+      hipLaunchKernelGGL(merge_kernel<f16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
+  }
   return launch_status();
 }

@@ -296,6 +296,43 @@ def test_packed_head_dim_dtype_sweep(dtype, D, mode, device):
     _close(unpack_from_kernel(out, meta, H), ref)
 
 
+# ---------------------------------------------------------------------------
+# split-KV: few work units over long key ranges are cut into parts whose partial
+# results are merged by the last part of each group (the schedule decides; these
+# shapes have far fewer units than workgroup slots and tens of key tiles per unit)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [16, 64, 128, 256])
+@pytest.mark.parametrize("mode", ["ctx", "causal_ctx", "shared_ctx", "causal_prefill"])
+def test_split_kv_long_key_ranges(dtype, D, mode, device):
+    torch.manual_seed(7000 + D)
+    causal = "causal" in mode
+    prefill = "prefill" in mode
+    lengths = [97, 1, 300, 0] if not prefill else [900, 1200, 64, 5]
+    B, H, N = len(lengths), 2, max(lengths)
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, dtype) for _ in range(3))
+    if mode == "shared_ctx":
+        cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, [4100], device, dtype, cbs=1)
+        cbs = 1
+    else:
+        cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, [3000, 700, 5000, 1500], device, dtype)
+        cbs = B
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    kw = dict(block_n=64, causal_query_seq_attn=causal, prefill=prefill, context_batch_size=cbs if mode == "shared_ctx" else None)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache if not prefill else InferenceCache(), 0, **kw)
+    ref = _packed_oracle(q, k, v, lengths, scale, causal=causal, prefill=prefill,
+                         k_cache=None if prefill else kc, v_cache=None if prefill else vc,
+                         cu_kv=None if prefill else cu_kv, cbs=cbs, Tc=0 if prefill else Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+    # the schedule split these units (header word 1 counts split groups)
+    (sched,) = meta.kernel_schedules.values()
+    assert int(sched[:8].view(torch.int32)[1]) > 0
+    # the cached schedule (and its split counters) is reused: same result again
+    out2 = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache if not prefill else InferenceCache(), 0, **kw)
+    assert torch.equal(out, out2)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [16, 64, 128, 256])
 @pytest.mark.parametrize("is_mla", [False, True])
