@@ -259,7 +259,7 @@ FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const i
     b = u.x;
     h = u.y & 0xffff;
     tile = (int)((uint32_t)u.y >> 16);
-    if (b < 0) return false;
+    if (b < 0 || b >= p.B || h >= p.H) return false;  // idle, or a schedule of other shapes
     if (u.w >= 0) {
       w.split_group = u.w & 0xfffff;
       w.split_s = (u.w >> 20) & 31;
@@ -1503,6 +1503,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const fmlm_attn_params p, in
   for (int gi = blockIdx.x; gi < n_groups; gi += gridDim.x) {
     const int4 gr = groups[gi];
     const int b = gr.x, h = gr.y & 0xffff, tile = (int)((uint32_t)gr.y >> 16), S = gr.w;
+    if (b < 0 || b >= p.B || h >= p.H) continue;
     const SeqInfo si = seq_info(p, b);
     const int qcount = min(BQ, si.len - tile * BQ);
     const int64_t ob = p.o_layout == FMLM_LAYOUT_PACKED

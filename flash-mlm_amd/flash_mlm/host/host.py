@@ -143,7 +143,9 @@ def _prepare(
     stream = _lib.stream_of(q.device)
     with _device_scope(q.device):
         if ws_bytes > 0 and schedule_cache is not None:
-            key = (p.dtype, D, B, total_q)
+            # what the unit list depends on (the kernel and its tile size, the heads);
+            # context lengths only steer where key ranges are split
+            key = (p.dtype, D, B, H, total_q, p.flags, p.kv_layout)
             sched = schedule_cache.get(key)
             if sched is None:
                 sched = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)

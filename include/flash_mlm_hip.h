@@ -175,8 +175,12 @@ typedef struct fmlm_attn_params {
   void* workspace;         /* device scratch for the work schedule                  */
   int64_t workspace_bytes;
   const void* schedule;    /* NULL, or a schedule built by fmlm_attn_schedule for the same
-                              cu_seqlens_q contents, B, total_q, dtype and D: then
-                              fmlm_attn_fwd launches the attention kernel only        */
+                              cu_seqlens_q contents, B, H, total_q, dtype, D, flags and
+                              kv_layout: then fmlm_attn_fwd launches the attention
+                              kernel (plus the split merge) only.  Context lengths may
+                              differ; they only steer where key ranges are split.  The
+                              buffer also holds split partial results: launches that may
+                              overlap need separate schedule buffers                  */
 } fmlm_attn_params;
 
 /* Bytes of device workspace (and of a schedule buffer) fmlm_attn_fwd needs for these

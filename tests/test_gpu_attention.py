@@ -298,8 +298,8 @@ def test_packed_head_dim_dtype_sweep(dtype, D, mode, device):
 
 # ---------------------------------------------------------------------------
 # split-KV: few work units over long key ranges are cut into parts whose partial
-# results are merged by the last part of each group (the schedule decides; these
-# shapes have far fewer units than workgroup slots and tens of key tiles per unit)
+# results a second kernel merges (the schedule decides; these shapes have far fewer
+# units than workgroup slots and tens of key tiles per unit)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [16, 64, 128, 256])
@@ -328,9 +328,28 @@ def test_split_kv_long_key_ranges(dtype, D, mode, device):
     # the schedule split these units (header word 1 counts split groups)
     (sched,) = meta.kernel_schedules.values()
     assert int(sched[:8].view(torch.int32)[1]) > 0
-    # the cached schedule (and its split counters) is reused: same result again
+    # the cached schedule (and its split records) is reused: same result again
     out2 = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache if not prefill else InferenceCache(), 0, **kw)
     assert torch.equal(out, out2)
+
+
+def test_cached_schedule_per_head_count_and_mode(device):
+    """One PackMetadata serves calls with different head counts, modes and contexts: each
+    call gets a schedule built for its own heads and kernel, and every result matches the
+    oracle (a schedule of another head count would skip or overrun heads)."""
+    torch.manual_seed(7100)
+    lengths = [97, 1, 300, 0]
+    B, N, D = len(lengths), 300, 64
+    scale = 1.0 / math.sqrt(D)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    for H, causal, ctx in ((4, False, [3000, 700, 5000, 1500]), (2, False, [3000, 700, 5000, 1500]),
+                           (2, True, [10, 2000, 0, 64]), (4, False, [10, 2000, 0, 64])):
+        q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+        cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, ctx, device, torch.bfloat16)
+        out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=causal)
+        ref = _packed_oracle(q, k, v, lengths, scale, causal=causal, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=B, Tc=Tc)
+        _close(unpack_from_kernel(out, meta, H), ref)
+    assert len(meta.kernel_schedules) == 3
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
