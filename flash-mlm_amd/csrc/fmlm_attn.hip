@@ -645,15 +645,17 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(con
 // ---------------------------------------------------------------------------
 // Software-pipelined MFMA kernel (v3) for head dims 16..256.
 //
-// The LDS holds two K tiles and two V tiles, filled by direct global->LDS loads (no
+// The LDS holds two K tiles and three V tiles, filled by direct global->LDS loads (no
 // staging registers) with 16-byte chunks XOR-swizzled per row by kv_swz, so both the
 // b128 K reads and the tr16 V reads are bank-conflict free.  Iteration t of a wave:
-//   1. issues the loads of K(t+2) (into K(t)'s buffer) and V(t+1) (into V(t-1)'s);
+//   1. issues the loads of K(t+2) (into K(t)'s buffer) and V(t+2) (into V(t-1)'s);
 //   2. row max of S(t) (lane-local + two permlane swaps) and the lazy-rescale decision;
 //   3. one basic block that runs S(t+1) = K(t+1) Q^T on the MFMA pipe while the VALU
 //      computes P(t) = exp2(S(t) c - m), then O += V(t)^T P(t) and l += 1^T P(t) (the row
 //      sums as an MFMA against a ones operand);
-//   4. waits for its loads and meets the other waves at a barrier.
+//   4. waits for its loads except V(t+2)'s, which have until the end of step t+1 (every
+//      wave issues the same number of loads per tile, so vmcnt leaves exactly those in
+//      flight), and meets the other waves at a barrier.
 // The loads are issued with inline asm: the compiler cannot tell the LDS writes of a
 // global_load_lds builtin from the V reads of the same iteration and would otherwise
 // wait for every outstanding load before the first V read; ordering is enforced here
@@ -737,7 +739,7 @@ struct Mfma3Cfg {
   static constexpr int RPI = 64 / CPR;        // rows per wave-wide direct load
   static constexpr int NINST = BK / RPI;      // wave-wide loads per tile per tensor
   static constexpr int NPW = (NINST + NW - 1) / NW;  // ... per wave
-  static constexpr int LDS_BYTES = 4 * TILEB;  // K[2], V[2]
+  static constexpr int LDS_BYTES = 5 * TILEB;  // K[2], V[3]
   static constexpr int KC = (D + 31) / 32;
   static constexpr int NDB = D / 16;
   static constexpr int NKB = BK / 16;
@@ -756,7 +758,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
   char* const kbuf = smem_raw;                   // [2][TILEB]
-  char* const vbuf = smem_raw + 2 * C::TILEB;    // [2][TILEB]
+  char* const vbuf = smem_raw + 2 * C::TILEB;    // [3][TILEB]
 
   WorkItem w;
   if (!resolve_work(p, units, n_units, C::BQ, w)) return;
@@ -847,7 +849,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
 #pragma unroll
     for (int j = 0; j < C::NPW; ++j) {
       const int row = drow0 + j * NW * C::RPI;
-      ofs[j] = (uint32_t)min(row, last) * rowb + 16 * ((lane % C::CPR) ^ kv_swz<D>(row));
+      ofs[j] = (uint32_t)__umul24((uint32_t)min(row, last), rowb) + 16 * ((lane % C::CPR) ^ kv_swz<D>(row));
     }
   };
   auto cursor_seg = [&](Cursor& cr, int sg, bool is_v) {
@@ -865,11 +867,20 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     cr.left -= skip;
     cr.p += (size_t)skip * cr.rowb;
   };
+  // lane offsets of a whole tile at the main segment's K row pitch (the common case)
+  const uint32_t oc_rowb = __builtin_amdgcn_readfirstlane((uint32_t)w.seg[1].ksn * 2u);
+  uint32_t oc[C::NPW];
+  lane_offsets(oc_rowb, BK, oc);
   // load the cursor's tile into LDS dst and advance to the next tile
   auto fetch = [&](Cursor& cr, char* dst, bool is_v) {
     const uint32_t lds0 = lds_addr(dst);
     uint32_t ofs[C::NPW];
-    lane_offsets(cr.rowb, cr.left - 1, ofs);
+    if (cr.left >= BK && cr.rowb == oc_rowb) {
+#pragma unroll
+      for (int j = 0; j < C::NPW; ++j) ofs[j] = oc[j];
+    } else {
+      lane_offsets(cr.rowb, cr.left - 1, ofs);
+    }
 #pragma unroll
     for (int j = 0; j < C::NPW; ++j) {
       const int i = wave + j * NW;
@@ -905,8 +916,6 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
   pin(ones);  // keep in registers rather than rematerialised per use
 
-  // One pipeline step: sc holds S(t); computes sn = S(t+1) from kn, consumes V(t) at vt,
-  // refills kdst with K(t+2) and vdst with V(t+1).
   // raw row maxima of a score tile (before the scale); rows past a segment end repeat
   // its last valid row, so they never change a maximum
   auto row_max = [&](const f32x4 (&sx)[C::NKB][QB], float (&mx)[QB]) {
@@ -920,14 +929,24 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     }
   };
 
+  // end of step t: wait for every load but V(t+2)'s (needed only at step t+2; loads
+  // complete in issue order, and they were issued last).  When the waves issue unequal
+  // numbers of loads (tiny tiles), wait for all.
+  auto vwait = [&](int t) {
+    constexpr int VPW = C::NINST / NW;
+    if (C::NINST % NW == 0 && t + 2 < te)
+      __builtin_amdgcn_s_waitcnt((VPW & 15) | (7 << 4) | (15 << 8) | ((VPW >> 4) << 14));
+    else
+      __builtin_amdgcn_s_waitcnt(0);
+  };
   // One pipeline step: sc holds S(t) and mx its row maxima; computes sn = S(t+1) from kn
-  // and its maxima, consumes V(t) at vt, refills kdst with K(t+2) and vdst with V(t+1).
+  // and its maxima, consumes V(t) at vt, refills kdst with K(t+2) and vdst with V(t+2).
   auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
                   const char* kn, const char* vt, char* kdst, char* vdst) {
     if (t + 2 < te) fetch(kcur, kdst, false);
-    if (t + 1 < te) fetch(vcur, vdst, true);
+    if (t + 2 < te) fetch(vcur, vdst, true);
     if (!wave_active) {  // every query row of this wave is padding: loads and barriers only
-      __builtin_amdgcn_s_waitcnt(0);
+      vwait(t);
       __syncthreads();
       return;
     }
@@ -1055,7 +1074,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) sbase[qb] = m_i[qb];
-    __builtin_amdgcn_s_waitcnt(0);
+    vwait(t);
     __syncthreads();
   };
 
@@ -1067,6 +1086,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     fetch(kcur, kbuf, false);
     fetch(vcur, vbuf, true);
     if (te - tb > 1) fetch(kcur, kbuf + C::TILEB, false);
+    if (te - tb > 1) fetch(vcur, vbuf + C::TILEB, true);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (wave_active) {
@@ -1077,7 +1097,9 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   }
   for (int t = tb; t < te; ++t) {
     const int cur = ((t - tb) & 1) * C::TILEB, nxt = C::TILEB - cur;
-    step(t, sa, sb, mx, kbuf + nxt, vbuf + cur, kbuf + cur, vbuf + nxt);
+    const int v3 = (t - tb) % 3;
+    const int vc = v3 * C::TILEB, vd = (v3 == 0 ? 2 : v3 - 1) * C::TILEB;
+    step(t, sa, sb, mx, kbuf + nxt, vbuf + vc, kbuf + cur, vbuf + vd);
 #pragma unroll
     for (int kb = 0; kb < C::NKB; ++kb)
 #pragma unroll
