@@ -376,6 +376,10 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 FMLM_DEV s16x4 lds_read_tr16(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLM_LDS s16x4*)(p));
 }
+// the same from an LDS byte address
+FMLM_DEV s16x4 lds_read_tr16_at(uint32_t a) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLM_LDS s16x4*)(uintptr_t)a);
+}
 
 template <typename T, int D, int QB, int NW, int BK>
 struct MfmaCfg {
@@ -1155,246 +1159,220 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// MLA kernel for a 512-wide latent (K = V = one latent row shared by all heads).
-//
-// Q and O of 16+ rows x 512 columns do not fit one wave's registers next to each
-// other, so a workgroup of 8 waves covers 64 query rows of one head as 2 row groups
-// x 4 slices.  Per 64-key tile, wave (rg, s):
-//   S^T for the 16 keys [16s, 16s+16) x its group's 32 rows (Q in registers, full D),
-//   row max and P exchanged with the group's other slices through LDS,
-//   O^T for the 128 columns [128s, 128s+128) x 32 rows over all 64 keys.
-// The latent tile (64 rows x 1 KiB) is fetched with direct-to-LDS loads into a
-// double-buffered, XOR-swizzled layout (16-byte chunk c of row r lives at c ^ swz(r)),
-// which keeps both the b128 K reads and the tr16 V reads free of bank conflicts.
+// MLA kernel for a 512-wide latent (K = V = one latent row shared by all heads), whole
+// rows per wave: 8 waves x 16 query rows = 128 rows of one head share every 64-key latent
+// tile loaded into LDS.  Filling those 64 KiB tiles is what bounds an MLA kernel (a
+// workgroup of 64 rows that splits the 512 columns over its waves spent ~20% of its time
+// on them), so the rows per tile matter more than anything else.  Wave w owns rows
+// [16w, 16w+16) end to end: S^T for all 64 keys over the full 512-wide dot product (Q in
+// registers), the online softmax in its own lanes, and O^T for all 512 columns (128
+// accumulator registers), so the waves never exchange scores.  K = V: one tile feeds the
+// b128 K reads of S^T and the tr16 V reads of O^T, with the pipelined kernel's swizzle
+// (kv_swz).  Both MFMA phases read their LDS fragments LEAD slots ahead, in fenced slots
+// (at ~246 VGPRs the compiler would otherwise read each fragment just before its MFMA).
 // ---------------------------------------------------------------------------
-struct MlaCfg {
+struct MlaRowsCfg {
   static constexpr int D = 512;
-  static constexpr int NT = 512;         // 8 waves
-  static constexpr int BQ = 64;          // query rows per workgroup
-  static constexpr int BK = 64;          // keys per tile
-  static constexpr int ROW_BYTES = D * 2;
-  static constexpr int TILE_BYTES = BK * ROW_BYTES;          // 64 KiB
-  static constexpr int PS = BK + 8;                          // P row stride (elements)
-  static constexpr int P_BYTES = 2 * 32 * PS * 2;            // [rg][32 rows][PS] 16-bit
-  static constexpr int RED_BYTES = 2 * 4 * 32 * 4;           // [rg][slice][32 rows] fp32
-  static constexpr int LDS_BYTES = 2 * TILE_BYTES + P_BYTES + RED_BYTES;
+  static constexpr int NW = 8;
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = NW * 16;       // query rows per workgroup
+  static constexpr int BK = 64;            // keys per tile
+  static constexpr int ROWB = D * 2;
+  static constexpr int TILEB = BK * ROWB;  // 64 KiB
+  static constexpr int KC = D / 32;        // 32-wide contraction steps of S^T
+  static constexpr int NDB = D / 16;       // 16-column blocks of O^T
+  static constexpr int NKB = BK / 16;      // 16-key blocks of S^T
+  static constexpr int NKS = BK / 32;      // 32-key steps of O^T
+  static constexpr int LDS_BYTES = 2 * TILEB;
 };
 
-FMLM_DEV int mla_swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
-
 template <typename T>
-__global__ __launch_bounds__(MlaCfg::NT, 1) void attn_mla512_kernel(const fmlm_attn_params p,
-                                                                   const int4* __restrict__ units,
-                                                                   const int32_t* __restrict__ n_units) {
-  typedef MlaCfg C;
+__global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
+    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
+  typedef MlaRowsCfg C;
   typedef typename Mfma<T>::v8 v8;
   constexpr int D = C::D, BK = C::BK;
   extern __shared__ __align__(16) char smem_raw[];
-  char* const tiles = smem_raw;                                    // 2 stages
-  T* const Ps = (T*)(smem_raw + 2 * C::TILE_BYTES);                // [rg][32][PS]
-  float* const red = (float*)(smem_raw + 2 * C::TILE_BYTES + C::P_BYTES);  // [rg][4][32]
 
   WorkItem w;
   if (!resolve_work(p, units, n_units, C::BQ, w)) return;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int rg = wave >> 2, sl = wave & 3;  // row group, slice
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
-  const float c = fmaxf(fabsf(p.scale) * kLog2e, 1e-30f);
+  const int row = wave * 16 + l16;  // the query row of this lane's S^T / O^T column
+  const bool wave_active = wave * 16 < w.qcount;
 
-  // ---- Q fragments of this row group's 32 rows (2 blocks of 16), full D
-  v8 qf[2][D / 32];
-  const char* qbase = (const char*)p.q;
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int row = rg * 32 + qb * 16 + l16;
+  // ---- Q^T fragments (B operand of S^T = K Q^T) for step kc, pre-scaled by
+  // scale*log2(e) (one rounding to the input type): S comes out in log2 units
+  const float cs = p.scale * kLog2e;
+  v8 qf[C::KC];
+  {
     const bool ok = row < w.qcount;
-    const int64_t off = w.q_row0 + (int64_t)row * w.q_sn;
+    const char* src = (const char*)p.q + (w.q_row0 + (int64_t)row * w.q_sn) * 2;
 #pragma unroll
-    for (int kc = 0; kc < D / 32; ++kc) {
-      u32x4 raw = u32x4{0u, 0u, 0u, 0u};
-      if (ok) raw = *(const u32x4*)(qbase + (off + kc * 32 + g * 8) * 2);
-      raw ^= qsign;
-      qf[qb][kc] = __builtin_bit_cast(v8, raw);
+    for (int kc = 0; kc < C::KC; ++kc) {
+      v8 raw = v8{};
+      if (ok) raw = *(const v8*)(src + (kc * 32 + g * 8) * 2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) raw[e] = (T)((float)raw[e] * cs);
+      qf[kc] = raw;
     }
   }
-  f32x4 o[8][2];
-#pragma unroll
-  for (int db = 0; db < 8; ++db)
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_i[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.f, 0.f};
+  // ---- per-lane LDS offsets (kv_swz layout, 1 KiB rows): the K fragment of block kb,
+  // step kc is at (kk ^ 64*(kc%4)) + kb*16*ROWB + 256*(kc/4); the V tr16 fragment of step
+  // ks, column block db, half h at (vv ^ 32*(db%8)) + (32 ks + 16 h)*ROWB + 256*(db/8).
+  // The XOR terms select the swizzled 16-byte chunk; they touch bits 5..7 only, which the
+  // row and stage offsets leave clear.
+  int kk, vv;
+  {
+    const int ksw = kv_swz<D>(l16);
+    kk = l16 * C::ROWB + 64 * (ksw >> 2) + 16 * (g ^ (ksw & 3));
+    const int vr = 4 * g + (l16 >> 2);
+    const int vsw = kv_swz<D>(vr);
+    const int x = (l16 & 3) >> 1;
+    vv = vr * C::ROWB + 32 * (vsw >> 1) + 16 * (x ^ (vsw & 1)) + 8 * (l16 & 1);
+  }
+  constexpr int LEAD = 3;  // LDS fragment reads in flight ahead of their MFMA
 
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
   const int ntiles = nt0 + nt1;
 
-  // direct-to-LDS fetch of tile t into stage st: wave w loads rows 8w..8w+7, lane l
-  // brings the logical chunk l ^ swz(row) so that physical chunk l holds it
+  // ---- direct loads of tile t into stage st: wave w brings rows w + 8j, one 1 KiB row
+  // per load; lane l fetches logical chunk l ^ kv_swz(row), which lands in physical chunk
+  // l.  Rows past a segment end repeat its last row (their scores are masked).  Issued
+  // from inline asm like the pipelined kernel's loads; the wait + barrier at the end of
+  // each tile orders them.
   auto fetch = [&](int t, int st) {
-    const KvSeg& s = t < nt0 ? w.seg[0] : w.seg[1];
-    const int j0 = (t < nt0 ? t : t - nt0) * BK;
+    const int sg = t < nt0 ? 0 : 1;
+    const KvSeg& s = w.seg[sg];
+    const int j0 = (sg == 0 ? t : t - nt0) * BK;
+    const int last = __builtin_amdgcn_readfirstlane(s.n - 1);
     const char* base = s.k + s.kbase * 2;
+    const uint32_t lds0 = lds_addr(smem_raw + st * C::TILEB);
 #pragma unroll
-    for (int rr = 0; rr < 8; ++rr) {
-      const int row = wave * 8 + rr;
-      const int key = min(j0 + row, s.n - 1);  // rows past the end repeat a valid row (masked)
-      const char* src = base + ((int64_t)key * s.ksn) * 2 + ((lane ^ mla_swz(row)) << 4);
-      __builtin_amdgcn_global_load_lds((const void*)src,
-                                       (FMLM_LDS void*)(tiles + st * C::TILE_BYTES + row * C::ROW_BYTES),
-                                       16, 0, 0);
+    for (int j = 0; j < BK / C::NW; ++j) {
+      const int r = wave + j * C::NW;
+      const int key = min(j0 + r, last);
+      dma16_sbase(uniform_ptr(base + (int64_t)key * s.ksn * 2), (uint32_t)((lane ^ kv_swz<D>(r)) << 4),
+                  __builtin_amdgcn_readfirstlane(lds0 + r * C::ROWB));
     }
   };
 
-  // Per-lane byte offsets inside a tile (see mla_swz).  K: row 16 sl + l16, 16-byte
-  // chunk 4(4a + b) + g lives at koff[b] + 256 a.  V: rows 8g + l16/4 (+4), columns
-  // 128 sl + 16 db + 4 (l16 % 4) live at voff[db] (and voff[db ^ 4] + 4 rows).
-  int koff[4], voff[8];
-  {
-    const int krow = sl * 16 + l16;
-    const int sw = mla_swz(krow);
+  f32x4 o[C::NDB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
-      koff[b] = krow * C::ROW_BYTES + 64 * (b ^ (sw >> 2)) + 16 * (g ^ (sw & 3));
-    const int r7 = l16 >> 2;  // swz of row 8g + r7 is 2 r7 + (g & 1)
-    const int low = ((l16 & 3) >> 1) ^ (g & 1);
-#pragma unroll
-    for (int db = 0; db < 8; ++db)
-      voff[db] = (8 * g + r7) * C::ROW_BYTES + 256 * sl + 32 * (db ^ r7) + 16 * low + (l16 & 1) * 8;
-  }
+  for (int db = 0; db < C::NDB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_i = -INFINITY, l_i = 0.f;
 
   if (ntiles > 0) fetch(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    const int st = t & 1;
-    const char* tile = tiles + st * C::TILE_BYTES;
-    if (t + 1 < ntiles) fetch(t + 1, st ^ 1);
-    const int nk = t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
-
-    // ---- S^T for keys [16 sl, 16 sl + 16) x 32 rows (MFMA phases run at raised wave
-    // priority so the other waves' exchanges and softmax fill the gaps)
-    __builtin_amdgcn_s_setprio(1);
-    f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const char* tile = smem_raw + (t & 1) * C::TILEB;
+    if (t + 1 < ntiles) fetch(t + 1, (t + 1) & 1);
+    if (wave_active) {
+      // ---- S^T = K Q^T for the tile's 64 keys x this wave's 16 rows
+      // K fragment f = 4 kc + kb; each slot issues the read of fragment f + LEAD, then
+      // the MFMA of fragment f (sched_barrier fences keep that order)
+      const uint32_t ktile = lds_addr(tile) + kk;
+      auto kread = [&](int f) {
+        const int kc = f / C::NKB, kb = f % C::NKB;
+        const uint32_t a = (ktile ^ (64 * (kc & 3))) + kb * 16 * C::ROWB + 256 * (kc >> 2);
+        return *(const FMLM_LDS v8*)(uintptr_t)a;
+      };
+      constexpr int NF = C::KC * C::NKB;
+      v8 fr[LEAD + 1];
 #pragma unroll
-    for (int a = 0; a < D / 128; ++a) {
+      for (int r = 0; r < LEAD; ++r) fr[r] = kread(r);
+      __builtin_amdgcn_s_setprio(1);
+      f32x4 s[C::NKB];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int kc = a * 4 + b;
-        const v8 kf = *(const v8*)(tile + koff[b] + a * 256);
-        s[0] = Mfma<T>::run(kf, qf[0][kc], s[0]);
-        s[1] = Mfma<T>::run(kf, qf[1][kc], s[1]);
+      for (int kb = 0; kb < C::NKB; ++kb) s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        if (f + LEAD < NF) fr[(f + LEAD) % (LEAD + 1)] = kread(f + LEAD);
+        s[f % C::NKB] = Mfma<T>::run(fr[f % (LEAD + 1)], qf[f / C::NKB], s[f % C::NKB]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    __builtin_amdgcn_s_setprio(0);
-    if (nk < BK) {
+      __builtin_amdgcn_s_setprio(0);
+      const int nk = t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
+      if (nk < BK) {
+        const int lim = nk - 4 * g;  // key kb*16 + 4g + r is valid iff kb*16 + r < lim
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (sl * 16 + g * 4 + r >= nk) {
-          s[0][r] = -INFINITY;
-          s[1][r] = -INFINITY;
+        for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kb * 16 + r >= lim) s[kb][r] = -INFINITY;
+      }
+      // the first V fragments load while the softmax runs
+      const uint32_t vtile = lds_addr(tile) + vv;
+      auto vread = [&](int f) {
+        const int ks = f / C::NDB, db = f % C::NDB;
+        const uint32_t a = (vtile ^ (32 * (db & 7))) + ks * 32 * C::ROWB + 256 * (db >> 3);
+        const s16x4 lo = lds_read_tr16_at(a);
+        const s16x4 hi = lds_read_tr16_at(a + 16 * C::ROWB);
+        return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      };
+      constexpr int NG = C::NKS * C::NDB;
+#pragma unroll
+      for (int r = 0; r < LEAD; ++r) fr[r] = vread(r);
+      // ---- online softmax: lane (l16, g) holds keys kb*16 + 4g + r of row l16
+      float mx = vmax(vmax(s[0][0], s[0][1]), vmax(s[0][2], s[0][3]));
+#pragma unroll
+      for (int kb = 1; kb < C::NKB; ++kb)
+        mx = vmax(vmax(mx, vmax(s[kb][0], s[kb][1])), vmax(s[kb][2], s[kb][3]));
+      mx = lane_max_xor16_32(mx);
+      const bool grow = mx > m_i + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float m_new = grow ? mx : m_i;
+        const float alpha = fast_exp2(m_i - m_new);  // 1 where unchanged, 0 on the first tile
+        m_i = m_new;
+        l_i *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) o[db] *= alpha;
+      }
+      // P^T fragment of key step ks: element (kb&1)*4 + r is key 32 ks + 16 (kb&1) + 4g + r,
+      // the key order of the V^T fragments (two tr16 reads 16 rows apart)
+      u32x4 pf[C::NKS];
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          f32x2 x = f32x2{fast_exp2(s[kb][r] - m_i), fast_exp2(s[kb][r + 1] - m_i)};
+          l_i += x[0] + x[1];
+          pf[kb >> 1][(kb & 1) * 2 + (r >> 1)] =
+              __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
         }
-    }
-    // ---- row max across the 4 slices of the row group
+      // ---- O^T += V^T P^T over the tile's 64 keys, all 512 columns; V fragment
+      // f = 32 ks + db, read LEAD slots ahead like the K fragments
+      __builtin_amdgcn_s_setprio(2);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      float mx = fmaxf(fmaxf(s[qb][0], s[qb][1]), fmaxf(s[qb][2], s[qb][3]));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if (g == 0) red[(rg * 4 + sl) * 32 + qb * 16 + l16] = mx;
-    }
-    __syncthreads();
-    bool need_rescale = false;
-    float m_new[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int r = qb * 16 + l16;
-      float mx = fmaxf(fmaxf(red[(rg * 4 + 0) * 32 + r], red[(rg * 4 + 1) * 32 + r]),
-                       fmaxf(red[(rg * 4 + 2) * 32 + r], red[(rg * 4 + 3) * 32 + r]));
-      mx *= c;
-      const bool grow = mx > m_i[qb] + kRescaleSlack;
-      m_new[qb] = grow ? mx : m_i[qb];
-      need_rescale = need_rescale || grow;
-    }
-    if (__builtin_amdgcn_ballot_w64(need_rescale)) {
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const float alpha = fast_exp2(m_i[qb] - m_new[qb]);
-        m_i[qb] = m_new[qb];
-        l_i[qb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) o[db][qb] *= alpha;
+      for (int f = 0; f < NG; ++f) {
+        if (f + LEAD < NG) fr[(f + LEAD) % (LEAD + 1)] = vread(f + LEAD);
+        o[f % C::NDB] = Mfma<T>::run(fr[f % (LEAD + 1)], __builtin_bit_cast(v8, pf[f / C::NDB]), o[f % C::NDB]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
-    // ---- P for this slice's keys -> LDS as P[row][key]
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const float mneg = -m_i[qb];
-      T pv4[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pv = fast_exp2(fmaf(s[qb][r], c, mneg));
-        l_i[qb] += pv;
-        pv4[r] = (T)pv;
-      }
-      *(u32x2*)(Ps + (rg * 32 + qb * 16 + l16) * C::PS + sl * 16 + g * 4) = *(const u32x2*)pv4;
-    }
-    __syncthreads();
-
-    // ---- O^T[128 sl + 16 db + i][row] += V^T P^T over the 64 keys; key order within a
-    // 32-key step: lane group g owns keys 8g..8g+7 (P: one b128 read, V: two tr16 reads,
-    // rows 8g + j/4 and 8g + 4 + j/4, the second at voff[db ^ 4] + 4 rows)
-    __builtin_amdgcn_s_setprio(2);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v8 pb[2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-        pb[qb] = *(const v8*)(Ps + (rg * 32 + qb * 16 + l16) * C::PS + ks * 32 + g * 8);
-      const char* vt = tile + ks * 32 * C::ROW_BYTES;
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        const s16x4 lo = lds_read_tr16(vt + voff[db]);
-        const s16x4 hi = lds_read_tr16(vt + voff[db ^ 4] + 4 * C::ROW_BYTES);
-        const v8 a = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[db][0] = Mfma<T>::run(a, pb[0], o[db][0]);
-        o[db][1] = Mfma<T>::run(a, pb[1], o[db][1]);
-      }
-    }
-    __builtin_amdgcn_s_setprio(0);
-    __builtin_amdgcn_s_waitcnt(0);  // next stage landed
-    __syncthreads();                // this stage, P and the max slots are free
+    __builtin_amdgcn_s_waitcnt(0);  // tile t+1 landed
+    __syncthreads();                // and every wave is done with tile t
   }
 
-  // ---- epilogue: l summed over the 4 slices, O /= l, store this slice's columns
+  // ---- epilogue: l over the 4 lanes holding the row's keys, O /= l, store the row
+  l_i += __shfl_xor(l_i, 16);
+  l_i += __shfl_xor(l_i, 32);
+  if (row < w.qcount) {
+    const float inv = l_i > 0.f ? 1.f / l_i : 1.f;
+    char* dst = (char*)p.o + (w.o_row0 + (int64_t)row * w.o_sn) * 2;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    float l = l_i[qb];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    if (g == 0) red[(rg * 4 + sl) * 32 + qb * 16 + l16] = l;
-  }
-  __syncthreads();
-  char* obase = (char*)p.o;
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int r = qb * 16 + l16;
-    const float l = red[(rg * 4 + 0) * 32 + r] + red[(rg * 4 + 1) * 32 + r] +
-                    red[(rg * 4 + 2) * 32 + r] + red[(rg * 4 + 3) * 32 + r];
-    const float inv = l > 0.f ? 1.f / l : 1.f;
-    const int row = rg * 32 + r;
-    if (row >= w.qcount) continue;
-    const int64_t off = w.o_row0 + (int64_t)row * w.o_sn;
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
+    for (int db = 0; db < C::NDB; ++db) {
       T v4[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v4[e] = (T)(o[db][qb][e] * inv);
-      *(u32x2*)(obase + (off + sl * 128 + db * 16 + g * 4) * 2) = *(const u32x2*)v4;
+      for (int r = 0; r < 4; ++r) v4[r] = (T)(o[db][r] * inv);
+      *(u32x2*)(dst + (db * 16 + g * 4) * 2) = *(const u32x2*)v4;
     }
   }
 }
@@ -1604,8 +1582,8 @@ static Launch mfma3_launch() {
 }
 
 template <typename T>
-static Launch mla512_launch() {
-  return Launch{MlaCfg::BQ, MlaCfg::NT, MlaCfg::LDS_BYTES, (const void*)&attn_mla512_kernel<T>};
+static Launch mla_rows_launch() {
+  return Launch{MlaRowsCfg::BQ, MlaRowsCfg::NT, MlaRowsCfg::LDS_BYTES, (const void*)&attn_mla_rows_kernel<T>};
 }
 
 // MFMA kernels by head dim.  The pipelined kernel and the 512-wide latent kernel need
@@ -1633,7 +1611,7 @@ static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
     case 256: L = mfma3_launch<T, 256, 1, 4, 64>(); return true;
     case 512:
       if (!(p.flags & FMLM_FLAG_MLA)) return false;
-      L = mla512_launch<T>();
+      L = mla_rows_launch<T>();
       return true;
     default: return false;
   }
