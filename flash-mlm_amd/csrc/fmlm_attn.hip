@@ -1274,87 +1274,114 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
     const char* tile = smem_raw + (t & 1) * C::TILEB;
     if (t + 1 < ntiles) fetch(t + 1, (t + 1) & 1);
     if (wave_active) {
-      // ---- S^T = K Q^T for the tile's 64 keys x this wave's 16 rows
-      // K fragment f = 4 kc + kb; each slot issues the read of fragment f + LEAD, then
-      // the MFMA of fragment f (sched_barrier fences keep that order)
+      // Four phases of 32 fenced slots: slot f issues the LDS read of fragment f + LEAD
+      // and the MFMA of fragment f.  K fragments f < 64 build S^T: half h = f / 32 covers
+      // key blocks 2h, 2h+1 (f = 32 h + 2 kc + kb % 2).  V fragments f = 64 + 32 ks + db
+      // build O^T from the P of key step ks.  Half 0's softmax runs beside half 1's S
+      // MFMAs, half 1's beside the key-step-0 P V MFMAs, so no phase waits on exp.
       const uint32_t ktile = lds_addr(tile) + kk;
-      auto kread = [&](int f) {
-        const int kc = f / C::NKB, kb = f % C::NKB;
-        const uint32_t a = (ktile ^ (64 * (kc & 3))) + kb * 16 * C::ROWB + 256 * (kc >> 2);
-        return *(const FMLM_LDS v8*)(uintptr_t)a;
-      };
-      constexpr int NF = C::KC * C::NKB;
-      v8 fr[LEAD + 1];
-#pragma unroll
-      for (int r = 0; r < LEAD; ++r) fr[r] = kread(r);
-      __builtin_amdgcn_s_setprio(1);
-      f32x4 s[C::NKB];
-#pragma unroll
-      for (int kb = 0; kb < C::NKB; ++kb) s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        if (f + LEAD < NF) fr[(f + LEAD) % (LEAD + 1)] = kread(f + LEAD);
-        s[f % C::NKB] = Mfma<T>::run(fr[f % (LEAD + 1)], qf[f / C::NKB], s[f % C::NKB]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      __builtin_amdgcn_s_setprio(0);
-      const int nk = t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
-      if (nk < BK) {
-        const int lim = nk - 4 * g;  // key kb*16 + 4g + r is valid iff kb*16 + r < lim
-#pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (kb * 16 + r >= lim) s[kb][r] = -INFINITY;
-      }
-      // the first V fragments load while the softmax runs
       const uint32_t vtile = lds_addr(tile) + vv;
-      auto vread = [&](int f) {
-        const int ks = f / C::NDB, db = f % C::NDB;
+      auto fread = [&](int f) -> v8 {
+        if (f < 64) {
+          const int kc = (f & 31) >> 1, kb = 2 * (f >> 5) + (f & 1);
+          const uint32_t a = (ktile ^ (64 * (kc & 3))) + kb * 16 * C::ROWB + 256 * (kc >> 2);
+          return *(const FMLM_LDS v8*)(uintptr_t)a;
+        }
+        const int ks = (f - 64) >> 5, db = (f - 64) & 31;
         const uint32_t a = (vtile ^ (32 * (db & 7))) + ks * 32 * C::ROWB + 256 * (db >> 3);
         const s16x4 lo = lds_read_tr16_at(a);
         const s16x4 hi = lds_read_tr16_at(a + 16 * C::ROWB);
         return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       };
-      constexpr int NG = C::NKS * C::NDB;
+      const int nk = t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
+      f32x4 s[C::NKB];
 #pragma unroll
-      for (int r = 0; r < LEAD; ++r) fr[r] = vread(r);
-      // ---- online softmax: lane (l16, g) holds keys kb*16 + 4g + r of row l16
-      float mx = vmax(vmax(s[0][0], s[0][1]), vmax(s[0][2], s[0][3]));
+      for (int kb = 0; kb < C::NKB; ++kb) s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      u32x4 pf[C::NKS];  // P^T of key step ks: element (kb&1)*4 + r is key 32 ks + 16 (kb&1) + 4g + r
+      // P of key block kb, keys 4g + r and 4g + r + 1 (r even), against the running max
+      auto exp_pair = [&](int kb, int r, bool add_l) {
+        if (r == 0) pin(s[kb]);
+        f32x2 x = f32x2{fast_exp2(s[kb][r] - m_i), fast_exp2(s[kb][r + 1] - m_i)};
+        if (add_l) l_i += x[0] + x[1];
+        uint32_t wv = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
+        pin(wv);
+        pf[kb >> 1][(kb & 1) * 2 + (r >> 1)] = wv;
+      };
+      // softmax bookkeeping of half h once its MFMAs are done: mask keys past the tile's
+      // end, row max (lane-local, then over the 4 lanes of the row), lazy rescale.  When
+      // half 1 raises the maximum, half 0's P (already computed) is rescaled like O and
+      // l_i, which holds half 0's sums.
+      auto half_check = [&](int h) {
+        if (nk < BK) {
+          const int lim = nk - 4 * g;  // key kb*16 + 4g + r is valid iff kb*16 + r < lim
 #pragma unroll
-      for (int kb = 1; kb < C::NKB; ++kb)
-        mx = vmax(vmax(mx, vmax(s[kb][0], s[kb][1])), vmax(s[kb][2], s[kb][3]));
-      mx = lane_max_xor16_32(mx);
-      const bool grow = mx > m_i + kRescaleSlack;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float m_new = grow ? mx : m_i;
-        const float alpha = fast_exp2(m_i - m_new);  // 1 where unchanged, 0 on the first tile
-        m_i = m_new;
-        l_i *= alpha;
+          for (int kb = 2 * h; kb < 2 * h + 2; ++kb)
 #pragma unroll
-        for (int db = 0; db < C::NDB; ++db) o[db] *= alpha;
-      }
-      // P^T fragment of key step ks: element (kb&1)*4 + r is key 32 ks + 16 (kb&1) + 4g + r,
-      // the key order of the V^T fragments (two tr16 reads 16 rows apart)
-      u32x4 pf[C::NKS];
-#pragma unroll
-      for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; r += 2) {
-          f32x2 x = f32x2{fast_exp2(s[kb][r] - m_i), fast_exp2(s[kb][r + 1] - m_i)};
-          l_i += x[0] + x[1];
-          pf[kb >> 1][(kb & 1) * 2 + (r >> 1)] =
-              __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
+            for (int r = 0; r < 4; ++r)
+              if (kb * 16 + r >= lim) s[kb][r] = -INFINITY;
         }
-      // ---- O^T += V^T P^T over the tile's 64 keys, all 512 columns; V fragment
-      // f = 32 ks + db, read LEAD slots ahead like the K fragments
+        float mx = vmax(vmax(vmax(s[2 * h][0], s[2 * h][1]), vmax(s[2 * h][2], s[2 * h][3])),
+                        vmax(vmax(s[2 * h + 1][0], s[2 * h + 1][1]), vmax(s[2 * h + 1][2], s[2 * h + 1][3])));
+        mx = lane_max_xor16_32(mx);
+        const bool grow = mx > m_i + kRescaleSlack;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+          const float m_new = grow ? mx : m_i;
+          const float alpha = fast_exp2(m_i - m_new);  // 1 where unchanged, 0 on the first tile
+          m_i = m_new;
+          l_i *= alpha;
+#pragma unroll
+          for (int db = 0; db < C::NDB; ++db) o[db] *= alpha;
+          if (h == 1)  // half 0's P, computed against the old maximum
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              typename Pair<T>::type v = __builtin_bit_cast(typename Pair<T>::type, pf[0][e]);
+              const f32x2 x = __builtin_convertvector(v, f32x2) * alpha;
+              pf[0][e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
+            }
+        }
+      };
+      constexpr int NF = 128;
+      v8 fr[LEAD + 1];
+#pragma unroll
+      for (int r = 0; r < LEAD; ++r) fr[r] = fread(r);
+      auto slot = [&](const int f) {
+        if (f + LEAD < NF) fr[(f + LEAD) % (LEAD + 1)] = fread(f + LEAD);
+        const v8 a = fr[f % (LEAD + 1)];
+        if (f < 64) {
+          const int kb = 2 * (f >> 5) + (f & 1);
+          s[kb] = Mfma<T>::run(a, qf[(f & 31) >> 1], s[kb]);
+          // half 0's P beside half 1's S MFMAs: one exp pair every 8 slots
+          if (f >= 32 && (f & 7) == 7) {
+            const int q = (f - 32) >> 3;
+            exp_pair(q >> 1, (q & 1) * 2, true);
+          }
+        } else {
+          const int ks = (f - 64) >> 5, db = (f - 64) & 31;
+          o[db] = Mfma<T>::run(a, __builtin_bit_cast(v8, pf[ks]), o[db]);
+          // half 1's P beside the key-step-0 P V MFMAs (done before step 1 starts)
+          if (ks == 0 && (db & 7) == 3) {
+            const int q = db >> 3;
+            exp_pair(2 + (q >> 1), (q & 1) * 2, true);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      // four unrolled phases of 32 slots (one 128-slot loop is too large to unroll)
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int f = 0; f < 32; ++f) slot(f);
+      __builtin_amdgcn_s_setprio(0);
+      half_check(0);
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int f = 32; f < 64; ++f) slot(f);
+      __builtin_amdgcn_s_setprio(0);
+      half_check(1);
       __builtin_amdgcn_s_setprio(2);
 #pragma unroll
-      for (int f = 0; f < NG; ++f) {
-        if (f + LEAD < NG) fr[(f + LEAD) % (LEAD + 1)] = vread(f + LEAD);
-        o[f % C::NDB] = Mfma<T>::run(fr[f % (LEAD + 1)], __builtin_bit_cast(v8, pf[f / C::NDB]), o[f % C::NDB]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int f = 64; f < 96; ++f) slot(f);
+#pragma unroll
+      for (int f = 96; f < 128; ++f) slot(f);
       __builtin_amdgcn_s_setprio(0);
     }
     __builtin_amdgcn_s_waitcnt(0);  // tile t+1 landed
