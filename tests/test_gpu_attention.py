@@ -555,6 +555,28 @@ def test_mla_latent512_packed(dtype, mode, device):
     _close(unpack_from_kernel(out, meta, H), ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mla_latent512_rising_scores(dtype, device):
+    """Scores that rise along the keys by more than the rescale slack every 32 keys: each
+    half of every 64-key latent tile raises the running maximum, so the kernel rescales
+    O, l and the already computed P of the tile's first half at every step."""
+    torch.manual_seed(3100)
+    lengths = [300, 77]
+    B, H, N, D = len(lengths), 2, 300, 512
+    q = _randn((B, H, N, D), device, dtype, std=0.5)
+    k = _randn((B, H, N, D), device, dtype, std=0.5)
+    q[..., 0] = 4.0
+    # +12 (log2 units) per 32 keys: 4 * 1.5 * 32 * scale * log2(e)
+    ramp = torch.arange(N, device=device, dtype=torch.float32) * 1.5
+    k[:, 0, :, 0] = ramp.to(dtype)  # MLA: head 0 of k is the latent
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    scale = 1.0 / math.sqrt(D)
+    out = flash_attn_mlm_compressed(q, k, k, H, meta, scale, is_mla=True, block_n=64)
+    assert torch.isfinite(out).all()
+    ref = _packed_oracle(q, k, k, lengths, scale, is_mla=True)
+    _close(unpack_from_kernel(out, meta, H), ref)
+
+
 @pytest.mark.parametrize("cbs", [1, 2])
 def test_mla_latent512_dense(cbs, device):
     torch.manual_seed(3100 + cbs)
