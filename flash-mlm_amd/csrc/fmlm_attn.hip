@@ -61,6 +61,13 @@ struct SeqInfo {
   int ctx, mainlen;  // context keys and main keys it attends to
 };
 
+// context batch of sequence b: ctx_index[b] (clamped) when given, else b for a
+// full-batch context and 0 for a shared one
+FMLM_DEV int ctx_batch_of(const fmlm_attn_params& p, int b) {
+  if (p.ctx_index) return min(max(p.ctx_index[b], 0), max(p.ctx_batch - 1, 0));
+  return p.ctx_batch > 1 ? b : 0;
+}
+
 FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
   const int32_t* cu = p.cu_seqlens_q;
   SeqInfo s;
@@ -74,7 +81,7 @@ FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
   s.len = L;
   s.ctx = 0;
   if (!(p.flags & FMLM_FLAG_PREFILL)) {
-    const int cb = p.ctx_batch > 1 ? b : 0;
+    const int cb = ctx_batch_of(p, b);
     int c0 = 0, c1 = p.ctx_len;
     if (p.cu_seqlens_kv) {
       c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
@@ -302,7 +309,7 @@ FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const i
   c.lookup = false;
   c.n = 0;
   if (!(p.flags & FMLM_FLAG_PREFILL)) {
-    const int cb = p.ctx_batch > 1 ? b : 0;
+    const int cb = ctx_batch_of(p, b);
     int c0 = 0, c1 = p.ctx_len;
     if (p.cu_seqlens_kv) {
       c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
@@ -1777,7 +1784,7 @@ static int check_params(const fmlm_attn_params& p) {
   if (!(p.flags & FMLM_FLAG_PREFILL)) {
     const bool has_ctx = p.cu_seqlens_kv || p.ctx_len > 0;
     if (has_ctx && !p.cu_seqlens_kv && p.ctx_len > 0 && !p.k_ctx) return FMLM_E_ARG;
-    if (p.cu_seqlens_kv && p.ctx_batch < 1) return FMLM_E_ARG;
+    if ((p.cu_seqlens_kv || p.ctx_index) && p.ctx_batch < 1) return FMLM_E_ARG;
   }
   return 0;
 }

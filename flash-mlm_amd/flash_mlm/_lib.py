@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libflash_mlm_hip.so"
 _LIB_PATH = Path(os.environ.get("FMLM_LIB_PATH", Path(__file__).resolve().parent / "_native" / LIB_NAME))
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
@@ -92,6 +92,7 @@ class AttnParams(ctypes.Structure):
         ("workspace", _c_ptr),
         ("workspace_bytes", _c_i64),
         ("schedule", _c_ptr),
+        ("ctx_index", _c_ptr),
     ]
 
 

@@ -113,6 +113,7 @@ def _prepare(
     flags: int,
     inference_cache: InferenceCache | None,
     schedule_cache: dict | None = None,
+    ctx_index: torch.Tensor | None = None,
 ) -> AttnLaunch:
     lib = _lib.load()
     p = _lib.AttnParams()
@@ -127,6 +128,7 @@ def _prepare(
     p.scale = float(scale)
     p.cu_seqlens_q = _lib.ptr(cu_seqlens_q)
     p.cu_seqlens_kv = _lib.ptr(cu_seqlens_kv)
+    p.ctx_index = _lib.ptr(ctx_index)
     p.q = q.data_ptr()
     p.q_sb, p.q_sh, p.q_sn = q_strides
     p.o = out.data_ptr()
@@ -158,13 +160,37 @@ def _prepare(
             ws = _workspace(inference_cache, ws_bytes, q.device)
             p.workspace = None if ws is None else ws.data_ptr()
             p.workspace_bytes = ws_bytes
-    keep = (q, out, k, v, k_ctx, v_ctx, cu_seqlens_q, cu_seqlens_kv, ws, sched)
+    keep = (q, out, k, v, k_ctx, v_ctx, cu_seqlens_q, cu_seqlens_kv, ctx_index, ws, sched)
     return AttnLaunch(lib, p, stream, q.device, keep)
 
 
 def _check_cache_dtype(k_cache: torch.Tensor, q: torch.Tensor) -> None:
     if k_cache.numel() and k_cache.dtype != q.dtype:
         raise ValueError("cached context dtype must match q dtype")
+
+
+def _context_index(context_index, *, b: int, cbs: int, prefill: bool, context_batch_size, device):
+    """Index-mapped context batching: sequence b attends to context batch
+    ``context_index[b]`` of the layer's cached entry (any number of context batches).
+    The reference supports only a shared or a full-batch context and lists this under
+    "variable context batch sizes" on its roadmap (README.md:34-36).  Returns an int32
+    copy on ``device``, or None.  A CPU index is range-checked here; a GPU index is not
+    read back (no host sync) and the kernel clamps it to [0, cbs)."""
+    if context_index is None:
+        return None
+    if prefill:
+        raise ValueError("context_index cannot be combined with prefill=True")
+    if context_batch_size is not None:
+        raise ValueError("context_index and context_batch_size are mutually exclusive")
+    if not isinstance(context_index, torch.Tensor) or context_index.ndim != 1 or context_index.numel() != b:
+        raise ValueError("context_index must be a rank-1 tensor with one entry per sequence")
+    if context_index.dtype not in (torch.int32, torch.int64):
+        raise ValueError("context_index must be an int32 or int64 tensor")
+    if not context_index.is_cuda and context_index.numel():
+        lo, hi = int(context_index.min()), int(context_index.max())
+        if lo < 0 or hi >= cbs:
+            raise ValueError(f"context_index values must lie in [0, {cbs})")
+    return context_index.to(device=device, dtype=torch.int32).contiguous()
 
 
 def flash_attn_mlm(
@@ -180,6 +206,7 @@ def flash_attn_mlm(
     block_n: int = 32,
     auto_tune_tiles: bool = False,
     prefill: bool = False,
+    context_index: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Dense MLM attention: q, k, v [B, H, N, D] -> out [B, H, N, D].
 
@@ -189,12 +216,18 @@ def flash_attn_mlm(
     [context_batch, H, context_len, D] flattened; ``context_batch_size`` 1 shares
     batch 0.  MLA keeps per-head main keys and uses V = K.  ``prefill=True`` skips
     the context and afterwards stores this call's K/V (MLA: head 0 of k) as the
-    layer's new context with context_batch_size = B.
+    layer's new context with context_batch_size = B.  ``context_index`` (int [B], an
+    extension) maps sequence b to cached context batch ``context_index[b]``.
     """
-    return _dense_impl(q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill)[0]
+    return _dense_impl(
+        q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill,
+        context_index=context_index,
+    )[0]
 
 
-def _dense_impl(q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill, run=True):
+def _dense_impl(
+    q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill, run=True, context_index=None
+):
     """Body of :func:`flash_attn_mlm`; returns (out, prepared launch or None)."""
     b, h, n, d = validate_qkv_same_shape_rank4(q, k, v, error_prefix="q/k/v")
     validate_cache_request(prefill=prefill, inference_cache=inference_cache, layer_id=layer_id)
@@ -217,7 +250,10 @@ def _dense_impl(q, k, v, scale, inference_cache, layer_id, is_mla, context_batch
     if cbs is None or cbs < 1:
         raise ValueError("context_batch_size must be >= 1")
     validate_head_dim_supported(d, is_mla=is_mla)
-    if cbs > 1 and cbs < b and not prefill and context_len > 0:
+    ctx_index = _context_index(
+        context_index, b=b, cbs=cbs, prefill=prefill, context_batch_size=context_batch_size, device=q.device
+    )
+    if cbs > 1 and cbs < b and not prefill and context_len > 0 and ctx_index is None:
         raise ValueError("context_batch_size must be 1 or at least the batch size")
     _check_cache_dtype(k_cache, q)
 
@@ -264,6 +300,7 @@ def _dense_impl(q, k, v, scale, inference_cache, layer_id, is_mla, context_batch
             scale=scale,
             flags=flags,
             inference_cache=inference_cache,
+            ctx_index=ctx_index,
         )
 
     if prefill and inference_cache is not None:
@@ -290,7 +327,7 @@ def _dense_impl(q, k, v, scale, inference_cache, layer_id, is_mla, context_batch
     return out, plan
 
 
-def _packed_context(ctx, *, num_heads: int, d: int, is_mla: bool, b: int, prefill: bool):
+def _packed_context(ctx, *, num_heads: int, d: int, is_mla: bool, b: int, prefill: bool, indexed: bool = False):
     """Strides / sizes of a packed (head-major) context entry, validated."""
     total_context_len = int(ctx.total_context_len)
     cu_kv = ctx.cu_seqlens_kv
@@ -301,7 +338,7 @@ def _packed_context(ctx, *, num_heads: int, d: int, is_mla: bool, b: int, prefil
         raise ValueError("context_batch_size must be >= 1")
     if cbs + 1 > cu_kv.numel():
         raise ValueError("context_batch_size is incompatible with cu_seqlens_kv length")
-    if 1 < cbs < b and not prefill and total_context_len > 0:
+    if 1 < cbs < b and not prefill and total_context_len > 0 and not indexed:
         raise ValueError("context_batch_size must be 1 or at least the batch size")
     c_strides = (0, 0 if is_mla else total_context_len * d, d)
     return cbs, c_strides
@@ -323,6 +360,7 @@ def flash_attn_mlm_compressed(
     auto_tune_tiles: bool = False,
     prefill: bool = False,
     causal_query_seq_attn: bool = False,
+    context_index: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Packed variable-length MLM attention over padded q/k/v [B, H, N, D].
 
@@ -333,17 +371,18 @@ def flash_attn_mlm_compressed(
     MLA: main K = V = head 0 of k (``v`` is ignored), context is a shared latent.
     ``prefill=True`` skips the context and stores this call's packed, zero-padded
     K/V [H_kv * T_pad, D] as the layer's context (cu_seqlens_kv = q_meta.cu_seqlens,
-    context_batch_size = B) before the attention runs.
+    context_batch_size = B) before the attention runs.  ``context_index`` (int [B], an
+    extension) maps sequence b to cached context batch ``context_index[b]`` instead.
     """
     return _compressed_impl(
         q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
-        block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn,
+        block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, context_index=context_index,
     )[0]
 
 
 def _compressed_impl(
     q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
-    block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, run=True,
+    block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, run=True, context_index=None,
 ):
     """Body of :func:`flash_attn_mlm_compressed`; returns (out, prepared launch or None)."""
     b, h, n, d = validate_qkv_same_shape_rank4(q, k, v, error_prefix="q/k/v")
@@ -384,7 +423,12 @@ def _compressed_impl(
     )
     validate_head_dim_supported(d, is_mla=is_mla)
     validate_cu_seqlens_rank1_min2(cu_seqlens_q, ctx.cu_seqlens_kv)
-    cbs, c_strides = _packed_context(ctx, num_heads=num_heads, d=d, is_mla=is_mla, b=b, prefill=prefill)
+    cbs, c_strides = _packed_context(
+        ctx, num_heads=num_heads, d=d, is_mla=is_mla, b=b, prefill=prefill, indexed=context_index is not None
+    )
+    ctx_index = _context_index(
+        context_index, b=b, cbs=cbs, prefill=prefill, context_batch_size=context_batch_size, device=q.device
+    )
     num_q_tiles = int(q_meta.q_tile_starts_q.numel())
     if q_meta.batch_ids_q.ndim != 1 or q_meta.batch_ids_q.numel() != num_q_tiles:
         raise ValueError("batch_ids_q must be rank-1 with exactly one entry per query tile")
@@ -501,6 +545,7 @@ def _compressed_impl(
         flags=flags,
         inference_cache=inference_cache,
         schedule_cache=q_meta.kernel_schedules if isinstance(q_meta, PackMetadata) else None,
+        ctx_index=ctx_index,
     )
     return out, plan
 
@@ -524,6 +569,7 @@ def flash_attn_mlm_precompressed(
     auto_tune_tiles: bool = False,
     prefill: bool = False,
     causal_query_seq_attn: bool = False,
+    context_index: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Like :func:`flash_attn_mlm_compressed` for already packed inputs.
 
@@ -569,7 +615,12 @@ def flash_attn_mlm_precompressed(
     )
     validate_head_dim_supported(d, is_mla=is_mla)
     validate_cu_seqlens_rank1_min2(cu_seqlens_q, ctx.cu_seqlens_kv)
-    cbs, c_strides = _packed_context(ctx, num_heads=num_heads, d=d, is_mla=is_mla, b=b, prefill=prefill)
+    cbs, c_strides = _packed_context(
+        ctx, num_heads=num_heads, d=d, is_mla=is_mla, b=b, prefill=prefill, indexed=context_index is not None
+    )
+    ctx_index = _context_index(
+        context_index, b=b, cbs=cbs, prefill=prefill, context_batch_size=context_batch_size, device=q.device
+    )
     num_q_tiles = int(q_tile_starts_q.numel())
     if batch_ids_q.ndim != 1 or batch_ids_q.numel() != num_q_tiles:
         raise ValueError("batch_ids_q must be rank-1 with exactly one entry per query tile")
@@ -613,6 +664,7 @@ def flash_attn_mlm_precompressed(
             | (_lib.FLAG_PREFILL if prefill else 0)
             | (_lib.FLAG_CAUSAL_SEQ if causal_query_seq_attn else 0),
             inference_cache=inference_cache,
+            ctx_index=ctx_index,
         )
 
     if prefill and inference_cache is not None:

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FMLM_ABI_VERSION 1
+#define FMLM_ABI_VERSION 2
 
 /* element types */
 enum {
@@ -142,7 +142,8 @@ FMLM_API int fmlm_unpack(int32_t elem_bytes, const void* packed, int64_t p_sh, v
  * (L_b = cu_seqlens_q[b+1]-cu_seqlens_q[b], or N when cu_seqlens_q == NULL):
  *   keys = [context of b] ++ [main keys of b]
  *   context (skipped with FMLM_FLAG_PREFILL): rows cb*c_sb + h*c_sh + (c0 + j)*c_sn,
- *       j < c1 - c0, where cb = (ctx_batch > 1 ? b : 0) and
+ *       j < c1 - c0, where cb = ctx_index[b] clamped to [0, ctx_batch) when ctx_index
+ *       is set, else (ctx_batch > 1 ? b : 0), and
  *       (c0, c1) = (cu_seqlens_kv[cb], cu_seqlens_kv[cb+1]) clamped to [0, ctx_rows], or
  *       (0, ctx_len) when cu_seqlens_kv == NULL
  *   main: packed token indices [cu_q[b], cu_q[b+1]), or [0, cu_q[b+1]) with
@@ -181,6 +182,10 @@ typedef struct fmlm_attn_params {
                               differ; they only steer where key ranges are split.  The
                               buffer also holds split partial results: launches that may
                               overlap need separate schedule buffers                  */
+  const int32_t* ctx_index;  /* [B] context batch of each sequence, or NULL (see above):
+                                index-mapped context batching.  No counterpart in the
+                                reference, whose roadmap lists it ("variable context
+                                batch sizes", README.md:34-36)                         */
 } fmlm_attn_params;
 
 /* Bytes of device workspace (and of a schedule buffer) fmlm_attn_fwd needs for these

@@ -50,6 +50,7 @@ def mlm_attention_packed(
     cu_seqlens_kv=None,
     total_context_len: int = 0,
     context_batch_size: int = 1,
+    context_index=None,
 ) -> np.ndarray:
     """Packed-path attention on padded q/k/v [B, H, N, D] -> [B, H, N, D] (float64),
     zeros at padding positions.
@@ -58,6 +59,8 @@ def mlm_attention_packed(
     ``h_off + cu_seqlens_kv[cb] .. h_off + cu_seqlens_kv[cb+1]`` of the head-major cache,
     ``cb = b`` if context_batch_size > 1 else 0, ``h_off = h * total_context_len``
     (0 for MLA).  MLA: main K = V = head 0 of k, context V = context K.
+    ``context_index`` (index-mapped context batching, an extension the reference lists on
+    its roadmap, README.md:34-36) sets ``cb = context_index[b]`` instead.
     """
     B, H, N, D = q.shape
     out = np.zeros((B, H, N, D), dtype=np.float64)
@@ -71,7 +74,7 @@ def mlm_attention_packed(
         pb = np.array([r[1] for r in rows])
         c0 = c1 = 0
         if not prefill and cu_kv is not None:
-            cb = b if context_batch_size > 1 else 0
+            cb = int(context_index[b]) if context_index is not None else (b if context_batch_size > 1 else 0)
             c0, c1 = int(cu_kv[cb]), int(cu_kv[cb + 1])
         for h in range(H):
             kh = 0 if is_mla else h
@@ -101,18 +104,20 @@ def mlm_attention_dense(
     v_cache: np.ndarray | None = None,
     context_len: int = 0,
     context_batch_size: int = 1,
+    context_index=None,
 ) -> np.ndarray:
     """Dense-path attention q/k/v [B, H, N, D] -> [B, H, N, D] (float64).
 
     Every query of (b, h) attends to [context || k[b, h, :N]].  Context rows (skipped
     when ``prefill``): MLA ``cb*context_len + [0, context_len)``; otherwise
     ``(cb*H + h)*context_len + [0, context_len)``, cb = b if context_batch_size > 1
-    else 0 (mlm_kernel_impl.py:132-141).  MLA keeps per-head main keys and V = K.
+    else 0 (mlm_kernel_impl.py:132-141), or ``context_index[b]`` when given (the
+    extension above).  MLA keeps per-head main keys and V = K.
     """
     B, H, N, D = q.shape
     out = np.zeros((B, H, N, D), dtype=np.float64)
     for b in range(B):
-        cb = b if context_batch_size > 1 else 0
+        cb = int(context_index[b]) if context_index is not None else (b if context_batch_size > 1 else 0)
         for h in range(H):
             K_main = k[b, h]
             V_main = K_main if is_mla else v[b, h]

@@ -45,14 +45,14 @@ def _randn(shape, device, dtype=torch.float16, std=1.0):
     return (torch.randn(shape, device=device) * std).to(dtype)
 
 
-def _packed_oracle(q, k, v, lengths, scale, *, is_mla=False, causal=False, prefill=False, k_cache=None, v_cache=None, cu_kv=None, cbs=1, Tc=0):
+def _packed_oracle(q, k, v, lengths, scale, *, is_mla=False, causal=False, prefill=False, k_cache=None, v_cache=None, cu_kv=None, cbs=1, Tc=0, context_index=None):
     return ar.mlm_attention_packed(
         _np(q), _np(k), _np(v), [int(x) for x in lengths], scale, is_mla=is_mla,
         causal_query_seq_attn=causal, prefill=prefill,
         k_cache=None if k_cache is None else _np(k_cache),
         v_cache=None if v_cache is None else _np(v_cache),
         cu_seqlens_kv=None if cu_kv is None else [int(x) for x in cu_kv],
-        total_context_len=Tc, context_batch_size=cbs,
+        total_context_len=Tc, context_batch_size=cbs, context_index=context_index,
     )
 
 
@@ -369,6 +369,97 @@ def test_dense_sweep_with_context(dtype, D, is_mla, cbs, device):
     out = flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0, is_mla=is_mla)
     ref = ar.mlm_attention_dense(_np(q), _np(k), _np(v), scale, is_mla=is_mla, k_cache=_np(kc), v_cache=_np(vc), context_len=C, context_batch_size=cbs)
     _close(out, ref)
+
+
+# ---------------------------------------------------------------------------
+# index-mapped context batching (context_index, an extension): sequence b attends to
+# context batch context_index[b] of a cache holding any number of context batches
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("mode", ["plain", "causal", "mla", "gpu_index"])
+def test_context_index_packed(dtype, D, mode, device):
+    torch.manual_seed(4100 + D + len(mode))
+    is_mla, causal = mode == "mla", mode == "causal"
+    lengths = [70, 1, 0, 133, 64]
+    B, H, N = len(lengths), 3, 140
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, dtype) for _ in range(3))
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, is_mla, [40, 0, 129], device, dtype)  # 3 contexts
+    idx = [2, 0, 2, 1, 0]
+    idx_t = torch.tensor(idx, dtype=torch.int32, device=device if mode == "gpu_index" else "cpu")
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, is_mla=is_mla, block_n=64,
+                                    causal_query_seq_attn=causal, context_index=idx_t)
+    ref = _packed_oracle(q, k, v, lengths, scale, is_mla=is_mla, causal=causal, k_cache=kc, v_cache=vc,
+                         cu_kv=cu_kv, cbs=3, Tc=Tc, context_index=idx)
+    _close(unpack_from_kernel(out, meta, H), ref)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_context_index_mla512_and_precompressed(is_mla, device):
+    torch.manual_seed(4200 + is_mla)
+    D = 512 if is_mla else 128
+    lengths = [150, 3, 96]
+    B, H, N = len(lengths), 2, 150
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16, std=0.5) for _ in range(3))
+    torch.manual_seed(9)
+    c1, kc, vc, cu_kv, Tc = _context_cache(B, H, D, is_mla, [65, 200], device, torch.bfloat16, std=0.5)
+    torch.manual_seed(9)
+    c2 = _context_cache(B, H, D, is_mla, [65, 200], device, torch.bfloat16, std=0.5)[0]
+    idx = torch.tensor([1, 1, 0], dtype=torch.int32)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, c1, 0, is_mla=is_mla, block_n=64, context_index=idx)
+    ref = _packed_oracle(q, k, v, lengths, scale, is_mla=is_mla, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=2,
+                         Tc=Tc, context_index=idx.tolist())
+    _close(unpack_from_kernel(out, meta, H), ref)
+    q_p, k_p, v_p = _prepack(q, k, v, meta, is_mla)
+    pre = flash_attn_mlm_precompressed(
+        q_p, k_p, v_p, num_heads=H, total_q_len=q_p.shape[0] // H, cu_seqlens_q=meta.cu_seqlens,
+        batch_ids_q=meta.batch_ids_q, q_tile_starts_q=meta.q_tile_starts_q, scale=scale, inference_cache=c2,
+        layer_id=0, is_mla=is_mla, block_n=64, context_index=idx,
+    )
+    torch.testing.assert_close(pre, out, atol=1e-5, rtol=0)
+
+
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_context_index_dense(is_mla, device):
+    torch.manual_seed(4300 + is_mla)
+    B, H, N, D, C, cbs = 3, 2, 77, 64, 45, 2
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    rows = cbs * C * (1 if is_mla else H)
+    kc, vc = _randn((rows, D), device, torch.bfloat16), _randn((rows, D), device, torch.bfloat16)
+    cache = InferenceCache()
+    cache.prefill_kv_cache(0, k_cache=kc, v_cache=None if is_mla else vc, context_batch_size=cbs, is_mla=is_mla,
+                           num_heads=H, head_dim=D, total_context_len=cbs * C)
+    idx = [1, 1, 0]
+    out = flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0, is_mla=is_mla,
+                         context_index=torch.tensor(idx))
+    ref = ar.mlm_attention_dense(_np(q), _np(k), _np(v), scale, is_mla=is_mla, k_cache=_np(kc), v_cache=_np(vc),
+                                 context_len=C, context_batch_size=cbs, context_index=idx)
+    _close(out, ref)
+
+
+def test_context_index_errors(device):
+    B, H, N, D = 3, 2, 32, 64
+    q, k, v = (_randn((B, H, N, D), device) for _ in range(3))
+    cache = _context_cache(B, H, D, False, [5, 6], device)[0]  # 2 contexts for 3 sequences
+    meta = build_pack_metadata(torch.tensor([32, 10, 20], device=device), N, block_n=32)
+    run = lambda **kw: flash_attn_mlm_compressed(q, k, v, H, meta, 0.3, cache, 0, **kw)  # noqa: E731
+    with pytest.raises(ValueError, match="must be 1 or at least the batch size"):
+        run()  # 2 contexts for 3 sequences need an index
+    with pytest.raises(ValueError, match=r"context_index values must lie in \[0, 2\)"):
+        run(context_index=torch.tensor([0, 2, 1]))
+    with pytest.raises(ValueError, match="one entry per sequence"):
+        run(context_index=torch.tensor([0, 1]))
+    with pytest.raises(ValueError, match="int32 or int64"):
+        run(context_index=torch.tensor([0.0, 1.0, 1.0]))
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        run(context_index=torch.tensor([0, 1, 1]), context_batch_size=1)
+    with pytest.raises(ValueError, match="prefill"):
+        run(context_index=torch.tensor([0, 1, 1]), prefill=True)
 
 
 def test_shared_context_override_on_multi_batch_entry(device):

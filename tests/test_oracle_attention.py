@@ -157,6 +157,46 @@ def test_dense_matches_sdpa_on_explicit_key_sets(mla, cbs, prefill):
             np.testing.assert_allclose(out[b, h], _sdpa(q[b, h], K, V, 0.6), atol=1e-12)
 
 
+@pytest.mark.parametrize("mla", [False, True])
+@pytest.mark.parametrize("causal", [False, True])
+def test_packed_context_index_matches_sdpa_on_explicit_key_sets(mla, causal):
+    """Index-mapped context batching (an extension): sequence b attends to context batch
+    context_index[b] of a 3-batch cache; checked against SDPA on the explicit key set of
+    that batch, and context_index = arange(B) must reproduce the full-batch result."""
+    rng = np.random.default_rng(90 + mla + 2 * causal)
+    c = _packed_case(rng, B=4, mla=mla, cbs=3)
+    idx = np.array([2, 0, 2, 1])
+    scale = 0.41
+    out = _run_packed(c, scale, is_mla=mla, causal_query_seq_attn=causal, context_index=idx)
+    for b in range(4):
+        for h in range(c["q"].shape[1]):
+            K, V = _keys_for(c, b, h, mla=mla, causal=causal, prefill=False, cb=int(idx[b]))
+            np.testing.assert_allclose(out[b, h, : c["L"][b]], _sdpa(c["q"][b, h, : c["L"][b]], K, V, scale), atol=1e-12)
+    full = _packed_case(np.random.default_rng(95 + mla), B=3, mla=mla)
+    np.testing.assert_array_equal(_run_packed(full, 0.3, is_mla=mla, context_index=np.arange(3)),
+                                  _run_packed(full, 0.3, is_mla=mla))
+
+
+@pytest.mark.parametrize("mla", [False, True])
+def test_dense_context_index_matches_sdpa_on_explicit_key_sets(mla):
+    rng = np.random.default_rng(97 + mla)
+    B, H, N, D, ctx, C = 3, 2, 6, 8, 4, 2
+    q, k, v = _rand(rng, B, H, N, D), _rand(rng, B, H, N, D), _rand(rng, B, H, N, D)
+    rows = C * ctx * (1 if mla else H)
+    kc, vc = _rand(rng, rows, D), _rand(rng, rows, D)
+    idx = [1, 1, 0]
+    out = ar.mlm_attention_dense(q, k, v, 0.6, is_mla=mla, k_cache=kc, v_cache=vc, context_len=ctx,
+                                 context_batch_size=C, context_index=idx)
+    for b in range(B):
+        for h in range(H):
+            s = idx[b] * ctx if mla else (idx[b] * H + h) * ctx
+            K_main = k[b, h]
+            V_main = K_main if mla else v[b, h]
+            K = np.concatenate([kc[s : s + ctx], K_main])
+            V = np.concatenate([K[:ctx] if mla else vc[s : s + ctx], V_main])
+            np.testing.assert_allclose(out[b, h], _sdpa(q[b, h], K, V, 0.6), atol=1e-12)
+
+
 def test_effective_flops_formula():
     # 4*H*D*sum Lq*(Lctx+Lmain); causal main = cu_q[b+1]; prefill drops context
     assert ar.effective_flops([2, 3], [5, 1], 2, 4) == 4 * 2 * 4 * (2 * 7 + 3 * 4)
