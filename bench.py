@@ -332,8 +332,9 @@ def _event_ms(fn, reps: int) -> float:
 
 def hbm_kernels(case: Case, reps: int = 30) -> dict:
     """HBM rate of the path's copy kernels on this workload's tensors: unpack_from_kernel
-    (read H*T*D, write B*H*N*D) and pack_and_pad_main_tensors_for_mlm_compressed (per
-    tensor: read heads*T*D, write heads*T_pad*D; MLA packs q and one latent head).
+    (read H*T*D, write B*H*N*D), pack_and_pad_main_tensors_for_mlm_compressed (per
+    tensor: read heads*T*D, write heads*T_pad*D; MLA packs q and one latent head) and the
+    KV append of this step's rows to the cached context (read + write every owned row).
     Algorithmic bytes / median time, against the 8 TB/s HBM peak."""
     import flash_mlm as fm
     from flash_mlm.host import host_utils as hu
@@ -364,6 +365,33 @@ def hbm_kernels(case: Case, reps: int = 30) -> dict:
     out["pack"] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
                    "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
                    "tensors": "q + latent head" if case.is_mla else "q, k, v"}
+
+    # KV append (InferenceCache.append_kv_cache): this step's K/V rows appended to every
+    # context batch of the layer's packed entry; reads and writes every owned row once
+    ent = t["cache"].get_kv_cache(0, is_mla=case.is_mla, num_heads=H, head_dim=D, dtype=case.dtype,
+                                  device=t["q"].device) if "cache" in t else None
+    if ent is not None and ent.cu_seqlens_kv is not None:
+        h_kv = 1 if case.is_mla else H
+        n_batch = int(ent.cu_seqlens_kv.numel()) - 1
+        cu_new = meta.cu_seqlens if n_batch == B else torch.tensor([0, T], dtype=torch.int32, device="cuda")
+        new_k = torch.randn((h_kv * T, D), device="cuda").to(case.dtype)
+        new_v = None if case.is_mla else torch.randn((h_kv * T, D), device="cuda").to(case.dtype)
+
+        def fresh():  # a cache holding (views of) the layer's entry; append replaces it
+            c = fm.InferenceCache()
+            c.prefill_kv_cache(0, k_cache=ent.k_cache, v_cache=ent.v_cache, total_context_len=ent.total_context_len,
+                               cu_seqlens_kv=ent.cu_seqlens_kv, context_batch_size=ent.context_batch_size,
+                               is_mla=case.is_mla, num_heads=H, head_dim=D)
+            return c
+
+        pool = [fresh() for _ in range(reps + 2)]
+        ms = _event_ms(lambda: pool.pop().append_kv_cache(0, k_cache=new_k, v_cache=new_v, cu_seqlens_kv=cu_new),
+                       reps)
+        rows = int(ent.cu_seqlens_kv[-1]) + T
+        nbytes = esz * D * h_kv * (1 if case.is_mla else 2) * 2 * rows
+        out["kv_append"] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                            "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                            "tensors": "latent" if case.is_mla else "k, v"}
     return out
 
 

@@ -237,6 +237,34 @@ __global__ __launch_bounds__(256) void unpack_kernel(const char* __restrict__ pa
   }
 }
 
+// ---------------------------------------------------------------------------
+// Segment copy (KV append): block (TX chunk lanes x TY rows) over grid (row blocks, head,
+// segment).  Segment c of head h: rows [src_cu[c], src_cu[c+1]) of src (head stride src_sh
+// elements) go to rows [dst_start[c], dst_start[c] + len) of dst (head stride dst_sh).
+// Lengths and starts are clamped to the row counts of src and dst, so inconsistent offsets
+// cannot address outside either tensor.  The row blocks stride over the segment, so the
+// grid does not depend on segment lengths the host has not read.
+// ---------------------------------------------------------------------------
+template <int VB>
+__global__ __launch_bounds__(256) void segment_copy_kernel(const char* __restrict__ src, int64_t src_sh,
+                                                           int src_rows, const int32_t* __restrict__ src_cu,
+                                                           char* __restrict__ dst, int64_t dst_sh, int dst_rows,
+                                                           const int32_t* __restrict__ dst_start, int D,
+                                                           int esz) {
+  typedef typename VecOf<VB>::type V;
+  const int cpr = D * esz / VB;
+  const int h = blockIdx.y, c = blockIdx.z;
+  const int s0 = min(max(src_cu[c], 0), src_rows);
+  const int d0 = min(max(dst_start[c], 0), dst_rows);
+  const int len = min(min(src_cu[c + 1] - s0, src_rows - s0), dst_rows - d0);
+  const char* const sbase = src + ((int64_t)h * src_sh + (int64_t)s0 * D) * esz;
+  char* const dbase = dst + ((int64_t)h * dst_sh + (int64_t)d0 * D) * esz;
+  const int64_t row_bytes = (int64_t)D * esz;
+  for (int r = blockIdx.x * blockDim.y + threadIdx.y; r < len; r += gridDim.x * blockDim.y)
+    for (int k = threadIdx.x; k < cpr; k += blockDim.x)
+      *(V*)(dbase + (int64_t)r * row_bytes + (int64_t)k * VB) = *(const V*)(sbase + (int64_t)r * row_bytes + (int64_t)k * VB);
+}
+
 // Block shape for a row-copy kernel: TX lanes across a row's chunks, TY rows.
 static dim3 row_block(int cpr) {
   const int tx = cpr < 256 ? cpr : 256;
@@ -375,5 +403,42 @@ extern "C" int fmlm_unpack(int32_t elem_bytes, const void* packed, int64_t p_sh,
     FMLM_UNPACK_CASE(1)
   }
 #undef FMLM_UNPACK_CASE
+  return launch_status();
+}
+
+extern "C" int fmlm_copy_segments(int32_t elem_bytes, const void* src, int64_t src_sh, int32_t src_rows,
+                                  const int32_t* src_cu, void* dst, int64_t dst_sh, int32_t dst_rows,
+                                  const int32_t* dst_start, int32_t C, int32_t H, int32_t D, void* stream) {
+  const int esz = elem_bytes;
+  if (!valid_elem_bytes(esz)) return FMLM_E_DTYPE;
+  if (C < 0 || H < 0 || D < 1 || src_rows < 0 || dst_rows < 0 || src_sh < 0 || dst_sh < 0) return FMLM_E_ARG;
+  if ((int64_t)C * H == 0 || src_rows == 0 || dst_rows == 0) return 0;
+  if (!src || !dst || !src_cu || !dst_start) return FMLM_E_ARG;
+  if (H > 65535 || C > 65535) return FMLM_E_ARG;
+  const int vb = pick_vec((int64_t)D * esz, {(uint64_t)src, (uint64_t)dst, (uint64_t)(src_sh * esz),
+                                             (uint64_t)(dst_sh * esz)});
+  if (!vb) return FMLM_E_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 blk = row_block((int)((int64_t)D * esz / vb));
+  // enough row blocks per (head, segment) to fill the GPU several times over at the
+  // average segment length; longer segments are covered by the stride loop
+  const int64_t avg = ((int64_t)src_rows + C - 1) / C;
+  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>((avg + blk.y - 1) / blk.y, 4096));
+  const dim3 grid((unsigned)gx, H, C);
+  const char* sp = (const char*)src;
+  char* dp = (char*)dst;
+#define FMLM_SEG_CASE(VB)                                                                              \
+  case VB:                                                                                             \
+    hipLaunchKernelGGL(segment_copy_kernel<VB>, grid, blk, 0, s, sp, src_sh, src_rows, src_cu, dp, dst_sh, \
+                       dst_rows, dst_start, D, esz);                                                    \
+    break;
+  switch (vb) {
+    FMLM_SEG_CASE(16)
+    FMLM_SEG_CASE(8)
+    FMLM_SEG_CASE(4)
+    FMLM_SEG_CASE(2)
+    FMLM_SEG_CASE(1)
+  }
+#undef FMLM_SEG_CASE
   return launch_status();
 }

@@ -128,6 +128,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_c_i32, _c_ptr, _c_i64, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32, _c_ptr, _c_ptr],
     ),
+    "fmlm_copy_segments": (
+        ctypes.c_int,
+        [_c_i32, _c_ptr, _c_i64, _c_i32, _c_ptr, _c_ptr, _c_i64, _c_i32, _c_ptr, _c_i32, _c_i32, _c_i32, _c_ptr],
+    ),
     "fmlm_attn_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(AttnParams)]),
     "fmlm_attn_schedule": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr, _c_i64, _c_ptr]),
     "fmlm_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr]),

@@ -263,6 +263,90 @@ class InferenceCache:
             device=k_cache.device,
         )
 
+    def append_kv_cache(
+        self,
+        layer_id: int | str,
+        *,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor | None = None,
+        cu_seqlens_kv: torch.Tensor,
+    ) -> None:
+        """Append rows to every context batch of ``layer_id``'s packed entry.
+
+        This is an extension: the reference replaces a layer's context on prefill and
+        lists appends with paged KV on its roadmap (README.md:34-41).
+
+        ``k_cache`` / ``v_cache`` hold the new rows head-major like the entry: [T_new, D]
+        for MLA (``v_cache`` must be None), else [H * T_new, D].  Batch c's new rows are
+        ``cu_seqlens_kv[c] .. cu_seqlens_kv[c+1]``.  The entry becomes [old rows of c ||
+        new rows of c] for every batch c: new buffers of T_old + T_new rows per head, and
+        cu_seqlens_kv = old + new offsets.  Rows per head past the last batch are left
+        unwritten (nothing attends to them).  The copy is a HIP segment copy per tensor and
+        source, stream-ordered; nothing is read back to the host.
+        """
+        key = self._layer_key(layer_id)
+        entry = self._layer_kv.get(key)
+        if entry is None:
+            raise ValueError(f"no cached KV entry for layer {layer_id!r}")
+        if entry.cu_seqlens_kv is None:
+            raise ValueError("append_kv_cache requires a packed entry (stored with cu_seqlens_kv)")
+        h_kv = 1 if entry.is_mla else entry.num_heads
+        d = entry.head_dim
+        _check_rank2(k_cache, "k_cache")
+        if k_cache.shape[1] != d:
+            raise ValueError("k_cache second dim must match head_dim")
+        if k_cache.dtype != entry.dtype or k_cache.device != entry.device:
+            raise ValueError("k_cache dtype/device must match the cached entry")
+        if k_cache.shape[0] % h_kv:
+            raise ValueError("non-MLA k_cache rows must be divisible by num_heads")
+        if entry.is_mla:
+            if v_cache is not None:
+                raise ValueError("MLA append takes k_cache only (V = K)")
+        elif v_cache is None or v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype \
+                or v_cache.device != k_cache.device:
+            raise ValueError("non-MLA append requires v_cache shaped like k_cache")
+        n_batch = int(entry.cu_seqlens_kv.numel()) - 1
+        if cu_seqlens_kv.ndim != 1 or int(cu_seqlens_kv.numel()) != n_batch + 1:
+            raise ValueError("cu_seqlens_kv must have one entry per cached context batch, plus one")
+        t_old, t_new = int(entry.total_context_len), int(k_cache.shape[0]) // h_kv
+        if not cu_seqlens_kv.is_cuda:
+            cu_host = cu_seqlens_kv.to(torch.int64)
+            if int(cu_host[0]) != 0 or bool((cu_host[1:] < cu_host[:-1]).any()) or int(cu_host[-1]) > t_new:
+                raise ValueError("cu_seqlens_kv must start at 0, be non-decreasing and end within the new rows")
+        from flash_mlm.host.host_utils import copy_segments
+
+        dev = entry.device
+        cu_old = entry.cu_seqlens_kv.to(device=dev, dtype=torch.int32).contiguous()
+        cu_new = cu_seqlens_kv.to(device=dev, dtype=torch.int32).contiguous()
+        cu_out = cu_old + cu_new
+        start_old = cu_out[:-1].contiguous()            # batch c's old rows open its segment
+        start_new = (cu_old[1:] + cu_new[:-1]).contiguous()  # its new rows follow them
+        rows = t_old + t_new
+
+        def merged(old: torch.Tensor, new: torch.Tensor) -> torch.Tensor:
+            out = torch.empty((h_kv * rows, d), dtype=entry.dtype, device=dev)
+            if n_batch > 0:
+                old = old.contiguous()
+                new = new.contiguous()
+                copy_segments(old, t_old, cu_old, out, rows, start_old, n_batch, h_kv, d)
+                copy_segments(new, t_new, cu_new, out, rows, start_new, n_batch, h_kv, d)
+            return out
+
+        k_out = merged(entry.k_cache, k_cache)
+        v_out = None if entry.is_mla else merged(entry.v_cache, v_cache)
+        self._layer_kv[key] = LayerKVEntry(
+            k_cache=k_out,
+            v_cache=v_out,
+            total_context_len=rows,
+            cu_seqlens_kv=cu_out,
+            context_batch_size=entry.context_batch_size,
+            is_mla=entry.is_mla,
+            num_heads=entry.num_heads,
+            head_dim=d,
+            dtype=entry.dtype,
+            device=dev,
+        )
+
     def get_kv_cache(
         self,
         layer_id: int | str,

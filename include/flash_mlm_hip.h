@@ -136,6 +136,18 @@ FMLM_API int fmlm_unpack(int32_t elem_bytes, const void* packed, int64_t p_sh, v
                 int32_t N, int32_t D, const int32_t* cu_seqlens, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Segment copy, the kernel of a true KV append (InferenceCache.append_kv_cache): for
+ * head h < H and segment c < C, rows [src_cu[c], src_cu[c+1]) of src (row h*src_sh/D +
+ * i) go to rows [dst_start[c], dst_start[c] + len) of dst (row h*dst_sh/D + i); rows are
+ * D elements of elem_bytes.  Offsets are clamped to src_rows / dst_rows rows per head.
+ * No counterpart in the reference, which replaces a layer's context on prefill and lists
+ * appends with paged KV on its roadmap (README.md:34-41).
+ * ------------------------------------------------------------------------- */
+FMLM_API int fmlm_copy_segments(int32_t elem_bytes, const void* src, int64_t src_sh, int32_t src_rows,
+                                const int32_t* src_cu, void* dst, int64_t dst_sh, int32_t dst_rows,
+                                const int32_t* dst_start, int32_t C, int32_t H, int32_t D, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Fused MLM attention forward, dense and packed (mlm_kernel_impl.py:65-216, 219-390).
  *
  * For every sequence b < B, head h < H and query position p < L_b

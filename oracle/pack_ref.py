@@ -108,3 +108,28 @@ def unpack(packed: np.ndarray, meta: MetaRef, H: int) -> np.ndarray:
     x = np.zeros((H, meta.B * meta.N, D), dtype=packed.dtype)
     x[:, meta.token_indices] = p
     return np.transpose(x.reshape(H, meta.B, meta.N, D), (1, 0, 2, 3)).copy()
+
+
+def append_segments(old: np.ndarray, cu_old, new: np.ndarray, cu_new, heads: int):
+    """KV append (an extension with no reference counterpart; the reference's roadmap
+    lists appends with paged KV, README.md:34-41): head-major caches old [heads*T_old, D]
+    and new [heads*T_new, D] with per-batch offsets cu_old / cu_new -> (merged
+    [heads*(T_old+T_new), D], cu_out) where batch c of every head holds its old rows then
+    its new rows, cu_out = cu_old + cu_new.  Rows past cu_out[-1] are zero here (the
+    GPU leaves them unwritten)."""
+    cu_old = np.asarray(cu_old, dtype=np.int64)
+    cu_new = np.asarray(cu_new, dtype=np.int64)
+    D = old.shape[1]
+    t_old, t_new = old.shape[0] // heads, new.shape[0] // heads
+    rows = t_old + t_new
+    out = np.zeros((heads * rows, D), dtype=old.dtype)
+    for h in range(heads):
+        r = h * rows
+        for c in range(len(cu_old) - 1):
+            seg_old = old[h * t_old + cu_old[c] : h * t_old + cu_old[c + 1]]
+            seg_new = new[h * t_new + cu_new[c] : h * t_new + cu_new[c + 1]]
+            out[r : r + len(seg_old)] = seg_old
+            r += len(seg_old)
+            out[r : r + len(seg_new)] = seg_new
+            r += len(seg_new)
+    return out, cu_old + cu_new

@@ -22,7 +22,8 @@ def _declared():
 
 def test_header_declares_entry_points():
     names = _declared()
-    assert {"fmlm_pack_metadata", "fmlm_pack", "fmlm_unpack", "fmlm_attn_fwd", "fmlm_tile_map"} <= set(names)
+    assert {"fmlm_pack_metadata", "fmlm_pack", "fmlm_unpack", "fmlm_attn_fwd", "fmlm_tile_map",
+            "fmlm_copy_segments"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol():
@@ -46,6 +47,9 @@ def test_argument_rejection_without_launch():
     assert lib.fmlm_pack(None, 0, 2, 1, 1, 16, None, 1, 1, None) == -1
     assert lib.fmlm_pack(None, 1, 3, 1, 1, 16, None, 1, 1, None) == -2  # bad element size
     assert lib.fmlm_unpack(2, None, 0, None, 1, 1, 1, 16, None, None) == -1
+    assert lib.fmlm_copy_segments(2, None, 16, 4, None, None, 16, 4, None, 1, 1, 16, None) == -1
+    assert lib.fmlm_copy_segments(3, None, 16, 4, None, None, 16, 4, None, 1, 1, 16, None) == -2
+    assert lib.fmlm_copy_segments(2, None, 16, 0, None, None, 16, 4, None, 1, 1, 16, None) == 0  # nothing to copy
     assert lib.fmlm_pack_metadata(None, 0, 1, 4, 0, None, None, None, None, None, None) == -1
     assert lib.fmlm_tile_map(None, 1, 4, 0, None, None, None, None) == -1
     assert lib.fmlm_attn_fwd(None, None) == -1

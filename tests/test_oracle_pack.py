@@ -144,3 +144,55 @@ def test_padded_length_closed_form():
     assert pack_ref.total_q_len_padded(12, cu, 4, 2) == max(12, 0 + 8, 5 + 0, 5 + 8)
     assert pack_ref.total_q_len_padded(12, cu, 1, 1) == 12
     assert pack_ref.total_q_len_padded(0, np.array([0]), 64, 64) == 0
+
+
+# ---------------------------------------------------------------------------
+# KV append oracle (extension): batch c of every head = old rows of c, then new rows of c
+# ---------------------------------------------------------------------------
+def test_append_segments_known_answer():
+    # one head, two batches: old [a0 a1 | b0], new [A0 | B0 B1] -> [a0 a1 A0 | b0 B0 B1]
+    old = np.array([[1.0], [2.0], [3.0]])
+    new = np.array([[10.0], [20.0], [30.0]])
+    out, cu = pack_ref.append_segments(old, [0, 2, 3], new, [0, 1, 3], heads=1)
+    np.testing.assert_array_equal(out[:, 0], [1, 2, 10, 3, 20, 30])
+    np.testing.assert_array_equal(cu, [0, 3, 6])
+    # two heads keep their own rows; trailing rows nobody owns are zero
+    old2 = np.arange(8, dtype=np.float64).reshape(8, 1)           # 2 heads x 4 rows, cu [0,1,3]
+    new2 = 100 + np.arange(4, dtype=np.float64).reshape(4, 1)     # 2 heads x 2 rows, cu [0,2,2]
+    out2, cu2 = pack_ref.append_segments(old2, [0, 1, 3], new2, [0, 2, 2], heads=2)
+    np.testing.assert_array_equal(out2[:, 0], [0, 100, 101, 1, 2, 0, 4, 102, 103, 5, 6, 0])
+    np.testing.assert_array_equal(cu2, [0, 3, 5])
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_append_segments_identities_and_associativity(seed):
+    rng = np.random.default_rng(seed)
+    H, D, C = 2, 3, 4
+
+    def cache():
+        lens = rng.integers(0, 5, size=C)
+        cu = np.concatenate([[0], np.cumsum(lens)])
+        t = int(cu[-1]) + int(rng.integers(0, 3))  # trailing rows nobody owns
+        return rng.standard_normal((H * t, D)), cu
+
+    A, ca = cache()
+    B, cb = cache()
+    Cc, cc = cache()
+    # appending nothing / appending to nothing keeps exactly the owned rows
+    empty, cz = np.zeros((0, D)), np.zeros(C + 1, dtype=np.int64)
+    out, cu = pack_ref.append_segments(A, ca, empty, cz, H)
+    np.testing.assert_array_equal(cu, ca)
+    t = A.shape[0] // H
+    for h in range(H):
+        np.testing.assert_array_equal(out[h * t : h * t + ca[-1]], A[h * t : h * t + ca[-1]])
+    out, cu = pack_ref.append_segments(empty, cz, B, cb, H)
+    np.testing.assert_array_equal(cu, cb)
+    # (A + B) + C == A + (B + C) on the owned rows
+    ab, cab = pack_ref.append_segments(A, ca, B, cb, H)
+    left, cl = pack_ref.append_segments(ab, cab, Cc, cc, H)
+    bc, cbc = pack_ref.append_segments(B, cb, Cc, cc, H)
+    right, cr = pack_ref.append_segments(A, ca, bc, cbc, H)
+    np.testing.assert_array_equal(cl, cr)
+    tl, tr = left.shape[0] // H, right.shape[0] // H
+    for h in range(H):
+        np.testing.assert_array_equal(left[h * tl : h * tl + cl[-1]], right[h * tr : h * tr + cr[-1]])
