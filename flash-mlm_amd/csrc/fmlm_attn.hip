@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
                                                                  int32_t* __restrict__ header,
                                                                  int4* __restrict__ groups,
                                                                  int groups_off, int records_off,
-                                                                 int rec_bytes) {
+                                                                 int rec_bytes, int hpack) {
   __shared__ int s_tiles[kSortMax];
   __shared__ float s_work[kSortMax];
   __shared__ int s_order[kSortMax];
@@ -111,6 +111,12 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
   const int tid = threadIdx.x;
   const int B = p.B, H = p.H;
   const bool sorted = B <= kSortMax;
+  // head-packed tiles (hpack, MLA): a tile is BQ consecutive rows of the H*L (head,
+  // position) rows of a sequence, since every head reads the same latent.  Sequence b's
+  // tiles t = j + kXcds*i form group (b, j), so group j of every sequence lands on XCD j.
+  const int HG = hpack ? kXcds : H;  // groups per sequence
+  auto seq_tiles = [&](int len) { return ((hpack ? H : 1) * len + BQ - 1) / BQ; };
+  auto group_tiles = [&](int tiles, int j) { return hpack ? max(0, (tiles - j + kXcds - 1) / kXcds) : tiles; };
   if (tid < 2) s_sum[tid] = 0.f;
   if (tid == 0) {
     s_chunk = 0;
@@ -122,12 +128,13 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
     // per sequence: query tiles and key tiles; totals of units and key-tile work
     for (int b = tid; b < B; b += kSchedThreads) {
       const SeqInfo si = seq_info(p, b);
-      const int tiles = (si.len + BQ - 1) / BQ;
+      const int tiles = seq_tiles(si.len);
       const int ktiles = (si.ctx + kSplitBK - 1) / kSplitBK + (si.mainlen + kSplitBK - 1) / kSplitBK;
+      const float units = (float)tiles * (hpack ? 1 : H);
       s_tiles[b] = tiles;
       s_work[b] = (float)ktiles;
-      atomicAdd(&s_sum[0], (float)tiles * H);
-      atomicAdd(&s_sum[1], (float)tiles * H * ktiles);
+      atomicAdd(&s_sum[0], units);
+      atomicAdd(&s_sum[1], units * ktiles);
     }
     __syncthreads();
     // split only when the units are too few to fill the slots for kSplitRounds rounds;
@@ -139,7 +146,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
         float recs = 0.f;
         for (int b = 0; b < B; ++b) {
           const int S = min(kMaxSplits, max(1, (int)ceilf(s_work[b] / chunk)));
-          if (S > 1) recs += (float)s_tiles[b] * H * S;
+          if (S > 1) recs += (float)s_tiles[b] * (hpack ? 1 : H) * S;
         }
         if (recs <= (float)rec_cap) {
           s_chunk = chunk;
@@ -167,16 +174,16 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
     __syncthreads();
   }
   const int x = tid >> 6, lane = tid & 63;
-  const int G = B * H;
+  const int G = B * HG;
   int carry = 0;
   for (int i0 = 0; x + kXcds * i0 < G; i0 += 64) {
     const int g = x + kXcds * (i0 + lane);
     int b = 0, h = 0, tiles = 0, S = 1;
     if (g < G) {
-      const int r = g / H;
-      h = g - r * H;
+      const int r = g / HG;
+      h = g - r * HG;
       b = sorted ? s_order[r] : r;
-      tiles = sorted ? s_tiles[b] : (seq_info(p, b).len + BQ - 1) / BQ;
+      tiles = group_tiles(sorted ? s_tiles[b] : seq_tiles(seq_info(p, b).len), h);
       S = sorted ? s_split[b] : 1;
     }
     const int n = tiles * S;
@@ -189,16 +196,18 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
     }
     const int pos = carry + incl - n;
     int gid0 = 0, rec0 = 0;
+    // (h, tile) field of the unit: head-packed tiles carry no head
+    auto hf = [&](int j) { return hpack ? ((h + kXcds * j) << 16) : (h | (j << 16)); };
     if (S > 1) {
       gid0 = atomicAdd(&s_groups, tiles);
       rec0 = atomicAdd(&s_recs, tiles * S);
-      for (int j = 0; j < tiles; ++j) groups[gid0 + j] = make_int4(b, h | (j << 16), rec0 + j * S, S);
+      for (int j = 0; j < tiles; ++j) groups[gid0 + j] = make_int4(b, hf(j), rec0 + j * S, S);
     }
     for (int j = 0; j < tiles; ++j) {
       for (int sp = 0; sp < S; ++sp) {
         const int64_t slot = (int64_t)x + (int64_t)kXcds * (pos + j * S + sp);
         const int wv = S > 1 ? (gid0 + j) | (sp << 20) | ((S - 1) << 25) : -1;
-        if (slot < capacity) units[slot] = make_int4(b, h | (j << 16), rec0 + j * S, wv);
+        if (slot < capacity) units[slot] = make_int4(b, hf(j), rec0 + j * S, wv);
       }
     }
     carry += __shfl(incl, 63);
@@ -237,7 +246,9 @@ struct WorkItem {
   int b, h;
   int split_s, split_n;  // part s of S of the key range (S = 1: whole range)
   int split_group, rec0; // split group and its first record
-  int qpos0, qcount;     // query positions [qpos0, qpos0+qcount) of sequence b
+  int qpos0, qcount;     // query positions [qpos0, qpos0+qcount) of sequence b, or with
+                         // head-packed tiles rows [qpos0, ...) of its H*len (head, pos) rows
+  int len, q0;           // sequence length and packed start (head-packed tiles)
   int64_t q_row0, o_row0;  // element offset of row qpos0
   int64_t q_sn, o_sn;
   KvSeg seg[2];          // context, main
@@ -254,7 +265,7 @@ FMLM_DEV int64_t seg_row(const KvSeg& s, int i, bool is_v, const int32_t* cu, in
 
 // Resolve the workgroup's unit.  Returns false for an idle workgroup.
 FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const int32_t* n_units,
-                           int BQ, WorkItem& w) {
+                           int BQ, WorkItem& w, bool hpack = false) {
   int b, h, tile;
   w.split_s = 0;
   w.split_n = 1;
@@ -289,8 +300,10 @@ FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const i
   const int L = si.len;
   w.b = b;
   w.h = h;
+  w.len = L;
+  w.q0 = q0;
   w.qpos0 = tile * BQ;
-  w.qcount = min(BQ, L - w.qpos0);
+  w.qcount = min(BQ, (hpack ? p.H : 1) * L - w.qpos0);
   if (w.qcount <= 0) return false;
   const int64_t qb = p.q_layout == FMLM_LAYOUT_PACKED ? (int64_t)h * p.q_sh + (int64_t)q0 * p.q_sn
                                                       : (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
@@ -1201,8 +1214,11 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   constexpr int D = C::D, BK = C::BK;
   extern __shared__ __align__(16) char smem_raw[];
 
+  // packed calls use head-packed tiles: 128 consecutive rows of the sequence's H*len
+  // (head, position) rows, all heads reading the same latent
+  const bool hpack = p.cu_seqlens_q != nullptr;
   WorkItem w;
-  if (!resolve_work(p, units, n_units, C::BQ, w)) return;
+  if (!resolve_work(p, units, n_units, C::BQ, w, hpack)) return;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1211,6 +1227,19 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   const int g = lane >> 4;
   const int row = wave * 16 + l16;  // the query row of this lane's S^T / O^T column
   const bool wave_active = wave * 16 < w.qcount;
+  // element offsets of this lane's q and o rows
+  int64_t q_off, o_off;
+  {
+    int hq = w.h, pq = w.qpos0 + row;
+    if (hpack && w.len > 0) {
+      hq = pq / w.len;
+      pq -= hq * w.len;
+    }
+    q_off = p.q_layout == FMLM_LAYOUT_PACKED ? (int64_t)hq * p.q_sh + (int64_t)(w.q0 + pq) * p.q_sn
+                                             : (int64_t)w.b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)pq * p.q_sn;
+    o_off = p.o_layout == FMLM_LAYOUT_PACKED ? (int64_t)hq * p.o_sh + (int64_t)(w.q0 + pq) * p.o_sn
+                                             : (int64_t)w.b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)pq * p.o_sn;
+  }
 
   // ---- Q^T fragments (B operand of S^T = K Q^T) for step kc, pre-scaled by
   // scale*log2(e) (one rounding to the input type): S comes out in log2 units
@@ -1218,7 +1247,7 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   v8 qf[C::KC];
   {
     const bool ok = row < w.qcount;
-    const char* src = (const char*)p.q + (w.q_row0 + (int64_t)row * w.q_sn) * 2;
+    const char* src = (const char*)p.q + q_off * 2;
 #pragma unroll
     for (int kc = 0; kc < C::KC; ++kc) {
       v8 raw = v8{};
@@ -1400,7 +1429,7 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   l_i += __shfl_xor(l_i, 32);
   if (row < w.qcount) {
     const float inv = l_i > 0.f ? 1.f / l_i : 1.f;
-    char* dst = (char*)p.o + (w.o_row0 + (int64_t)row * w.o_sn) * 2;
+    char* dst = (char*)p.o + o_off * 2;
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db) {
       T v4[4];
@@ -1594,6 +1623,7 @@ struct Launch {
   int lds;
   const void* fn;
   bool split = false;  // kernel can run split-KV units
+  bool hpack = false;  // packed tiles span (head, position) rows (MLA: one latent for all heads)
 };
 
 template <typename T, int D, int QB, int NW, int BK>
@@ -1617,7 +1647,8 @@ static Launch mfma3_launch() {
 
 template <typename T>
 static Launch mla_rows_launch() {
-  return Launch{MlaRowsCfg::BQ, MlaRowsCfg::NT, MlaRowsCfg::LDS_BYTES, (const void*)&attn_mla_rows_kernel<T>};
+  return Launch{MlaRowsCfg::BQ, MlaRowsCfg::NT, MlaRowsCfg::LDS_BYTES, (const void*)&attn_mla_rows_kernel<T>, false,
+                true};
 }
 
 // MFMA kernels by head dim.  The pipelined kernel and the 512-wide latent kernel need
@@ -1736,10 +1767,14 @@ static SplitCfg split_cfg(const fmlm_attn_params& p, const Launch& L) {
 // schedule, whose XCD slots are bounded by ceil(total/8) + the largest group (with
 // splits: at most kSplitRounds*slots unsplit units plus rec_cap split parts, a group
 // growing by up to kMaxSplits).
-static int64_t grid_units(const fmlm_attn_params& p, int bq, const SplitCfg& sc) {
+static int64_t grid_units(const fmlm_attn_params& p, int bq, const SplitCfg& sc, bool hpack = false) {
   if (!p.cu_seqlens_q) {
     const int64_t groups = (int64_t)p.B * p.H;
     return kXcds * ((groups + kXcds - 1) / kXcds) * ((p.N + bq - 1) / bq);
+  }
+  if (hpack) {  // sum over b of ceil(H*L_b/bq) units; each XCD list pads by < 1 per sequence
+    const int64_t units = ((int64_t)p.H * p.total_q + bq - 1) / bq + p.B;
+    return kXcds * ((units + kXcds - 1) / kXcds + p.B + 1);
   }
   const int64_t total = (int64_t)p.H * (p.B + p.total_q / bq + 1);
   const int64_t max_group = (p.N > 0 ? (p.N + bq - 1) / bq : p.total_q / bq + 1) + 1;
@@ -1757,10 +1792,10 @@ struct SchedLayout {
   int64_t units_off, groups_off, records_off, bytes;
 };
 
-static SchedLayout sched_layout(const fmlm_attn_params& p, int bq, const SplitCfg& sc) {
+static SchedLayout sched_layout(const fmlm_attn_params& p, int bq, const SplitCfg& sc, bool hpack) {
   SchedLayout l;
   l.units_off = 256;
-  l.groups_off = l.units_off + grid_units(p, bq, sc) * (int64_t)sizeof(int4);
+  l.groups_off = l.units_off + grid_units(p, bq, sc, hpack) * (int64_t)sizeof(int4);
   l.groups_off = (l.groups_off + 255) / 256 * 256;
   l.records_off = l.groups_off + (int64_t)sc.rec_cap * (int64_t)sizeof(int4);
   l.records_off = (l.records_off + 255) / 256 * 256;
@@ -1770,7 +1805,7 @@ static SchedLayout sched_layout(const fmlm_attn_params& p, int bq, const SplitCf
 
 static int64_t workspace_for(const fmlm_attn_params& p, const Launch& L) {
   if (!p.cu_seqlens_q) return 0;
-  return sched_layout(p, L.bq, split_cfg(p, L)).bytes;
+  return sched_layout(p, L.bq, split_cfg(p, L), L.hpack).bytes;
 }
 
 static int check_params(const fmlm_attn_params& p) {
@@ -1791,14 +1826,16 @@ static int check_params(const fmlm_attn_params& p) {
 
 static int launch_schedule(const fmlm_attn_params& p, const Launch& L, char* sched, hipStream_t s) {
   const SplitCfg sc = split_cfg(p, L);
-  const SchedLayout l = sched_layout(p, L.bq, sc);
-  const int64_t cap = grid_units(p, L.bq, sc);
-  if (cap > 0x7fffffff || p.H > 0xffff || (p.N + L.bq - 1) / L.bq > 0xffff) return FMLM_E_ARG;
+  const SchedLayout l = sched_layout(p, L.bq, sc, L.hpack);
+  const int64_t cap = grid_units(p, L.bq, sc, L.hpack);
+  // the unit's 16-bit tile field: tiles of N rows, or of H*N (H*total_q) rows head-packed
+  const int64_t rows = L.hpack ? (int64_t)p.H * (p.N > 0 ? p.N : p.total_q) : p.N;
+  if (cap > 0x7fffffff || p.H > 0xffff || (rows + L.bq - 1) / L.bq > 0xffff) return FMLM_E_ARG;
   int32_t* header = (int32_t*)sched;
   hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, s, p, L.bq, (int)cap,
                      sc.slots, sc.rec_cap, (int4*)(sched + l.units_off), header,
                      (int4*)(sched + l.groups_off), (int)l.groups_off, (int)l.records_off,
-                     (int)sc.rec_bytes);
+                     (int)sc.rec_bytes, (int)L.hpack);
   return launch_status();
 }
 
@@ -1853,7 +1890,7 @@ extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
       if (rc) return rc;
     }
   }
-  const int64_t gx = grid_units(p, L.bq, split_cfg(p, L));
+  const int64_t gx = grid_units(p, L.bq, split_cfg(p, L), L.hpack);
   if (gx <= 0) return 0;
   if (gx > 0x7fffffff) return FMLM_E_ARG;
   fmlm_attn_params pc = p;
