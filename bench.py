@@ -103,8 +103,42 @@ def _randn(shape, gen, device, dtype, std=1.0):
     return t.to(dtype)
 
 
+def _prefill_paged(cache, k_cache, v_cache, cu_kv, *, hk: int, H: int, D: int, mla: bool, seed: int,
+                   shuffle: bool = True) -> None:
+    """Store a contiguous head-major context [hk*Tc, D] as a paged one: every context batch's
+    rows in 64-row pages [hk, P, 64, D], pages placed in a seeded random order (or in key
+    order with shuffle=False)."""
+    page = 64
+    lens = (cu_kv[1:] - cu_kv[:-1]).tolist()
+    need = [(n + page - 1) // page for n in lens]
+    P = sum(need)
+    order = torch.randperm(P, generator=torch.Generator().manual_seed(seed)) if shuffle else torch.arange(P)
+    bt = torch.zeros((len(lens), max(need + [1])), dtype=torch.int32)
+    src, dst, k0 = [], [], 0
+    for c, (n, npg) in enumerate(zip(lens, need)):
+        bt[c, :npg] = order[k0 : k0 + npg]
+        j = torch.arange(n)
+        src.append(int(cu_kv[c]) + j)
+        dst.append(bt[c, j // page].long() * page + j % page)
+        k0 += npg
+    src_i = torch.cat(src).to(k_cache.device)
+    dst_i = torch.cat(dst).to(k_cache.device)
+    Tc = int(cu_kv[-1])
+
+    def pool_of(x):
+        pool = torch.zeros((hk, P * page, D), dtype=x.dtype, device=x.device)
+        pool[:, dst_i] = x.view(hk, Tc, D)[:, src_i]
+        return pool.view(hk, P, page, D)
+
+    cache.prefill_paged_kv_cache(0, k_pages=pool_of(k_cache), v_pages=None if mla else pool_of(v_cache),
+                                 block_table=bt.to(k_cache.device), context_lens=torch.tensor(lens, dtype=torch.int32),
+                                 is_mla=mla, num_heads=H, head_dim=D)
+
+
 def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
-    """Build BASELINE config `cfg` (1..5; config 5 variant "prefill" is 5b) with
+    """Build BASELINE config `cfg` (1..5; config 5 variant "prefill" is 5b, variant
+    "paged" / "paged_seq" store configs 3-5's context as a paged KV pool, pages shuffled /
+    in key order) with
     seeded synthetic inputs: lengths from a CPU generator seeded 1000+cfg (query
     lengths first, then context lengths), tensors from a device generator with the
     same seed, fp32 normal * std cast to the config dtype."""
@@ -178,10 +212,14 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
         k_cache = _randn((hk * Tc, D), gdev, device, dt, std)
         v_cache = None if mla else _randn((hk * Tc, D), gdev, device, dt, std)
         cache = fm.InferenceCache()
-        cache.prefill_kv_cache(
-            0, k_cache=k_cache, v_cache=v_cache, total_context_len=Tc, cu_seqlens_kv=cu_kv.to(device),
-            context_batch_size=cbs, is_mla=mla, num_heads=H, head_dim=D,
-        )
+        if variant in ("paged", "paged_seq"):  # the same context rows in a 64-row page pool
+            _prefill_paged(cache, k_cache, v_cache, cu_kv, hk=hk, H=H, D=D, mla=mla, seed=seed,
+                           shuffle=variant == "paged")
+        else:
+            cache.prefill_kv_cache(
+                0, k_cache=k_cache, v_cache=v_cache, total_context_len=Tc, cu_seqlens_kv=cu_kv.to(device),
+                context_batch_size=cbs, is_mla=mla, num_heads=H, head_dim=D,
+            )
         meta = cache.packing.get_pack_metadata(lq.to(device=device, dtype=torch.int32), N=N, block_n=bn)
         kw = dict(is_mla=mla, block_n=bn, causal_query_seq_attn=causal)
 
@@ -204,7 +242,8 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
             5: "cfg5 MLA bf16 B=8 64 heads : 1 latent D=512, cached latent ctx 8192/seq",
         }
         return Case(
-            cfg, names[cfg] + (" (prefill=True)" if prefill else ""), dt, H, D,
+            cfg, names[cfg] + (" (prefill=True)" if prefill else "") + (f" ({variant} KV context)" if variant.startswith("paged") else ""),
+            dt, H, D,
             [int(x) for x in lq], lengths_ctx, causal, prefill, mla,
             step=step,
             attention=plan,
@@ -370,7 +409,7 @@ def hbm_kernels(case: Case, reps: int = 30) -> dict:
     # context batch of the layer's packed entry; reads and writes every owned row once
     ent = t["cache"].get_kv_cache(0, is_mla=case.is_mla, num_heads=H, head_dim=D, dtype=case.dtype,
                                   device=t["q"].device) if "cache" in t else None
-    if ent is not None and ent.cu_seqlens_kv is not None:
+    if ent is not None and ent.cu_seqlens_kv is not None and ent.block_table is None:
         h_kv = 1 if case.is_mla else H
         n_batch = int(ent.cu_seqlens_kv.numel()) - 1
         cu_new = meta.cu_seqlens if n_batch == B else torch.tensor([0, T], dtype=torch.int32, device="cuda")

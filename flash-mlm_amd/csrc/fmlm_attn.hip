@@ -68,6 +68,21 @@ FMLM_DEV int ctx_batch_of(const fmlm_attn_params& p, int b) {
   return p.ctx_batch > 1 ? b : 0;
 }
 
+// context rows [c0, c1) of context batch cb (contiguous context), or (0, n) of a paged one
+FMLM_DEV void ctx_range(const fmlm_attn_params& p, int cb, int& c0, int& c1) {
+  c0 = 0;
+  c1 = p.ctx_len;
+  if (p.cu_seqlens_kv) {
+    if (p.ctx_block_table) {
+      c1 = p.cu_seqlens_kv[cb + 1] - p.cu_seqlens_kv[cb];
+    } else {
+      c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
+      c1 = min(max(p.cu_seqlens_kv[cb + 1], c0), p.ctx_rows);
+    }
+  }
+  if (p.ctx_block_table) c1 = min(max(c1, 0), p.ctx_pages_per_batch * FMLM_PAGE_ROWS);
+}
+
 FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
   const int32_t* cu = p.cu_seqlens_q;
   SeqInfo s;
@@ -81,12 +96,8 @@ FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
   s.len = L;
   s.ctx = 0;
   if (!(p.flags & FMLM_FLAG_PREFILL)) {
-    const int cb = ctx_batch_of(p, b);
-    int c0 = 0, c1 = p.ctx_len;
-    if (p.cu_seqlens_kv) {
-      c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
-      c1 = min(max(p.cu_seqlens_kv[cb + 1], c0), p.ctx_rows);
-    }
+    int c0, c1;
+    ctx_range(p, ctx_batch_of(p, b), c0, c1);
     s.ctx = max(c1 - c0, 0);
   }
   s.mainlen = ((p.flags & FMLM_FLAG_CAUSAL_SEQ) && cu) ? s.q0 + L : L;
@@ -240,6 +251,10 @@ struct KvSeg {
   int64_t ksb, vsb;      // sequence strides (lookup only)
   int n;                 // number of keys
   bool lookup;           // keys are packed token indices over a padded tensor
+  const int32_t* pages;  // paged segment: page of each FMLM_PAGE_ROWS-key tile, else NULL
+  int64_t page_elems;    // elements between pages
+  int npool;             // pages in the pool (page ids are clamped to it)
+  int ntab;              // entries of the segment's block-table row
 };
 
 struct WorkItem {
@@ -321,21 +336,33 @@ FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const i
   c.v = (const char*)(mla ? p.k_ctx : p.v_ctx);
   c.lookup = false;
   c.n = 0;
+  c.pages = nullptr;
+  c.page_elems = 0;
+  c.npool = 0;
+  c.ntab = 0;
   if (!(p.flags & FMLM_FLAG_PREFILL)) {
     const int cb = ctx_batch_of(p, b);
-    int c0 = 0, c1 = p.ctx_len;
-    if (p.cu_seqlens_kv) {
-      c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
-      c1 = min(max(p.cu_seqlens_kv[cb + 1], c0), p.ctx_rows);
-    }
+    int c0, c1;
+    ctx_range(p, cb, c0, c1);
     c.n = max(c1 - c0, 0);
-    c.kbase = (int64_t)cb * p.c_sb + (int64_t)h * p.c_sh + (int64_t)c0 * p.c_sn;
+    if (p.ctx_block_table) {  // paged: rows come from the batch's pages
+      c.pages = p.ctx_block_table + (int64_t)cb * p.ctx_pages_per_batch;
+      c.page_elems = p.ctx_page_stride;
+      c.npool = p.ctx_rows;
+      c.ntab = p.ctx_pages_per_batch;
+    }
+    c.kbase = p.ctx_block_table ? (int64_t)h * p.c_sh
+                                : (int64_t)cb * p.c_sb + (int64_t)h * p.c_sh + (int64_t)c0 * p.c_sn;
     c.vbase = c.kbase;
     c.ksn = c.vsn = p.c_sn;
     c.ksb = c.vsb = 0;
   }
   // main segment (mlm_kernel_impl.py:288-293, 360-379)
   KvSeg& m = w.seg[1];
+  m.pages = nullptr;
+  m.page_elems = 0;
+  m.npool = 0;
+  m.ntab = 0;
   m.k = (const char*)p.k;
   m.v = (const char*)(mla ? p.k : p.v);
   const int64_t v_sb = mla ? p.k_sb : p.v_sb, v_sh = mla ? p.k_sh : p.v_sh,
@@ -746,11 +773,37 @@ struct Pair<f16> {
 };
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+// Page ids of 64 consecutive key tiles of a paged segment, one per lane of a VGPR: a tile
+// then costs a lane read.  A page id fetched per tile by a vector load would make its use
+// wait for every outstanding vector memory operation, the in-flight tile loads too; the
+// window's reload pays that wait once per 64 tiles.
+struct PageWindow {
+  int ids;    // lane i: page of tile first + i
+  int first;  // first tile of the window
+};
+FMLM_DEV void page_window_reset(PageWindow& w) { w.first = -(1 << 30); }
+// first row of tile `tile` of a paged segment (page ids clamped to the pool)
+FMLM_DEV const char* page_row0(const KvSeg& s, const char* base, int tile, PageWindow& w) {
+  tile = __builtin_amdgcn_readfirstlane(tile);
+  if ((unsigned)(tile - w.first) >= 64u) {
+    w.first = tile;
+    const int lane = threadIdx.x & 63;
+    w.ids = s.pages[min(tile + lane, max(s.ntab - 1, 0))];
+    // consume the load here: the wait for it then stays on this path, not after the join
+    asm volatile("" ::"v"(w.ids));
+  }
+  int pg = __builtin_amdgcn_readlane(w.ids, tile - w.first);
+  pg = min(max(pg, 0), max(s.npool - 1, 0));
+  return base + (int64_t)pg * s.page_elems * 2;
+}
+
 // walks the key tiles of a work item for the direct loads (see attn_mfma3_kernel)
 struct KeyCursor {
-  const char* p;
+  const char* p;     // row 0 of the current tile
+  const char* base;  // the segment's first row (paged: its row 0 of page 0 of the pool)
   uint32_t rowb;
-  int left, seg;
+  int left, seg, tile;
+  PageWindow pw;     // paged segment: page ids of the tiles around `tile`
 };
 
 template <typename T, int D, int QB, int NW, int BK>
@@ -775,7 +828,7 @@ struct Mfma3Cfg {
   static_assert(BK % 32 == 0 && BK % RPI == 0, "key tile");
 };
 
-template <typename T, int D, int QB, int NW, int BK>
+template <typename T, int D, int QB, int NW, int BK, bool PAGED>
 __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
   typedef Mfma3Cfg<T, D, QB, NW, BK> C;
@@ -876,20 +929,32 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       ofs[j] = (uint32_t)__umul24((uint32_t)min(row, last), rowb) + 16 * ((lane % C::CPR) ^ kv_swz<D>(row));
     }
   };
+  // a paged context (PAGED instantiation, segment 0 only) puts each key tile in a page
+  const bool ctx_paged = PAGED && w.seg[0].pages != nullptr;
   auto cursor_seg = [&](Cursor& cr, int sg, bool is_v) {
     const KvSeg& sgm = w.seg[sg];
     cr.seg = sg;
+    cr.tile = 0;
     cr.left = __builtin_amdgcn_readfirstlane(sgm.n);
     cr.rowb = __builtin_amdgcn_readfirstlane((uint32_t)(is_v ? sgm.vsn : sgm.ksn) * 2u);
-    cr.p = uniform_ptr((is_v ? sgm.v : sgm.k) + (is_v ? sgm.vbase : sgm.kbase) * 2);
+    cr.base = uniform_ptr((is_v ? sgm.v : sgm.k) + (is_v ? sgm.vbase : sgm.kbase) * 2);
+    cr.p = cr.base;
+    page_window_reset(cr.pw);
+    if constexpr (PAGED)
+      if (sg == 0 && ctx_paged && cr.left > 0) cr.p = uniform_ptr(page_row0(w.seg[0], cr.base, 0, cr.pw));
   };
   // position a cursor on key tile t
   auto cursor_seek = [&](Cursor& cr, int t, bool is_v) {
     const int sg = t < nt0 ? 0 : 1;
     cursor_seg(cr, sg, is_v);
-    const int skip = (sg == 0 ? t : t - nt0) * BK;
-    cr.left -= skip;
-    cr.p += (size_t)skip * cr.rowb;
+    const int skip = sg == 0 ? t : t - nt0;
+    cr.left -= skip * BK;
+    cr.tile = skip;
+    if (PAGED && sg == 0 && ctx_paged) {
+      if constexpr (PAGED) cr.p = cr.left > 0 ? uniform_ptr(page_row0(w.seg[0], cr.base, skip, cr.pw)) : cr.base;
+    } else {
+      cr.p += (size_t)skip * BK * cr.rowb;
+    }
   };
   // lane offsets of a whole tile at the main segment's K row pitch (the common case)
   const uint32_t oc_rowb = __builtin_amdgcn_readfirstlane((uint32_t)w.seg[1].ksn * 2u);
@@ -912,7 +977,12 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
         dma16_sbase(uniform_ptr(cr.p), ofs[j], __builtin_amdgcn_readfirstlane(lds0 + i * 1024));
     }
     cr.left -= BK;
-    cr.p += (size_t)BK * cr.rowb;
+    cr.tile += 1;
+    if (PAGED && cr.seg == 0 && ctx_paged) {  // one page per context tile
+      if constexpr (PAGED) cr.p = cr.left > 0 ? uniform_ptr(page_row0(w.seg[0], cr.base, cr.tile, cr.pw)) : cr.base;
+    } else {
+      cr.p += (size_t)BK * cr.rowb;
+    }
     if (cr.left <= 0 && cr.seg == 0 && w.seg[1].n > 0) cursor_seg(cr, 1, is_v);
   };
   auto tile_keys = [&](int t) {
@@ -1206,7 +1276,7 @@ struct MlaRowsCfg {
   static constexpr int LDS_BYTES = 2 * TILEB;
 };
 
-template <typename T>
+template <typename T, bool PAGED>
 __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
     const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
   typedef MlaRowsCfg C;
@@ -1276,6 +1346,8 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
   const int ntiles = nt0 + nt1;
+  PageWindow pwin;  // paged context: page ids of the tiles around the last one fetched
+  page_window_reset(pwin);
 
   // ---- direct loads of tile t into stage st: wave w brings rows w + 8j, one 1 KiB row
   // per load; lane l fetches logical chunk l ^ kv_swz(row), which lands in physical chunk
@@ -1285,14 +1357,23 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   auto fetch = [&](int t, int st) {
     const int sg = t < nt0 ? 0 : 1;
     const KvSeg& s = w.seg[sg];
-    const int j0 = (sg == 0 ? t : t - nt0) * BK;
+    const int tt = sg == 0 ? t : t - nt0;
+    const int j0 = tt * BK;
     const int last = __builtin_amdgcn_readfirstlane(s.n - 1);
-    const char* base = s.k + s.kbase * 2;
     const uint32_t lds0 = lds_addr(smem_raw + st * C::TILEB);
+    // paged segments (the context): tile tt is one page; rows are relative to its row 0
+    const char* base = s.k + s.kbase * 2;
+    int kb0 = j0;
+    if constexpr (PAGED) {
+      if (sg == 0 && w.seg[0].pages) {
+        base = page_row0(w.seg[0], base, tt, pwin);
+        kb0 = 0;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < BK / C::NW; ++j) {
       const int r = wave + j * C::NW;
-      const int key = min(j0 + r, last);
+      const int key = min(j0 + r, last) - j0 + kb0;
       dma16_sbase(uniform_ptr(base + (int64_t)key * s.ksn * 2), (uint32_t)((lane ^ kv_swz<D>(r)) << 4),
                   __builtin_amdgcn_readfirstlane(lds0 + r * C::ROWB));
     }
@@ -1624,6 +1705,7 @@ struct Launch {
   const void* fn;
   bool split = false;  // kernel can run split-KV units
   bool hpack = false;  // packed tiles span (head, position) rows (MLA: one latent for all heads)
+  bool paged = false;  // kernel reads a paged context (key tile = FMLM_PAGE_ROWS rows)
 };
 
 template <typename T, int D, int QB, int NW, int BK>
@@ -1638,17 +1720,24 @@ static Launch simt_launch() {
   return Launch{C::RPW, C::NT, C::LDS_BYTES, (const void*)&attn_simt_kernel<T, D>};
 }
 
+// the paged instantiation only for paged contexts, so the contiguous one keeps its code
 template <typename T, int D, int QB, int NW, int BK>
-static Launch mfma3_launch() {
+static Launch mfma3_launch(bool paged) {
   typedef Mfma3Cfg<T, D, QB, NW, BK> C;
   static_assert(BK == kSplitBK, "split planning assumes the kernel's key tile");
-  return Launch{C::BQ, C::NT, C::LDS_BYTES, (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK>, true};
+  static_assert(BK == FMLM_PAGE_ROWS, "a paged context tile is one page");
+  const void* fn = paged ? (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK, true>
+                         : (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK, false>;
+  return Launch{C::BQ, C::NT, C::LDS_BYTES, fn, true, false, true};
 }
 
+// the paged instantiation only for paged contexts: the page lookup costs registers the
+// contiguous kernel (at 256 VGPRs) does not have
 template <typename T>
-static Launch mla_rows_launch() {
-  return Launch{MlaRowsCfg::BQ, MlaRowsCfg::NT, MlaRowsCfg::LDS_BYTES, (const void*)&attn_mla_rows_kernel<T>, false,
-                true};
+static Launch mla_rows_launch(bool paged) {
+  static_assert(MlaRowsCfg::BK == FMLM_PAGE_ROWS, "a paged context tile is one page");
+  const void* fn = paged ? (const void*)&attn_mla_rows_kernel<T, true> : (const void*)&attn_mla_rows_kernel<T, false>;
+  return Launch{MlaRowsCfg::BQ, MlaRowsCfg::NT, MlaRowsCfg::LDS_BYTES, fn, false, true, true};
 }
 
 // MFMA kernels by head dim.  The pipelined kernel and the 512-wide latent kernel need
@@ -1668,15 +1757,16 @@ static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
       default: return false;
     }
   }
+  const bool paged = p.ctx_block_table != nullptr;
   switch (p.D) {
-    case 16: L = mfma3_launch<T, 16, 2, 4, 64>(); return true;
-    case 32: L = mfma3_launch<T, 32, 2, 4, 64>(); return true;
-    case 64: L = mfma3_launch<T, 64, 2, 4, 64>(); return true;
-    case 128: L = mfma3_launch<T, 128, 2, 4, 64>(); return true;
-    case 256: L = mfma3_launch<T, 256, 1, 4, 64>(); return true;
+    case 16: L = mfma3_launch<T, 16, 2, 4, 64>(paged); return true;
+    case 32: L = mfma3_launch<T, 32, 2, 4, 64>(paged); return true;
+    case 64: L = mfma3_launch<T, 64, 2, 4, 64>(paged); return true;
+    case 128: L = mfma3_launch<T, 128, 2, 4, 64>(paged); return true;
+    case 256: L = mfma3_launch<T, 256, 1, 4, 64>(paged); return true;
     case 512:
       if (!(p.flags & FMLM_FLAG_MLA)) return false;
-      L = mla_rows_launch<T>();
+      L = mla_rows_launch<T>(p.ctx_block_table != nullptr);
       return true;
     default: return false;
   }
@@ -1703,7 +1793,10 @@ static int pick_launch(const fmlm_attn_params& p, Launch& L) {
     case FMLM_DTYPE_F32: ok = pick_simt<float>(p.D, L); break;
     default: return FMLM_E_DTYPE;
   }
-  return ok ? 0 : FMLM_E_HEAD_DIM;
+  if (!ok) return FMLM_E_HEAD_DIM;
+  // a paged context needs a kernel whose key tile is one page (not fp32, not per-row lookups)
+  if (p.ctx_block_table && !(p.flags & FMLM_FLAG_PREFILL) && !L.paged) return FMLM_E_ARG;
+  return 0;
 }
 
 // Allow the kernel's dynamic LDS (> 64 KiB for some tiles), once per kernel.
@@ -1820,6 +1913,9 @@ static int check_params(const fmlm_attn_params& p) {
     const bool has_ctx = p.cu_seqlens_kv || p.ctx_len > 0;
     if (has_ctx && !p.cu_seqlens_kv && p.ctx_len > 0 && !p.k_ctx) return FMLM_E_ARG;
     if ((p.cu_seqlens_kv || p.ctx_index) && p.ctx_batch < 1) return FMLM_E_ARG;
+    if (p.ctx_block_table && (p.ctx_pages_per_batch < 0 || p.ctx_rows < 1 || p.ctx_page_stride < 0 ||
+                              p.ctx_batch < 1 || !p.k_ctx))
+      return FMLM_E_ARG;
   }
   return 0;
 }

@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libflash_mlm_hip.so"
 _LIB_PATH = Path(os.environ.get("FMLM_LIB_PATH", Path(__file__).resolve().parent / "_native" / LIB_NAME))
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
@@ -93,6 +93,10 @@ class AttnParams(ctypes.Structure):
         ("workspace_bytes", _c_i64),
         ("schedule", _c_ptr),
         ("ctx_index", _c_ptr),
+        ("ctx_block_table", _c_ptr),
+        ("ctx_page_stride", _c_i64),
+        ("ctx_pages_per_batch", _c_i32),
+        ("reserved0", _c_i32),
     ]
 
 

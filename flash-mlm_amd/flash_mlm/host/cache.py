@@ -109,6 +109,14 @@ class LayerKVEntry:
     head_dim: int
     dtype: torch.dtype
     device: torch.device
+    # paged entries (an extension, see InferenceCache.prefill_paged_kv_cache): k_cache /
+    # v_cache are the page pool [H_kv, P, PAGE_ROWS, D] flattened to rank 2 (head-major,
+    # like the packed entries), total_context_len = P * PAGE_ROWS, cu_seqlens_kv the prefix
+    # sums of the batch lengths
+    block_table: torch.Tensor | None = None
+
+
+PAGE_ROWS = 64  # rows per page of a paged context (FMLM_PAGE_ROWS, the kernels' key tile)
 
 
 def _check_rank2(t: torch.Tensor, what: str) -> None:
@@ -263,6 +271,75 @@ class InferenceCache:
             device=k_cache.device,
         )
 
+    def prefill_paged_kv_cache(
+        self,
+        layer_id: int | str,
+        *,
+        k_pages: torch.Tensor,
+        v_pages: torch.Tensor | None = None,
+        block_table: torch.Tensor,
+        context_lens: torch.Tensor,
+        is_mla: bool,
+        num_heads: int,
+        head_dim: int,
+    ) -> None:
+        """Store a paged context as ``layer_id``'s entry (no copy).
+
+        This is an extension: the reference's roadmap lists paged KV (README.md:41).
+
+        ``k_pages`` / ``v_pages`` are page pools [H_kv, P, 64, D] (contiguous, head-major
+        like the packed entries: a head's pages are adjacent; H_kv = 1 and ``v_pages`` None
+        for MLA).  ``block_table`` [C, max_pages] (int, on the
+        device) lists the pages of each of the C context batches in key order.
+        ``context_lens`` [C] gives their lengths: batch c's key j is row j % 64 of page
+        ``block_table[c, j // 64]``.  The attention kernels read the pages in place,
+        one page per key tile.  Served by the packed paths (flash_attn_mlm_compressed /
+        _precompressed) for bf16/fp16.
+        """
+        if num_heads < 1:
+            raise ValueError("num_heads must be >= 1")
+        h_kv = 1 if is_mla else num_heads
+        if k_pages.ndim != 4 or k_pages.shape[0] != h_kv or tuple(k_pages.shape[2:]) != (PAGE_ROWS, head_dim):
+            raise ValueError(f"k_pages must be [{h_kv}, pages, {PAGE_ROWS}, head_dim]")
+        if not k_pages.is_contiguous():
+            raise ValueError("k_pages must be contiguous")
+        if is_mla:
+            if v_pages is not None:
+                raise ValueError("MLA paged cache takes k_pages only (V = K)")
+        elif v_pages is None or v_pages.shape != k_pages.shape or not v_pages.is_contiguous() \
+                or v_pages.dtype != k_pages.dtype or v_pages.device != k_pages.device:
+            raise ValueError("non-MLA paged cache requires contiguous v_pages shaped like k_pages")
+        if k_pages.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("paged KV contexts need bf16 or fp16 pages")
+        if block_table.ndim != 2 or block_table.dtype not in (torch.int32, torch.int64):
+            raise ValueError("block_table must be a rank-2 integer tensor [context_batch, max_pages]")
+        n_batch, max_pages = int(block_table.shape[0]), int(block_table.shape[1])
+        if n_batch < 1:
+            raise ValueError("block_table needs at least one context batch")
+        if context_lens.ndim != 1 or int(context_lens.numel()) != n_batch:
+            raise ValueError("context_lens must have one entry per block_table row")
+        if not context_lens.is_cuda and n_batch:
+            lo, hi = int(context_lens.min()), int(context_lens.max())
+            if lo < 0 or hi > max_pages * PAGE_ROWS:
+                raise ValueError(f"context_lens must lie in [0, {max_pages * PAGE_ROWS}]")
+        dev = k_pages.device
+        n_pages = int(k_pages.shape[1])
+        cu = torch.zeros(n_batch + 1, dtype=torch.int32, device=dev)
+        cu[1:] = torch.cumsum(context_lens.to(device=dev, dtype=torch.int32), 0)
+        self._layer_kv[self._layer_key(layer_id)] = LayerKVEntry(
+            k_cache=k_pages.view(n_pages * h_kv * PAGE_ROWS, head_dim),
+            v_cache=None if is_mla else v_pages.view(n_pages * h_kv * PAGE_ROWS, head_dim),
+            total_context_len=n_pages * PAGE_ROWS,
+            cu_seqlens_kv=cu,
+            context_batch_size=n_batch,
+            is_mla=bool(is_mla),
+            num_heads=int(num_heads),
+            head_dim=int(head_dim),
+            dtype=k_pages.dtype,
+            device=dev,
+            block_table=block_table.to(device=dev, dtype=torch.int32).contiguous(),
+        )
+
     def append_kv_cache(
         self,
         layer_id: int | str,
@@ -288,7 +365,7 @@ class InferenceCache:
         entry = self._layer_kv.get(key)
         if entry is None:
             raise ValueError(f"no cached KV entry for layer {layer_id!r}")
-        if entry.cu_seqlens_kv is None:
+        if entry.cu_seqlens_kv is None or entry.block_table is not None:
             raise ValueError("append_kv_cache requires a packed entry (stored with cu_seqlens_kv)")
         h_kv = 1 if entry.is_mla else entry.num_heads
         d = entry.head_dim

@@ -20,7 +20,7 @@ from __future__ import annotations
 import torch
 
 from flash_mlm import _lib
-from flash_mlm.host.cache import InferenceCache, PackMetadata
+from flash_mlm.host.cache import PAGE_ROWS, InferenceCache, PackMetadata
 from flash_mlm.host.host_utils import (
     _compute_total_q_len_padded,
     _device_scope,
@@ -114,6 +114,8 @@ def _prepare(
     inference_cache: InferenceCache | None,
     schedule_cache: dict | None = None,
     ctx_index: torch.Tensor | None = None,
+    block_table: torch.Tensor | None = None,
+    page_stride: int = 0,
 ) -> AttnLaunch:
     lib = _lib.load()
     p = _lib.AttnParams()
@@ -129,6 +131,10 @@ def _prepare(
     p.cu_seqlens_q = _lib.ptr(cu_seqlens_q)
     p.cu_seqlens_kv = _lib.ptr(cu_seqlens_kv)
     p.ctx_index = _lib.ptr(ctx_index)
+    p.ctx_block_table = _lib.ptr(block_table)
+    if block_table is not None:
+        p.ctx_page_stride = page_stride
+        p.ctx_pages_per_batch = int(block_table.shape[1])
     p.q = q.data_ptr()
     p.q_sb, p.q_sh, p.q_sn = q_strides
     p.o = out.data_ptr()
@@ -160,7 +166,7 @@ def _prepare(
             ws = _workspace(inference_cache, ws_bytes, q.device)
             p.workspace = None if ws is None else ws.data_ptr()
             p.workspace_bytes = ws_bytes
-    keep = (q, out, k, v, k_ctx, v_ctx, cu_seqlens_q, cu_seqlens_kv, ctx_index, ws, sched)
+    keep = (q, out, k, v, k_ctx, v_ctx, cu_seqlens_q, cu_seqlens_kv, ctx_index, block_table, ws, sched)
     return AttnLaunch(lib, p, stream, q.device, keep)
 
 
@@ -327,6 +333,17 @@ def _dense_impl(
     return out, plan
 
 
+def _ctx_rows(ctx) -> int:
+    """The kernel's ctx_rows: rows per head of a packed context, or pages of a paged pool."""
+    total = int(ctx.total_context_len)
+    return total // PAGE_ROWS if ctx.block_table is not None else total
+
+
+def _page_stride(ctx, num_heads: int, d: int, is_mla: bool) -> int:
+    """Elements between pages of a paged pool [H_kv, P, PAGE_ROWS, D] (0 when not paged)."""
+    return 0 if ctx.block_table is None else PAGE_ROWS * d
+
+
 def _packed_context(ctx, *, num_heads: int, d: int, is_mla: bool, b: int, prefill: bool, indexed: bool = False):
     """Strides / sizes of a packed (head-major) context entry, validated."""
     total_context_len = int(ctx.total_context_len)
@@ -340,6 +357,8 @@ def _packed_context(ctx, *, num_heads: int, d: int, is_mla: bool, b: int, prefil
         raise ValueError("context_batch_size is incompatible with cu_seqlens_kv length")
     if 1 < cbs < b and not prefill and total_context_len > 0 and not indexed:
         raise ValueError("context_batch_size must be 1 or at least the batch size")
+    if ctx.block_table is not None:  # paged pool [H_kv, P, PAGE_ROWS, D]: heads total_context_len rows apart
+        return cbs, (0, 0 if is_mla else total_context_len * d, d)
     c_strides = (0, 0 if is_mla else total_context_len * d, d)
     return cbs, c_strides
 
@@ -540,12 +559,14 @@ def _compressed_impl(
         cu_seqlens_kv=cu_kv,
         ctx_len=0,
         ctx_batch=cbs,
-        ctx_rows=int(ctx.total_context_len),
+        ctx_rows=_ctx_rows(ctx),
         scale=scale,
         flags=flags,
         inference_cache=inference_cache,
         schedule_cache=q_meta.kernel_schedules if isinstance(q_meta, PackMetadata) else None,
         ctx_index=ctx_index,
+        block_table=ctx.block_table,
+        page_stride=_page_stride(ctx, num_heads, d, is_mla),
     )
     return out, plan
 
@@ -658,13 +679,15 @@ def flash_attn_mlm_precompressed(
             cu_seqlens_kv=ctx.cu_seqlens_kv.to(torch.int32).contiguous(),
             ctx_len=0,
             ctx_batch=cbs,
-            ctx_rows=int(ctx.total_context_len),
+            ctx_rows=_ctx_rows(ctx),
             scale=scale,
             flags=(_lib.FLAG_MLA if is_mla else 0)
             | (_lib.FLAG_PREFILL if prefill else 0)
             | (_lib.FLAG_CAUSAL_SEQ if causal_query_seq_attn else 0),
             inference_cache=inference_cache,
             ctx_index=ctx_index,
+            block_table=ctx.block_table,
+            page_stride=_page_stride(ctx, num_heads, d, is_mla),
         )
 
     if prefill and inference_cache is not None:

@@ -60,6 +60,7 @@ class CacheContext:
     context_len: int
     total_context_len: int
     cu_seqlens_kv: torch.Tensor | None
+    block_table: torch.Tensor | None = None  # paged entries (extension)
 
 
 # ---------------------------------------------------------------------------
@@ -349,6 +350,20 @@ def _maybe_get_cache_context(
 
     total = int(entry.total_context_len)
     context_len = 0
+    if entry.block_table is not None:  # paged entry (extension)
+        if not compressed:
+            raise ValueError("paged KV contexts serve the packed paths (flash_attn_mlm_compressed / _precompressed)")
+        if cbs != stored_cbs:
+            raise ValueError("a paged context cannot be shared with context_batch_size=1")
+        return CacheContext(
+            k_cache=entry.k_cache,
+            v_cache=entry.v_cache,
+            context_batch_size=cbs,
+            context_len=0,
+            total_context_len=total,
+            cu_seqlens_kv=entry.cu_seqlens_kv,
+            block_table=entry.block_table,
+        )
     if compressed:
         cu_kv = entry.cu_seqlens_kv
         if cu_kv is None:

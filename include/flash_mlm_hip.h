@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FMLM_ABI_VERSION 2
+#define FMLM_ABI_VERSION 3
 
 /* element types */
 enum {
@@ -167,6 +167,8 @@ FMLM_API int fmlm_copy_segments(int32_t elem_bytes, const void* src, int64_t src
  * L_b is clamped to N (when N > 0) and to total_q - cu_seqlens_q[b].  Rows p >= L_b of
  * the output are not written.
  * ------------------------------------------------------------------------- */
+#define FMLM_PAGE_ROWS 64  /* rows per page of a paged context (the kernels' key tile) */
+
 typedef struct fmlm_attn_params {
   int32_t dtype;           /* FMLM_DTYPE_* of q, k, v, contexts and o                */
   int32_t flags;           /* FMLM_FLAG_*                                            */
@@ -198,6 +200,17 @@ typedef struct fmlm_attn_params {
                                 index-mapped context batching.  No counterpart in the
                                 reference, whose roadmap lists it ("variable context
                                 batch sizes", README.md:34-36)                         */
+  /* Paged context (NULL block table: contiguous context as above).  Context batch cb has
+   * cu_seqlens_kv[cb+1] - cu_seqlens_kv[cb] rows (or ctx_len); its row j lives in page
+   * ctx_block_table[cb * ctx_pages_per_batch + j / FMLM_PAGE_ROWS], row j % FMLM_PAGE_ROWS:
+   * element page * ctx_page_stride + h * c_sh + (j % FMLM_PAGE_ROWS) * c_sn of k_ctx /
+   * v_ctx.  ctx_rows is then the number of pages in the pool (page ids are clamped to it).
+   * bf16/f16 with linear main keys only.  No counterpart in the reference, whose roadmap
+   * lists paged KV (README.md:41).                                                     */
+  const int32_t* ctx_block_table;
+  int64_t ctx_page_stride;
+  int32_t ctx_pages_per_batch;
+  int32_t reserved0;
 } fmlm_attn_params;
 
 /* Bytes of device workspace (and of a schedule buffer) fmlm_attn_fwd needs for these

@@ -133,3 +133,20 @@ def append_segments(old: np.ndarray, cu_old, new: np.ndarray, cu_new, heads: int
             out[r : r + len(seg_new)] = seg_new
             r += len(seg_new)
     return out, cu_old + cu_new
+
+
+def gather_pages(pool: np.ndarray, block_table, lengths):
+    """Paged context (an extension; the reference's roadmap lists paged KV, README.md:41)
+    -> contiguous head-major cache: pool [P, H_kv, page_rows, D]; batch c's key j is row
+    j % page_rows of page block_table[c][j // page_rows].  Returns (cache [H_kv*T, D],
+    cu [C+1]) with batch c at rows cu[c]..cu[c+1] of every head."""
+    P, H, R, D = pool.shape
+    lengths = [int(x) for x in lengths]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    T = int(cu[-1])
+    out = np.zeros((H * T, D), dtype=pool.dtype)
+    for c, n in enumerate(lengths):
+        for j in range(n):
+            page = int(block_table[c][j // R])
+            out[np.arange(H) * T + cu[c] + j] = pool[page, :, j % R]
+    return out, cu

@@ -196,3 +196,15 @@ def test_append_segments_identities_and_associativity(seed):
     tl, tr = left.shape[0] // H, right.shape[0] // H
     for h in range(H):
         np.testing.assert_array_equal(left[h * tl : h * tl + cl[-1]], right[h * tr : h * tr + cr[-1]])
+
+
+def test_gather_pages_known_answer():
+    # pool of 3 pages x 1 head x 2 rows; batch 0 = pages [2, 0] (3 keys), batch 1 = page [1] (1 key)
+    pool = np.arange(6, dtype=np.float64).reshape(3, 1, 2, 1)  # page p rows (2p, 2p+1)
+    cache, cu = pack_ref.gather_pages(pool, [[2, 0], [1, 9]], [3, 1])
+    np.testing.assert_array_equal(cu, [0, 3, 4])
+    np.testing.assert_array_equal(cache[:, 0], [4, 5, 0, 2])
+    # two heads: each head keeps its own rows of the page
+    pool2 = np.arange(8, dtype=np.float64).reshape(2, 2, 2, 1)  # page p, head h rows (4p+2h, 4p+2h+1)
+    cache2, _ = pack_ref.gather_pages(pool2, [[1, 0]], [3])
+    np.testing.assert_array_equal(cache2[:, 0], [4, 5, 0, 6, 7, 2])
