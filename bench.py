@@ -434,6 +434,32 @@ def hbm_kernels(case: Case, reps: int = 30) -> dict:
     return out
 
 
+def backward_kernels(case: Case, reps: int = 20) -> dict | None:
+    """fmlm_attn_bwd (the dq kernel, then the dK/dV kernels of the main keys and of the
+    context) on this workload's prepared call, gradients of q, k, v and of the cached
+    context: median of HIP-event times with L2/MALL flushed before each launch.
+    Effective work = 2.5x the forward's FLOPs (the products dP = dO V^T, dV = P^T dO,
+    dq = dS K, dK = dS^T q besides S = q K^T), padding excluded; the kernels also
+    recompute S twice for dq (the row statistics, then dS), which is not counted."""
+    from flash_mlm import _lib
+    from flash_mlm.host import host as hh
+
+    plan = case.attention
+    if plan is None or case.dtype not in (torch.bfloat16, torch.float16) or case.D not in (32, 64, 128, 256) \
+            or plan.params.ctx_block_table:
+        return None
+    plan()  # the forward output the backward reads
+    out = plan.keep[1]
+    dout = torch.randn(out.shape, device=out.device).to(out.dtype)
+    g, keep = hh._backward_args(plan, out, dout, want_ctx=True)
+    ms = _event_ms(lambda: _lib.check(plan.lib.fmlm_attn_bwd(plan.params, g, plan.stream), "fmlm_attn_bwd"), reps)
+    F = 2.5 * case.flops
+    peak = MFMA_PEAK_TFLOPS[case.dtype]
+    return {"ms": round(ms, 5), "effective_gflop": round(F / 1e9, 4), "tflops": round(F / (ms * 1e-3) / 1e12, 3),
+            "frac": round(F / (ms * 1e-3) / 1e12 / peak, 5),
+            "grads": "q, k, v" + (", context" if g.dk_ctx else "")}
+
+
 def cpu_baseline(case: Case, budget_s: float = 20.0) -> dict:
     """The reference's per-sequence PyTorch SDPA path (oracle/cpu_baseline.py) on this
     host's CPU cores, fp32, over a bounded prefix of the workload's sequences."""
@@ -532,6 +558,9 @@ def main() -> None:
     hbm = hbm_kernels(case)
     if hbm:
         print(f"[bench] copy kernels: {hbm}", file=sys.stderr, flush=True)
+    bwd = backward_kernels(case)
+    if bwd:
+        print(f"[bench] backward: {bwd}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(case)
@@ -556,6 +585,7 @@ def main() -> None:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "hbm_kernels": hbm or None,
+        "backward": bwd,
     }
     print(json.dumps(line), flush=True)
 

@@ -56,53 +56,6 @@ constexpr int kMaxSplits = 16;
 constexpr int kMinSplitTiles = 8;   // key tiles per part at least
 constexpr float kSplitRounds = 1.5f;
 
-struct SeqInfo {
-  int q0, len;       // packed start and clamped length of sequence b
-  int ctx, mainlen;  // context keys and main keys it attends to
-};
-
-// context batch of sequence b: ctx_index[b] (clamped) when given, else b for a
-// full-batch context and 0 for a shared one
-FMLM_DEV int ctx_batch_of(const fmlm_attn_params& p, int b) {
-  if (p.ctx_index) return min(max(p.ctx_index[b], 0), max(p.ctx_batch - 1, 0));
-  return p.ctx_batch > 1 ? b : 0;
-}
-
-// context rows [c0, c1) of context batch cb (contiguous context), or (0, n) of a paged one
-FMLM_DEV void ctx_range(const fmlm_attn_params& p, int cb, int& c0, int& c1) {
-  c0 = 0;
-  c1 = p.ctx_len;
-  if (p.cu_seqlens_kv) {
-    if (p.ctx_block_table) {
-      c1 = p.cu_seqlens_kv[cb + 1] - p.cu_seqlens_kv[cb];
-    } else {
-      c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
-      c1 = min(max(p.cu_seqlens_kv[cb + 1], c0), p.ctx_rows);
-    }
-  }
-  if (p.ctx_block_table) c1 = min(max(c1, 0), p.ctx_pages_per_batch * FMLM_PAGE_ROWS);
-}
-
-FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
-  const int32_t* cu = p.cu_seqlens_q;
-  SeqInfo s;
-  s.q0 = seq_start(cu, b, p.N);
-  int L = p.N;
-  if (cu) {
-    L = cu[b + 1] - s.q0;
-    if (p.N > 0) L = min(L, p.N);
-    L = max(min(L, p.total_q - s.q0), 0);
-  }
-  s.len = L;
-  s.ctx = 0;
-  if (!(p.flags & FMLM_FLAG_PREFILL)) {
-    int c0, c1;
-    ctx_range(p, ctx_batch_of(p, b), c0, c1);
-    s.ctx = max(c1 - c0, 0);
-  }
-  s.mainlen = ((p.flags & FMLM_FLAG_CAUSAL_SEQ) && cu) ? s.q0 + L : L;
-  return s;
-}
 
 __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn_params p, int BQ,
                                                                  int capacity, int slots,
@@ -391,42 +344,10 @@ FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const i
   return true;
 }
 
-FMLM_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
 // MFMA kernel (bf16 / fp16)
 // ---------------------------------------------------------------------------
-template <typename T>
-struct Mfma;
-template <>
-struct Mfma<bf16> {
-  typedef bf16x8 v8;
-  static FMLM_DEV f32x4 run(v8 a, v8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<f16> {
-  typedef f16x8 v8;
-  static FMLM_DEV f32x4 run(v8 a, v8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-#define FMLM_LDS __attribute__((address_space(3)))
-
-// ds_read_b64_tr_b16: within each group of 16 lanes, lane j supplies the address of
-// four consecutive 16-bit elements M[j][0..3]; lane i receives M[4e + i/4][i%4], e=0..3.
-FMLM_DEV s16x4 lds_read_tr16(const void* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLM_LDS s16x4*)(p));
-}
-// the same from an LDS byte address
-FMLM_DEV s16x4 lds_read_tr16_at(uint32_t a) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLM_LDS s16x4*)(uintptr_t)a);
-}
 
 template <typename T, int D, int QB, int NW, int BK>
 struct MfmaCfg {

@@ -1,0 +1,632 @@
+// Backward of the fused MLM attention for gfx950 (bf16 / fp16, MFMA 16x16x32).
+//
+// No counterpart in the reference: its roadmap lists backpropagation
+// (README.md:26-28).  What is differentiated is the forward of fmlm_attn.hip, i.e. the
+// reference's attention over [cached context || main keys] (mlm_kernel_impl.py:10-62,
+// 65-216, 219-390).  For one query row with key set K, values V, P = softmax(scale q K^T)
+// and O = P V:
+//   delta = rowsum(dO * O),  dP = dO V^T,  dS = scale * P * (dP - delta),
+//   dq = dS K,  dK = dS^T q,  dV = P^T dO.
+// Two kernels, no atomics, so every gradient row has exactly one writer:
+//   attn_bwd_dq_kernel   one workgroup per (query tile, head, sequence), as in the
+//     forward.  Pass 1 recomputes each row's log2-sum-exp over the key set, pass 2
+//     accumulates dq^T = K^T dS^T.  It stores lse and delta per row for the next kernel.
+//   attn_bwd_dkv_kernel  one workgroup per 64-key tile of a key segment (the main keys of
+//     a sequence, the causal token range of a head, or a context batch), 16 keys per
+//     wave.  It walks every query row that attends to those keys in steps of 32 rows
+//     staged through LDS and accumulates dK^T = Q^T dS and dV^T = dO^T P in registers.
+//     Keys whose head stride is 0 (the MLA latent) are shared by all heads and take the
+//     queries of every head; with MLA (V = K) both gradients land in dk.
+// Layouts: every product is in the forward's transposed MFMA form, so the accumulator
+// lane (j + 16g) holds rows 4g..4g+3 of column j, and the transposed operands come from
+// row-major LDS tiles through ds_read_b64_tr_b16.
+#include "fmlm_common.h"
+
+#include <mutex>
+
+namespace fmlm {
+namespace {
+
+constexpr int kBwdNW = 4;   // waves per workgroup
+constexpr int kBwdBK = 64;  // keys per dq-kernel tile and per dkv workgroup (16 per wave)
+constexpr int kBwdQS = 32;  // query rows per dkv step
+
+template <int D>
+struct BwdCfg {
+  static constexpr int NT = kBwdNW * 64;
+  static constexpr int KC = D / 32;               // 32-wide contraction steps over D
+  static constexpr int NDB = D / 16;              // 16-wide column blocks
+  static constexpr int RS = D + 16;               // LDS row stride (elements)
+  static constexpr int C8 = D / 8;                // 16-byte chunks per row
+  static constexpr int QB = D >= 128 ? 1 : 2;     // 16-row query blocks per wave (dq kernel)
+  static constexpr int BQ = kBwdNW * QB * 16;     // query rows per dq workgroup
+  static constexpr int NKB = kBwdBK / 16;
+  static constexpr int NKS = kBwdBK / 32;
+  static constexpr int DQ_LDS = 2 * kBwdBK * RS * 2;                  // K and V tiles
+  static constexpr int DKV_LDS = 2 * kBwdQS * RS * 2 + 2 * kBwdQS * 4;  // Q, dO, lse, delta
+  static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
+};
+
+// element offset of row (sequence b, head h, position pos) in a tensor of `layout`
+FMLM_DEV int64_t row_at(int layout, int b, int h, int q0, int pos, int64_t sb, int64_t sh, int64_t sn) {
+  return layout == FMLM_LAYOUT_PACKED ? (int64_t)h * sh + (int64_t)(q0 + pos) * sn
+                                      : (int64_t)b * sb + (int64_t)h * sh + (int64_t)pos * sn;
+}
+
+// One key segment for key head h: rows kbase + j*ksn of k (vbase + j*vsn of v), j < n;
+// the gradient rows of key j are dkbase + j*dksn of dk (dvbase + j*dvsn of dv).
+struct BSeg {
+  const char* k;
+  const char* v;
+  char* dk;
+  char* dv;
+  int64_t kbase, vbase, ksn, vsn;
+  int64_t dkbase, dvbase, dksn, dvsn;
+  int n;
+};
+
+// context rows of context batch cb (mlm_kernel_impl.py:297-313 packed, :132-141 dense)
+FMLM_DEV BSeg ctx_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int cb, int h) {
+  const bool mla = p.flags & FMLM_FLAG_MLA;
+  BSeg s;
+  int c0, c1;
+  ctx_range(p, cb, c0, c1);
+  s.n = (p.flags & FMLM_FLAG_PREFILL) || !p.k_ctx ? 0 : max(c1 - c0, 0);
+  s.k = (const char*)p.k_ctx;
+  s.v = (const char*)(mla ? p.k_ctx : p.v_ctx);
+  s.dk = (char*)g.dk_ctx;
+  s.dv = (char*)(mla ? g.dk_ctx : g.dv_ctx);
+  s.kbase = s.vbase = (int64_t)cb * p.c_sb + (int64_t)h * p.c_sh + (int64_t)c0 * p.c_sn;
+  s.dkbase = s.dvbase = s.kbase;
+  s.ksn = s.vsn = s.dksn = s.dvsn = p.c_sn;
+  return s;
+}
+
+// main keys of sequence b (mlm_kernel_impl.py:288-293, 360-379): its own tokens, or
+// with causal_query_seq_attn the packed tokens [0, cu[b+1]) (n = those of all of them
+// when b < 0)
+FMLM_DEV BSeg main_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int b, int h) {
+  const bool mla = p.flags & FMLM_FLAG_MLA;
+  const int64_t v_sb = mla ? p.k_sb : p.v_sb, v_sh = mla ? p.k_sh : p.v_sh, v_sn = mla ? p.k_sn : p.v_sn;
+  const int64_t dv_sb = mla ? g.dk_sb : g.dv_sb, dv_sh = mla ? g.dk_sh : g.dv_sh, dv_sn = mla ? g.dk_sn : g.dv_sn;
+  BSeg s;
+  s.k = (const char*)p.k;
+  s.v = (const char*)(mla ? p.k : p.v);
+  s.dk = (char*)g.dk;
+  s.dv = (char*)(mla ? g.dk : g.dv);
+  s.ksn = p.k_sn;
+  s.vsn = v_sn;
+  s.dksn = g.dk_sn;
+  s.dvsn = dv_sn;
+  const bool causal = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q;
+  if (causal) {  // packed K/V: token j is row h*sh + j*sn
+    s.n = b < 0 ? min(p.cu_seqlens_q[p.B], p.total_q) : seq_info(p, b).mainlen;
+    s.kbase = (int64_t)h * p.k_sh;
+    s.vbase = (int64_t)h * v_sh;
+    s.dkbase = (int64_t)h * g.dk_sh;
+    s.dvbase = (int64_t)h * dv_sh;
+    return s;
+  }
+  const SeqInfo si = seq_info(p, b);
+  s.n = si.len;
+  s.kbase = row_at(p.kv_layout, b, h, si.q0, 0, p.k_sb, p.k_sh, p.k_sn);
+  s.vbase = row_at(p.kv_layout, b, h, si.q0, 0, v_sb, v_sh, v_sn);
+  s.dkbase = row_at(p.kv_layout, b, h, si.q0, 0, g.dk_sb, g.dk_sh, g.dk_sn);
+  s.dvbase = row_at(p.kv_layout, b, h, si.q0, 0, dv_sb, dv_sh, dv_sn);
+  return s;
+}
+
+FMLM_DEV u32x4 ld16(const char* base, int64_t elem) { return *(const u32x4*)(base + elem * 2); }
+
+// A-operand fragment of X^T (16 columns of X from column 16db, 32 rows from row0) from a
+// row-major LDS tile: lane (i + 16g) receives X[row0 + 16h + 4g + e][16db + i] as element
+// 4h + e, the row order of the packed B operands below.
+template <typename T>
+FMLM_DEV typename Mfma<T>::v8 tr_frag(const T* tile, int rs, int row0, int db, int l16, int g) {
+  const T* base = tile + (row0 + g * 4 + (l16 >> 2)) * rs + db * 16 + (l16 & 3) * 4;
+  const s16x4 lo = lds_read_tr16(base);
+  const s16x4 hi = lds_read_tr16(base + 16 * rs);
+  return __builtin_bit_cast(typename Mfma<T>::v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// ---------------------------------------------------------------------------
+// dq kernel: grid (query tiles, H, B), kBwdNW waves, QB blocks of 16 rows per wave.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_attn_params p,
+                                                                     const fmlm_attn_grads g) {
+  typedef BwdCfg<D> C;
+  typedef typename Mfma<T>::v8 v8;
+  constexpr int QB = C::QB;
+  extern __shared__ __align__(16) char smem_raw[];
+  T* const Ks = (T*)smem_raw;
+  T* const Vs = Ks + kBwdBK * C::RS;
+
+  const int b = blockIdx.z, h = blockIdx.y;
+  const SeqInfo si = seq_info(p, b);
+  const int qpos0 = blockIdx.x * C::BQ;
+  if (qpos0 >= si.len) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, gq = lane >> 4;
+  const float c = p.scale * kLog2e;  // scores in log2 units
+
+  BSeg seg[2];
+  seg[0] = ctx_seg(p, g, ctx_batch_of(p, b), h);
+  seg[1] = main_seg(p, g, b, h);
+
+  // Q and dO fragments (B operands): lane (q + 16g), block qb, step kc holds row q's
+  // columns kc*32 + 8g .. +8; delta = rowsum(dO * O) of the lane's row
+  v8 qf[QB][C::KC], df[QB][C::KC];
+  float delta[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int row = qpos0 + (wave * QB + qb) * 16 + l16;
+    const bool ok = row < si.len;
+    const int64_t qo = row_at(p.q_layout, b, h, si.q0, row, p.q_sb, p.q_sh, p.q_sn);
+    const int64_t doo = row_at(p.o_layout, b, h, si.q0, row, g.do_sb, g.do_sh, g.do_sn);
+    const int64_t oo = row_at(p.o_layout, b, h, si.q0, row, p.o_sb, p.o_sh, p.o_sn);
+    float dsum = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc) {
+      const int col = kc * 32 + gq * 8;
+      u32x4 rq = u32x4{0u, 0u, 0u, 0u}, rd = rq, ro = rq;
+      if (ok) {
+        rq = ld16((const char*)p.q, qo + col);
+        rd = ld16((const char*)g.dout, doo + col);
+        ro = ld16((const char*)p.o, oo + col);
+      }
+      qf[qb][kc] = __builtin_bit_cast(v8, rq);
+      df[qb][kc] = __builtin_bit_cast(v8, rd);
+      const v8 ov = __builtin_bit_cast(v8, ro);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum += (float)df[qb][kc][e] * (float)ov[e];
+    }
+    dsum += __shfl_xor(dsum, 16);
+    dsum += __shfl_xor(dsum, 32);
+    delta[qb] = dsum;
+  }
+
+  // stage keys [j0, j0 + 64) of a segment (and their values) in LDS; rows past the end are 0
+  auto load_tile = [&](const BSeg& s, int j0, bool with_v) {
+#pragma unroll
+    for (int it = tid; it < kBwdBK * C::C8; it += C::NT) {
+      const int row = it / C::C8, c8 = it % C::C8;
+      const int key = j0 + row;
+      u32x4 kv = u32x4{0u, 0u, 0u, 0u}, vv = kv;
+      if (key < s.n) {
+        kv = ld16(s.k, s.kbase + (int64_t)key * s.ksn + c8 * 8);
+        if (with_v) vv = ld16(s.v, s.vbase + (int64_t)key * s.vsn + c8 * 8);
+      }
+      *(u32x4*)(Ks + row * C::RS + c8 * 8) = kv;
+      if (with_v) *(u32x4*)(Vs + row * C::RS + c8 * 8) = vv;
+    }
+  };
+  // S^T = K Q^T of the staged tile: lane (q + 16g) reg r = S[query q][key 16kb + 4g + r]
+  auto scores = [&](f32x4 (&s)[C::NKB][QB]) {
+#pragma unroll
+    for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) s[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc)
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb) {
+        const v8 a = *(const v8*)(Ks + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) s[kb][qb] = Mfma<T>::run(a, qf[qb][kc], s[kb][qb]);
+      }
+  };
+
+  // ---- pass 1: log2-sum-exp of each row over the whole key set
+  float m_i[QB], l_i[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_i[qb] = -INFINITY;
+    l_i[qb] = 0.f;
+  }
+  for (int sg = 0; sg < 2; ++sg) {
+    for (int j0 = 0; j0 < seg[sg].n; j0 += kBwdBK) {
+      const int nk = min(kBwdBK, seg[sg].n - j0);
+      __syncthreads();
+      load_tile(seg[sg], j0, false);
+      __syncthreads();
+      f32x4 s[C::NKB][QB];
+      scores(s);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float z = kb * 16 + gq * 4 + r < nk ? s[kb][qb][r] * c : -INFINITY;
+            s[kb][qb][r] = z;
+            mx = fmaxf(mx, z);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_i[qb], mx);
+        if (m_new == -INFINITY) continue;  // no key yet (row-uniform)
+        float rs = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rs += fast_exp2(s[kb][qb][r] - m_new);
+        l_i[qb] = l_i[qb] * fast_exp2(m_i[qb] - m_new) + rs;
+        m_i[qb] = m_new;
+      }
+    }
+  }
+  float lse[QB];
+  float* const st_lse = (float*)g.workspace;
+  float* const st_delta = st_lse + (int64_t)p.H * p.total_q;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    float l = l_i[qb];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    lse[qb] = l > 0.f ? m_i[qb] + __log2f(l) : INFINITY;  // no keys: P = 0
+    const int row = qpos0 + (wave * QB + qb) * 16 + l16;
+    if (gq == 0 && row < si.len) {
+      const int64_t at = (int64_t)h * p.total_q + si.q0 + row;
+      st_lse[at] = lse[qb];
+      st_delta[at] = delta[qb];
+    }
+  }
+
+  // ---- pass 2: dq^T += K^T dS^T
+  f32x4 dq[C::NDB][QB];
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) dq[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int sg = 0; sg < 2; ++sg) {
+    for (int j0 = 0; j0 < seg[sg].n; j0 += kBwdBK) {
+      const int nk = min(kBwdBK, seg[sg].n - j0);
+      __syncthreads();
+      load_tile(seg[sg], j0, true);
+      __syncthreads();
+      f32x4 s[C::NKB][QB], dp[C::NKB][QB];
+      scores(s);
+      // dP^T = V dO^T, same layout as S^T
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < C::KC; ++kc)
+#pragma unroll
+        for (int kb = 0; kb < C::NKB; ++kb) {
+          const v8 a = *(const v8*)(Vs + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = Mfma<T>::run(a, df[qb][kc], dp[kb][qb]);
+        }
+      // dS = scale * P * (dP - delta), packed as B operands: element 4h + r of step ks is
+      // key 32ks + 16h + 4g + r
+      v8 dsf[C::NKS][QB];
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const bool ok = kb * 16 + gq * 4 + r < nk;
+            const float pv = ok ? fast_exp2(fmaf(s[kb][qb][r], c, -lse[qb])) : 0.f;
+            dsf[kb >> 1][qb][(kb & 1) * 4 + r] = (T)(pv * (dp[kb][qb][r] - delta[qb]) * p.scale);
+          }
+#pragma unroll
+      for (int ks = 0; ks < C::NKS; ++ks)
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) {
+          const v8 a = tr_frag<T>(Ks, C::RS, ks * 32, db, l16, gq);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) dq[db][qb] = Mfma<T>::run(a, dsf[ks][qb], dq[db][qb]);
+        }
+    }
+  }
+
+  // ---- dq rows: lane (q + 16g) holds dq[q][16db + 4g .. +4]
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int row = qpos0 + (wave * QB + qb) * 16 + l16;
+    if (row >= si.len) continue;
+    const int64_t off = row_at(p.q_layout, b, h, si.q0, row, g.dq_sb, g.dq_sh, g.dq_sn);
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) {
+      T v4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = (T)dq[db][qb][r];
+      *(u32x2*)((char*)g.dq + (off + db * 16 + gq * 4) * 2) = *(const u32x2*)v4;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV kernel.  SEG: 0 = main keys of sequence blockIdx.z, 1 = causal token range,
+// 2 = context batch blockIdx.z.  grid (key tiles, key heads, slots).
+// ---------------------------------------------------------------------------
+template <typename T, int D, int SEG>
+__global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm_attn_params p,
+                                                                      const fmlm_attn_grads g) {
+  typedef BwdCfg<D> C;
+  typedef typename Mfma<T>::v8 v8;
+  extern __shared__ __align__(16) char smem_raw[];
+  T* const Qs = (T*)smem_raw;
+  T* const Os = Qs + kBwdQS * C::RS;  // dO rows
+  float* const lse_s = (float*)(Os + kBwdQS * C::RS);
+  float* const dl_s = lse_s + kBwdQS;
+
+  const bool mla = p.flags & FMLM_FLAG_MLA;
+  const int32_t* cu = p.cu_seqlens_q;
+  const int kh = blockIdx.y, slot = blockIdx.z;
+  const int j0 = blockIdx.x * kBwdBK;
+  BSeg s;
+  int b_lo, b_hi;  // sequences whose queries may attend to these keys
+  bool shared;     // key rows shared by all heads (head stride 0)
+  if (SEG == 2) {
+    s = ctx_seg(p, g, slot, kh);
+    b_lo = 0;
+    b_hi = p.B;
+    shared = p.c_sh == 0;
+  } else if (SEG == 1) {
+    s = main_seg(p, g, -1, kh);
+    b_lo = j0 < s.n ? find_seq(cu, p.B, j0) : p.B;
+    b_hi = p.B;
+    shared = p.k_sh == 0;
+  } else {
+    s = main_seg(p, g, slot, kh);
+    b_lo = slot;
+    b_hi = slot + 1;
+    shared = p.k_sh == 0;
+  }
+  if (j0 >= s.n) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, gq = lane >> 4;
+  const float c = p.scale * kLog2e;
+  const float* const st_lse = (const float*)g.workspace;
+  const float* const st_delta = st_lse + (int64_t)p.H * p.total_q;
+
+  // this lane's key (B-operand column / accumulator column) and its K, V fragments:
+  // kf[kc] = K[key][kc*32 + 8g .. +8]
+  const int key = j0 + wave * 16 + l16;
+  const bool kok = key < s.n;
+  v8 kf[C::KC], vf[C::KC];
+#pragma unroll
+  for (int kc = 0; kc < C::KC; ++kc) {
+    u32x4 rk = u32x4{0u, 0u, 0u, 0u}, rv = rk;
+    if (kok) {
+      rk = ld16(s.k, s.kbase + (int64_t)key * s.ksn + kc * 32 + gq * 8);
+      if (!mla) rv = ld16(s.v, s.vbase + (int64_t)key * s.vsn + kc * 32 + gq * 8);
+    }
+    kf[kc] = __builtin_bit_cast(v8, rk);
+    vf[kc] = mla ? kf[kc] : __builtin_bit_cast(v8, rv);
+  }
+  f32x4 dkt[C::NDB], dvt[C::NDB];
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db) {
+    dkt[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dvt[db] = dkt[db];
+  }
+
+  const int hq_lo = shared ? 0 : kh, hq_hi = shared ? p.H : kh + 1;
+  for (int hq = hq_lo; hq < hq_hi; ++hq) {
+    for (int b = b_lo; b < b_hi; ++b) {
+      if (SEG == 2 && ctx_batch_of(p, b) != slot) continue;
+      const SeqInfo si = seq_info(p, b);
+      const int lim = SEG == 1 ? si.mainlen : 0x7fffffff;  // causal: tokens < cu[b+1]
+      if (lim <= j0) continue;
+      const bool kvalid = kok && key < lim;
+      for (int p0 = 0; p0 < si.len; p0 += kBwdQS) {
+        __syncthreads();  // the previous step's LDS reads are done
+#pragma unroll
+        for (int it = tid; it < kBwdQS * C::C8; it += C::NT) {
+          const int r = it / C::C8, c8 = it % C::C8;
+          const int pos = p0 + r;
+          u32x4 rq = u32x4{0u, 0u, 0u, 0u}, rd = rq;
+          if (pos < si.len) {
+            rq = ld16((const char*)p.q, row_at(p.q_layout, b, hq, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + c8 * 8);
+            rd = ld16((const char*)g.dout, row_at(p.o_layout, b, hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + c8 * 8);
+          }
+          *(u32x4*)(Qs + r * C::RS + c8 * 8) = rq;
+          *(u32x4*)(Os + r * C::RS + c8 * 8) = rd;
+        }
+        if (tid < kBwdQS) {
+          const int pos = p0 + tid;
+          const bool ok = pos < si.len;
+          const int64_t at = (int64_t)hq * p.total_q + si.q0 + pos;
+          lse_s[tid] = ok ? st_lse[at] : INFINITY;  // padding rows: P = 0
+          dl_s[tid] = ok ? st_delta[at] : 0.f;
+        }
+        __syncthreads();
+
+        // S and dP for the two 16-row halves: lane (key + 16g) reg r = row 16h + 4g + r;
+        // P and dS packed as B operands (element 4h + r)
+        v8 pb, dsb;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = sc;
+#pragma unroll
+          for (int kc = 0; kc < C::KC; ++kc) {
+            const v8 aq = *(const v8*)(Qs + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
+            const v8 ao = *(const v8*)(Os + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
+            sc = Mfma<T>::run(aq, kf[kc], sc);
+            dp = Mfma<T>::run(ao, vf[kc], dp);
+          }
+          const f32x4 L4 = *(const f32x4*)(lse_s + hh * 16 + gq * 4);
+          const f32x4 D4 = *(const f32x4*)(dl_s + hh * 16 + gq * 4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pv = kvalid ? fast_exp2(fmaf(sc[r], c, -L4[r])) : 0.f;
+            pb[hh * 4 + r] = (T)pv;
+            dsb[hh * 4 + r] = (T)(pv * (dp[r] - D4[r]) * p.scale);
+          }
+        }
+        // dV^T += dO^T P and dK^T += Q^T dS (MLA: both into dK)
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) {
+          const v8 ao = tr_frag<T>(Os, C::RS, 0, db, l16, gq);
+          const v8 aq = tr_frag<T>(Qs, C::RS, 0, db, l16, gq);
+          if (mla) {
+            dkt[db] = Mfma<T>::run(ao, pb, dkt[db]);
+          } else {
+            dvt[db] = Mfma<T>::run(ao, pb, dvt[db]);
+          }
+          dkt[db] = Mfma<T>::run(aq, dsb, dkt[db]);
+        }
+      }
+    }
+  }
+
+  // ---- rows: lane (key + 16g) holds d?[key][16db + 4g .. +4]
+  if (!kok) return;
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db) {
+    T k4[4], v4[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      k4[r] = (T)dkt[db][r];
+      v4[r] = (T)dvt[db][r];
+    }
+    *(u32x2*)(s.dk + (s.dkbase + (int64_t)key * s.dksn + db * 16 + gq * 4) * 2) = *(const u32x2*)k4;
+    if (!mla) *(u32x2*)(s.dv + (s.dvbase + (int64_t)key * s.dvsn + db * 16 + gq * 4) * 2) = *(const u32x2*)v4;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct BwdFns {
+  const void* dq;
+  const void* dkv[3];
+  int dq_lds, dkv_lds, bq;
+};
+
+template <typename T, int D>
+static BwdFns bwd_fns() {
+  typedef BwdCfg<D> C;
+  return BwdFns{(const void*)attn_bwd_dq_kernel<T, D>,
+                {(const void*)attn_bwd_dkv_kernel<T, D, 0>, (const void*)attn_bwd_dkv_kernel<T, D, 1>,
+                 (const void*)attn_bwd_dkv_kernel<T, D, 2>},
+                C::DQ_LDS,
+                C::DKV_LDS,
+                C::BQ};
+}
+
+template <typename T>
+static bool pick_bwd(int D, BwdFns& f) {
+  switch (D) {
+    case 32: f = bwd_fns<T, 32>(); return true;
+    case 64: f = bwd_fns<T, 64>(); return true;
+    case 128: f = bwd_fns<T, 128>(); return true;
+    case 256: f = bwd_fns<T, 256>(); return true;
+    default: return false;
+  }
+}
+
+static int raise_lds(const void* fn, int bytes) {
+  if (bytes <= 65536) return 0;
+  static std::mutex mu;
+  static const void* done[32];
+  static int n_done = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_done; ++i)
+    if (done[i] == fn) return 0;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return (int)e;
+  if (n_done < 32) done[n_done++] = fn;
+  return 0;
+}
+
+static bool row_ok(const void* ptr, int64_t sb, int64_t sh, int64_t sn) {
+  // 16-byte aligned rows: base and every row stride a multiple of 8 elements
+  return ((uintptr_t)ptr % 16 == 0) && sb % 8 == 0 && sh % 8 == 0 && sn % 8 == 0 && sn >= 0 &&
+         sn < (1 << 22);
+}
+
+static int check_bwd(const fmlm_attn_params& p, const fmlm_attn_grads& g, BwdFns& f) {
+  if (p.B < 0 || p.H < 0 || p.N < 0 || p.total_q < 0 || p.ctx_len < 0) return FMLM_E_ARG;
+  const bool mla = p.flags & FMLM_FLAG_MLA;
+  if (!p.q || !p.o || !p.k || (!mla && !p.v) || !g.dout || !g.dq || !g.dk || (!mla && !g.dv)) return FMLM_E_ARG;
+  if (p.dtype == FMLM_DTYPE_BF16) {
+    if (!pick_bwd<bf16>(p.D, f)) return FMLM_E_HEAD_DIM;
+  } else if (p.dtype == FMLM_DTYPE_F16) {
+    if (!pick_bwd<f16>(p.D, f)) return FMLM_E_HEAD_DIM;
+  } else {
+    return FMLM_E_DTYPE;
+  }
+  const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
+  if (causal && (!p.cu_seqlens_q || p.kv_layout != FMLM_LAYOUT_PACKED)) return FMLM_E_ARG;
+  if (p.ctx_block_table) return FMLM_E_ARG;  // paged contexts: forward only
+  // keys shared by all heads must be shared by K and V alike
+  if (!mla && ((p.k_sh == 0) != (p.v_sh == 0))) return FMLM_E_ARG;
+  if (!row_ok(p.q, p.q_sb, p.q_sh, p.q_sn) || !row_ok(p.o, p.o_sb, p.o_sh, p.o_sn) ||
+      !row_ok(p.k, p.k_sb, p.k_sh, p.k_sn) || (!mla && !row_ok(p.v, p.v_sb, p.v_sh, p.v_sn)) ||
+      !row_ok(g.dout, g.do_sb, g.do_sh, g.do_sn) || !row_ok(g.dq, g.dq_sb, g.dq_sh, g.dq_sn) ||
+      !row_ok(g.dk, g.dk_sb, g.dk_sh, g.dk_sn) || (!mla && !row_ok(g.dv, g.dv_sb, g.dv_sh, g.dv_sn)))
+    return FMLM_E_ALIGN;
+  // the gradients of shared keys are shared too
+  if ((p.k_sh == 0) != (g.dk_sh == 0) || (!mla && (p.v_sh == 0) != (g.dv_sh == 0))) return FMLM_E_ARG;
+  if (g.dk_ctx) {
+    if (!p.k_ctx || (!mla && (!p.v_ctx || !g.dv_ctx))) return FMLM_E_ARG;
+    if (!row_ok(p.k_ctx, p.c_sb, p.c_sh, p.c_sn) || !row_ok(g.dk_ctx, p.c_sb, p.c_sh, p.c_sn) ||
+        (!mla && (!row_ok(p.v_ctx, p.c_sb, p.c_sh, p.c_sn) || !row_ok(g.dv_ctx, p.c_sb, p.c_sh, p.c_sn))))
+      return FMLM_E_ALIGN;
+    if ((p.cu_seqlens_kv || p.ctx_index) && p.ctx_batch < 1) return FMLM_E_ARG;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace fmlm
+
+using namespace fmlm;
+
+extern "C" int fmlm_attn_grads_size(void) { return (int)sizeof(fmlm_attn_grads); }
+
+extern "C" int64_t fmlm_attn_bwd_workspace_bytes(const fmlm_attn_params* p) {
+  if (!p || p->H < 0 || p->total_q < 0) return FMLM_E_ARG;
+  const int64_t bytes = 2 * (int64_t)p->H * p->total_q * 4;
+  return (bytes + 255) / 256 * 256;
+}
+
+extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* gp, void* stream) {
+  if (!pp || !gp) return FMLM_E_ARG;
+  const fmlm_attn_params& p = *pp;
+  const fmlm_attn_grads& g = *gp;
+  BwdFns f;
+  int rc = check_bwd(p, g, f);
+  if (rc) return rc;
+  if (p.B == 0 || p.H == 0 || p.total_q == 0) return 0;
+  if (!g.workspace || g.workspace_bytes < fmlm_attn_bwd_workspace_bytes(pp)) return FMLM_E_WORKSPACE;
+  if (p.B > 65535 || p.H > 65535 || p.ctx_batch > 65535) return FMLM_E_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  const bool prefill = p.flags & FMLM_FLAG_PREFILL;
+  const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
+  const int64_t maxlen = p.N > 0 ? p.N : p.total_q;
+  fmlm_attn_params pc = p;
+  fmlm_attn_grads gc = g;
+  void* args[] = {(void*)&pc, (void*)&gc};
+
+  // 1. dq (+ the row statistics)
+  if ((rc = raise_lds(f.dq, f.dq_lds))) return rc;
+  hipError_t e = hipLaunchKernel(f.dq, dim3((unsigned)((maxlen + f.bq - 1) / f.bq), p.H, p.B), dim3(kBwdNW * 64),
+                                 args, (size_t)f.dq_lds, s);
+  if (e != hipSuccess) return (int)e;
+  // 2. main keys
+  const unsigned kheads = p.k_sh == 0 ? 1u : (unsigned)p.H;
+  const int64_t mrows = causal ? p.total_q : maxlen;
+  e = hipLaunchKernel(causal ? f.dkv[1] : f.dkv[0], dim3((unsigned)((mrows + kBwdBK - 1) / kBwdBK), kheads, causal ? 1 : p.B),
+                      dim3(kBwdNW * 64), args, (size_t)f.dkv_lds, s);
+  if (e != hipSuccess) return (int)e;
+  // 3. context keys
+  if (g.dk_ctx && !prefill && p.k_ctx) {
+    const int64_t crows = p.cu_seqlens_kv ? p.ctx_rows : p.ctx_len;
+    const int cbs = (p.cu_seqlens_kv || p.ctx_index) ? p.ctx_batch : (p.ctx_batch > 1 ? p.ctx_batch : 1);
+    if (crows > 0) {
+      e = hipLaunchKernel(f.dkv[2], dim3((unsigned)((crows + kBwdBK - 1) / kBwdBK), p.c_sh == 0 ? 1u : (unsigned)p.H, cbs),
+                          dim3(kBwdNW * 64), args, (size_t)f.dkv_lds, s);
+      if (e != hipSuccess) return (int)e;
+    }
+  }
+  return launch_status();
+}

@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libflash_mlm_hip.so"
 _LIB_PATH = Path(os.environ.get("FMLM_LIB_PATH", Path(__file__).resolve().parent / "_native" / LIB_NAME))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
@@ -114,6 +114,21 @@ class PackTensor(ctypes.Structure):
     ]
 
 
+class AttnGrads(ctypes.Structure):
+    """Mirror of fmlm_attn_grads (include/flash_mlm_hip.h)."""
+
+    _fields_ = [
+        (name if s == "" else f"{pre}{s}", _c_ptr if s == "" else _c_i64)
+        for name, pre in (("dout", "do"), ("dq", "dq"), ("dk", "dk"), ("dv", "dv"))
+        for s in ("", "_sb", "_sh", "_sn")
+    ] + [
+        ("dk_ctx", _c_ptr),
+        ("dv_ctx", _c_ptr),
+        ("workspace", _c_ptr),
+        ("workspace_bytes", _c_i64),
+    ]
+
+
 # (name, restype, argtypes) of every exported entry point
 SIGNATURES = {
     "fmlm_abi_version": (ctypes.c_int, []),
@@ -139,6 +154,9 @@ SIGNATURES = {
     "fmlm_attn_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(AttnParams)]),
     "fmlm_attn_schedule": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr, _c_i64, _c_ptr]),
     "fmlm_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr]),
+    "fmlm_attn_grads_size": (ctypes.c_int, []),
+    "fmlm_attn_bwd_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(AttnParams)]),
+    "fmlm_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), ctypes.POINTER(AttnGrads), _c_ptr]),
 }
 
 _lock = threading.Lock()
@@ -173,6 +191,8 @@ def load() -> ctypes.CDLL:
             raise RuntimeError("fmlm_attn_params layout mismatch between library and binding")
         if lib.fmlm_pack_tensor_size() != ctypes.sizeof(PackTensor):
             raise RuntimeError("fmlm_pack_tensor layout mismatch between library and binding")
+        if lib.fmlm_attn_grads_size() != ctypes.sizeof(AttnGrads):
+            raise RuntimeError("fmlm_attn_grads layout mismatch between library and binding")
         _lib = lib
         return lib
 

@@ -65,10 +65,13 @@ def _workspace(inference_cache: InferenceCache | None, nbytes: int, device: torc
 class AttnLaunch:
     """A prepared fmlm_attn_fwd call: the parameter block plus the tensors it points to."""
 
-    __slots__ = ("lib", "params", "stream", "device", "keep")
+    __slots__ = ("lib", "params", "stream", "device", "keep", "unpack_kv")
 
     def __init__(self, lib, params, stream, device, keep):
         self.lib, self.params, self.stream, self.device, self.keep = lib, params, stream, device, keep
+        # (B, N, H, kv_heads, rows, cu_q) when the kernel read packed copies of padded
+        # K/V (causal_query_seq_attn): the backward unpacks their gradient
+        self.unpack_kv = None
 
     def __call__(self) -> None:
         with _device_scope(self.device):
@@ -81,6 +84,134 @@ def _launch(*, run: bool = True, **kw) -> AttnLaunch:
     if run:
         plan()
     return plan
+
+
+# ---------------------------------------------------------------------------
+# Backward (an extension: the reference's roadmap lists backpropagation,
+# README.md:26-28).  Each entry point is differentiable in q, k, v and the cached
+# context tensors: the forward runs as before inside an autograd Function, and its
+# backward runs fmlm_attn_bwd on the forward's own parameter block.
+# ---------------------------------------------------------------------------
+_BWD_HEAD_DIMS = (32, 64, 128, 256)
+
+
+def _cache_tensors(inference_cache, layer_id, prefill: bool):
+    """The cached context tensors a call reads, (None, None) without a context."""
+    if prefill or inference_cache is None or layer_id is None:
+        return None, None, None
+    entry = inference_cache._layer_kv.get(inference_cache._layer_key(layer_id))
+    if entry is None:
+        return None, None, None
+    return entry.k_cache, entry.v_cache, entry
+
+
+def _wants_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
+def _check_backward_supported(q: torch.Tensor, d: int, entry) -> None:
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("the attention backward needs bf16 or fp16 inputs")
+    if d not in _BWD_HEAD_DIMS:
+        raise ValueError("the attention backward supports head_dim 32, 64, 128 or 256")
+    if entry is not None and entry.block_table is not None:
+        raise ValueError("paged KV contexts have no attention backward")
+
+
+class _Attention(torch.autograd.Function):
+    """One attention call made differentiable: ``impl()`` runs the forward and returns
+    (out, prepared launch); the backward hands that launch's parameter block to
+    fmlm_attn_bwd."""
+
+    @staticmethod
+    def forward(ctx, impl, q, k, v, k_cache, v_cache):
+        out, plan = impl()
+        ctx.plan = plan
+        ctx.save_for_backward(out, q, k, v)
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dout):
+        out = ctx.saved_tensors[0]
+        if ctx.plan is None:
+            return (None,) * 6
+        want_ctx = ctx.needs_input_grad[4] or ctx.needs_input_grad[5]
+        dq, dk, dv, dkc, dvc = _attention_backward(ctx.plan, out, dout, want_ctx)
+        return None, dq, dk, dv, dkc, dvc
+
+
+def _attention_backward(plan: AttnLaunch, out: torch.Tensor, dout: torch.Tensor, want_ctx: bool):
+    """Gradients (dq, dk, dv, dk_cache, dv_cache) of the prepared call ``plan`` whose
+    output is ``out``, shaped like the caller's tensors (dv None for MLA: V is K and both
+    gradients are in dk)."""
+    g, (dq, dk, dv, dkc, dvc, _ws, _dout) = _backward_args(plan, out, dout, want_ctx)
+    with _device_scope(out.device):
+        rc = plan.lib.fmlm_attn_bwd(plan.params, g, plan.stream)
+    _lib.check(rc, "fmlm_attn_bwd")
+    if plan.unpack_kv is not None:
+        mla = bool(plan.params.flags & _lib.FLAG_MLA)
+        dk = _unpack_kv_grad(plan.lib, dk, plan, mla)
+        dv = None if mla else _unpack_kv_grad(plan.lib, dv, plan, mla)
+    return dq, dk, dv, dkc, dvc
+
+
+def _backward_args(plan: AttnLaunch, out: torch.Tensor, dout: torch.Tensor, want_ctx: bool):
+    """The fmlm_attn_grads block of one backward call and the tensors it points to:
+    zeroed gradients shaped like the tensors the kernel read, the workspace and dout."""
+    p, lib = plan.params, plan.lib
+    q_, _, k_, v_, k_ctx, v_ctx = plan.keep[:6]
+    mla = bool(p.flags & _lib.FLAG_MLA)
+    prefill = bool(p.flags & _lib.FLAG_PREFILL)
+    dout = dout.contiguous()
+    if dout.shape != out.shape or not out.is_contiguous():
+        raise ValueError("gradient of the attention output has the wrong shape")
+
+    def grad_of(x: torch.Tensor, strides):
+        gx = torch.zeros(x.shape, dtype=x.dtype, device=x.device)
+        if x.ndim == 4:  # padded [B, H, N, D]; head stride 0 = rows shared by all heads
+            return gx, (gx.stride(0), 0 if strides[1] == 0 else gx.stride(1), gx.stride(2))
+        return gx, strides  # packed rows of a contiguous tensor
+
+    g = _lib.AttnGrads()
+    g.dout = dout.data_ptr()
+    g.do_sb, g.do_sh, g.do_sn = p.o_sb, p.o_sh, p.o_sn
+    dq, (g.dq_sb, g.dq_sh, g.dq_sn) = grad_of(q_, (p.q_sb, p.q_sh, p.q_sn))
+    dk, (g.dk_sb, g.dk_sh, g.dk_sn) = grad_of(k_, (p.k_sb, p.k_sh, p.k_sn))
+    g.dq, g.dk = dq.data_ptr(), dk.data_ptr()
+    dv = None
+    if not mla:
+        dv, (g.dv_sb, g.dv_sh, g.dv_sn) = grad_of(v_, (p.v_sb, p.v_sh, p.v_sn))
+        g.dv = dv.data_ptr()
+    dkc = dvc = None
+    if want_ctx and not prefill and k_ctx is not None and k_ctx.numel():
+        dkc = torch.zeros_like(k_ctx)
+        g.dk_ctx = dkc.data_ptr()
+        if not mla:
+            dvc = torch.zeros_like(v_ctx)
+            g.dv_ctx = dvc.data_ptr()
+    nbytes = int(lib.fmlm_attn_bwd_workspace_bytes(p))
+    _lib.check(nbytes if nbytes < 0 else 0, "fmlm_attn_bwd_workspace_bytes")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=out.device)
+    g.workspace, g.workspace_bytes = ws.data_ptr(), nbytes
+    return g, (dq, dk, dv, dkc, dvc, ws, dout)
+
+
+def _unpack_kv_grad(lib, packed: torch.Tensor, plan: AttnLaunch, mla: bool) -> torch.Tensor:
+    """Gradient rows of packed K/V [kv_heads * rows, D] -> padded [B, H, N, D] (MLA: head 0)."""
+    B, N, H, kv_heads, rows, cu_q = plan.unpack_kv
+    D = int(packed.shape[1])
+    dst = torch.empty((B, kv_heads, N, D), dtype=packed.dtype, device=packed.device)
+    if dst.numel():
+        with _device_scope(packed.device):
+            rc = lib.fmlm_unpack(packed.element_size(), packed.data_ptr(), rows * D, dst.data_ptr(), B, kv_heads,
+                                 N, D, cu_q.data_ptr(), plan.stream)
+        _lib.check(rc, "fmlm_unpack")
+    if mla and H > 1:
+        full = torch.zeros((B, H, N, D), dtype=packed.dtype, device=packed.device)
+        full[:, :1] = dst
+        return full
+    return dst
 
 
 def _prepare(
@@ -225,10 +356,17 @@ def flash_attn_mlm(
     layer's new context with context_batch_size = B.  ``context_index`` (int [B], an
     extension) maps sequence b to cached context batch ``context_index[b]``.
     """
-    return _dense_impl(
-        q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill,
-        context_index=context_index,
-    )[0]
+    def impl():
+        return _dense_impl(
+            q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill,
+            context_index=context_index,
+        )
+
+    kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
+    if _wants_grad(q, k, v, kc, vc):
+        _check_backward_supported(q, int(q.shape[-1]), entry)
+        return _Attention.apply(impl, q, k, v, kc, vc)
+    return impl()[0]
 
 
 def _dense_impl(
@@ -393,10 +531,17 @@ def flash_attn_mlm_compressed(
     context_batch_size = B) before the attention runs.  ``context_index`` (int [B], an
     extension) maps sequence b to cached context batch ``context_index[b]`` instead.
     """
-    return _compressed_impl(
-        q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
-        block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, context_index=context_index,
-    )[0]
+    def impl():
+        return _compressed_impl(
+            q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
+            block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, context_index=context_index,
+        )
+
+    kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
+    if _wants_grad(q, k, v, kc, vc):
+        _check_backward_supported(q, int(q.shape[-1]), entry)
+        return _Attention.apply(impl, q, k, v, kc, vc)
+    return impl()[0]
 
 
 def _compressed_impl(
@@ -503,6 +648,7 @@ def _compressed_impl(
     cu_q = cu_seqlens_q.to(torch.int32).contiguous()
     cu_kv = ctx.cu_seqlens_kv.to(torch.int32).contiguous()
     kv_layout = _lib.LAYOUT_PADDED
+    unpack_kv = None
     if causal_query_seq_attn:
         # the causal key range [0, cu[b+1]) spans sequences: pack K/V once (or reuse the
         # prefill entry) so the kernel streams it linearly
@@ -523,6 +669,7 @@ def _compressed_impl(
         k_, v_, rows = packed_kv
         k_strides = v_strides = (0, 0 if is_mla else rows * d, d)
         kv_layout = _lib.LAYOUT_PACKED
+        unpack_kv = (b, n, num_heads, 1 if is_mla else num_heads, rows, cu_q)
     elif is_mla:
         k_strides = (k_.stride(0), 0, k_.stride(2))  # every head reads head 0
         v_strides = k_strides
@@ -568,6 +715,7 @@ def _compressed_impl(
         block_table=ctx.block_table,
         page_stride=_page_stride(ctx, num_heads, d, is_mla),
     )
+    plan.unpack_kv = unpack_kv
     return out, plan
 
 
@@ -601,6 +749,25 @@ def flash_attn_mlm_precompressed(
     validated as in the reference.  ``prefill=True`` stores k / v (views) as the
     layer's context after the launch.
     """
+
+    def impl():
+        return _precompressed_impl(
+            q, k, v, num_heads, total_q_len, cu_seqlens_q, batch_ids_q, q_tile_starts_q, scale, inference_cache,
+            layer_id, is_mla, context_batch_size, prefill, causal_query_seq_attn, context_index,
+        )
+
+    kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
+    if _wants_grad(q, k, v, kc, vc):
+        _check_backward_supported(q, int(q.shape[-1]), entry)
+        return _Attention.apply(impl, q, k, v, kc, vc)
+    return impl()[0]
+
+
+def _precompressed_impl(
+    q, k, v, num_heads, total_q_len, cu_seqlens_q, batch_ids_q, q_tile_starts_q, scale, inference_cache, layer_id,
+    is_mla, context_batch_size, prefill, causal_query_seq_attn, context_index,
+):
+    """Body of :func:`flash_attn_mlm_precompressed`; returns (out, prepared launch or None)."""
     validate_cache_request(prefill=prefill, inference_cache=inference_cache, layer_id=layer_id)
     if q.ndim != 2 or k.ndim != 2 or v.ndim != 2:
         raise ValueError("q/k/v must be pre-packed rank-2 tensors")
@@ -653,9 +820,10 @@ def flash_attn_mlm_precompressed(
     q_, k_, v_ = make_contiguous(q, k, v)
     k_cache, v_cache = make_contiguous(ctx.k_cache, ctx.v_cache)
     out = torch.empty_like(q_)
+    plan = None
     if num_heads > 0 and total_q_len > 0 and b > 0:
         kv_sh = 0 if is_mla else total_q_len * d
-        _launch(
+        plan = _launch(
             q=q_,
             out=out,
             k=k_,
@@ -702,4 +870,4 @@ def flash_attn_mlm_precompressed(
             num_heads=num_heads,
             head_dim=d,
         )
-    return out
+    return out, plan

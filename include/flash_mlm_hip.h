@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FMLM_ABI_VERSION 3
+#define FMLM_ABI_VERSION 4
 
 /* element types */
 enum {
@@ -226,6 +226,37 @@ FMLM_API int fmlm_attn_schedule(const fmlm_attn_params* p, void* schedule, int64
                                 void* stream);
 
 FMLM_API int fmlm_attn_fwd(const fmlm_attn_params* p, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Attention backward.  No counterpart in the reference, whose roadmap lists
+ * backpropagation (README.md:26-28); it differentiates fmlm_attn_fwd for the same
+ * parameter block p (p->o holding that call's output):
+ *   dq      rows laid out like q (q_layout) with the dq strides: every real row
+ *   dk, dv  main-key rows laid out like k / v (kv_layout) with the dk / dv strides: every
+ *           key row some query attends to.  With FMLM_FLAG_MLA dk receives the gradient
+ *           of K and of V (V is K) and dv is unused.  Keys with head stride 0 (the MLA
+ *           latent) are shared by all heads, and so is their gradient row (dk_sh = 0).
+ *   dk_ctx, dv_ctx  the context's gradient, laid out like k_ctx / v_ctx (c_sb, c_sh,
+ *           c_sn), or NULL to skip it: rows [c0, c1) of every context batch.
+ * Rows not listed are not written.  dout is laid out like o (o_layout).
+ * bf16 / f16, D in {32, 64, 128, 256}; contiguous (non-paged) contexts; with
+ * FMLM_FLAG_CAUSAL_SEQ the main keys must be packed (kv_layout PACKED).
+ * workspace: fmlm_attn_bwd_workspace_bytes(p) bytes (per-row softmax statistics).
+ * ------------------------------------------------------------------------- */
+typedef struct fmlm_attn_grads {
+  const void* dout; int64_t do_sb, do_sh, do_sn;
+  void* dq;  int64_t dq_sb, dq_sh, dq_sn;
+  void* dk;  int64_t dk_sb, dk_sh, dk_sn;
+  void* dv;  int64_t dv_sb, dv_sh, dv_sn;
+  void* dk_ctx;
+  void* dv_ctx;
+  void* workspace;
+  int64_t workspace_bytes;
+} fmlm_attn_grads;
+
+FMLM_API int fmlm_attn_grads_size(void);  /* sizeof(fmlm_attn_grads), for bindings */
+FMLM_API int64_t fmlm_attn_bwd_workspace_bytes(const fmlm_attn_params* p);
+FMLM_API int fmlm_attn_bwd(const fmlm_attn_params* p, const fmlm_attn_grads* g, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,6 +27,27 @@ def attend(q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float) -> np.ndar
     return p @ V
 
 
+def attend_backward(q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float, dO: np.ndarray):
+    """Gradients of ``attend`` for an upstream gradient dO [L, D]: returns (dq, dK, dV) in
+    float64.  With P = softmax(scale q K^T) and O = P V:
+    dV = P^T dO, dP = dO V^T, dS = P * (dP - rowsum(dO * O)), dq = scale dS K,
+    dK = scale dS^T q (the softmax Jacobian diag(P) - P P^T applied row by row)."""
+    q = q.astype(np.float64)
+    K = K.astype(np.float64)
+    V = V.astype(np.float64)
+    dO = dO.astype(np.float64)
+    s = (q @ K.T) * float(scale)
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=1, keepdims=True)
+    o = p @ V
+    dV = p.T @ dO
+    dP = dO @ V.T
+    delta = (dO * o).sum(axis=1, keepdims=True)
+    dS = p * (dP - delta) * float(scale)
+    return dS @ K, dS.T @ q, dV
+
+
 def packed_key_rows(b: int, lengths, causal_query_seq_attn: bool) -> list[tuple[int, int]]:
     """(sequence, position) of the main keys of sequence b in packed order:
     sequence b's own tokens, or with causal_query_seq_attn all tokens of sequences
@@ -90,6 +111,128 @@ def mlm_attention_packed(
                 K_all, V_all = K_main, V_main
             out[b, h, :Lq] = attend(q[b, h, :Lq], K_all, V_all, scale)
     return out
+
+
+def mlm_attention_packed_backward(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    dout: np.ndarray,
+    lengths,
+    scale: float,
+    *,
+    is_mla: bool = False,
+    causal_query_seq_attn: bool = False,
+    prefill: bool = False,
+    k_cache: np.ndarray | None = None,
+    v_cache: np.ndarray | None = None,
+    cu_seqlens_kv=None,
+    total_context_len: int = 0,
+    context_batch_size: int = 1,
+    context_index=None,
+):
+    """Gradients of :func:`mlm_attention_packed` (same arguments, plus the upstream
+    gradient ``dout`` [B, H, N, D]; its padding rows are ignored).  Returns float64
+    (dq, dk, dv, dk_cache, dv_cache) shaped like q, k, v, k_cache, v_cache; dv is None for
+    MLA (V is K: both gradients land in dk, head 0) and the cache gradients are None
+    without a cache.  The reference has no backward (its roadmap lists one,
+    README.md:26-28): this differentiates the forward restated above, key set by key set.
+    """
+    B, H, N, D = q.shape
+    dq = np.zeros(q.shape, dtype=np.float64)
+    dk = np.zeros(k.shape, dtype=np.float64)
+    dv = None if is_mla else np.zeros(v.shape, dtype=np.float64)
+    dkc = None if k_cache is None else np.zeros(k_cache.shape, dtype=np.float64)
+    dvc = None if (v_cache is None or is_mla) else np.zeros(v_cache.shape, dtype=np.float64)
+    cu_kv = None if cu_seqlens_kv is None else np.asarray(cu_seqlens_kv, dtype=np.int64)
+    for b in range(B):
+        Lq = int(lengths[b])
+        if Lq == 0:
+            continue
+        rows = packed_key_rows(b, lengths, causal_query_seq_attn)
+        sb = np.array([r[0] for r in rows], dtype=np.int64)
+        pb = np.array([r[1] for r in rows], dtype=np.int64)
+        c0 = c1 = 0
+        if not prefill and cu_kv is not None:
+            cb = int(context_index[b]) if context_index is not None else (b if context_batch_size > 1 else 0)
+            c0, c1 = int(cu_kv[cb]), int(cu_kv[cb + 1])
+        nc = c1 - c0
+        for h in range(H):
+            kh = 0 if is_mla else h
+            K_main = k[sb, kh, pb]
+            V_main = K_main if is_mla else v[sb, h, pb]
+            off = 0 if is_mla else h * total_context_len
+            if nc > 0:
+                K_ctx = k_cache[off + c0 : off + c1]
+                V_ctx = K_ctx if is_mla else v_cache[off + c0 : off + c1]
+                K_all = np.concatenate([K_ctx, K_main])
+                V_all = np.concatenate([V_ctx, V_main])
+            else:
+                K_all, V_all = K_main, V_main
+            g_q, g_K, g_V = attend_backward(q[b, h, :Lq], K_all, V_all, scale, dout[b, h, :Lq])
+            dq[b, h, :Lq] += g_q
+            if is_mla:  # V is K
+                g_K = g_K + g_V
+            if nc > 0:
+                dkc[off + c0 : off + c1] += g_K[:nc]
+                if not is_mla:
+                    dvc[off + c0 : off + c1] += g_V[:nc]
+            np.add.at(dk, (sb, kh, pb), g_K[nc:])
+            if not is_mla:
+                np.add.at(dv, (sb, h, pb), g_V[nc:])
+    return dq, dk, dv, dkc, dvc
+
+
+def mlm_attention_dense_backward(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    dout: np.ndarray,
+    scale: float,
+    *,
+    is_mla: bool = False,
+    prefill: bool = False,
+    k_cache: np.ndarray | None = None,
+    v_cache: np.ndarray | None = None,
+    context_len: int = 0,
+    context_batch_size: int = 1,
+    context_index=None,
+):
+    """Gradients of :func:`mlm_attention_dense`: (dq, dk, dv, dk_cache, dv_cache) in
+    float64, dv None for MLA (V = K per head: both land in dk), cache gradients None
+    without a cache.  No reference counterpart (roadmap, README.md:26-28)."""
+    B, H, N, D = q.shape
+    dq = np.zeros(q.shape, dtype=np.float64)
+    dk = np.zeros(k.shape, dtype=np.float64)
+    dv = None if is_mla else np.zeros(v.shape, dtype=np.float64)
+    dkc = None if k_cache is None else np.zeros(k_cache.shape, dtype=np.float64)
+    dvc = None if (v_cache is None or is_mla) else np.zeros(v_cache.shape, dtype=np.float64)
+    for b in range(B):
+        cb = int(context_index[b]) if context_index is not None else (b if context_batch_size > 1 else 0)
+        for h in range(H):
+            K_main = k[b, h]
+            V_main = K_main if is_mla else v[b, h]
+            nc = context_len if (not prefill and context_len > 0) else 0
+            if nc:
+                start = cb * context_len if is_mla else (cb * H + h) * context_len
+                K_ctx = k_cache[start : start + nc]
+                V_ctx = K_ctx if is_mla else v_cache[start : start + nc]
+                K_all = np.concatenate([K_ctx, K_main])
+                V_all = np.concatenate([V_ctx, V_main])
+            else:
+                K_all, V_all = K_main, V_main
+            g_q, g_K, g_V = attend_backward(q[b, h], K_all, V_all, scale, dout[b, h])
+            dq[b, h] += g_q
+            if is_mla:
+                g_K = g_K + g_V
+            if nc:
+                dkc[start : start + nc] += g_K[:nc]
+                if not is_mla:
+                    dvc[start : start + nc] += g_V[:nc]
+            dk[b, h] += g_K[nc:]
+            if not is_mla:
+                dv[b, h] += g_V[nc:]
+    return dq, dk, dv, dkc, dvc
 
 
 def mlm_attention_dense(

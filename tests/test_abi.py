@@ -39,6 +39,7 @@ def test_struct_layouts_match():
     assert lib.fmlm_abi_version() == _lib.ABI_VERSION
     assert lib.fmlm_attn_params_size() == ctypes.sizeof(_lib.AttnParams)
     assert lib.fmlm_pack_tensor_size() == ctypes.sizeof(_lib.PackTensor)
+    assert lib.fmlm_attn_grads_size() == ctypes.sizeof(_lib.AttnGrads)
 
 
 def test_argument_rejection_without_launch():
@@ -60,5 +61,20 @@ def test_argument_rejection_without_launch():
     assert lib.fmlm_attn_workspace_bytes(p) == 0  # dense: no schedule workspace
     p.dtype = 7
     assert lib.fmlm_attn_workspace_bytes(p) == -2
+    # backward: argument checks return before any HIP call
+    assert lib.fmlm_attn_bwd(None, None, None) == -1
+    g = _lib.AttnGrads()
+    p.dtype, p.D, p.total_q = _lib.DTYPE_BF16, 48, 4
+    p.q = p.o = p.k = p.v = 256
+    g.dout = g.dq = g.dk = g.dv = 256
+    assert lib.fmlm_attn_bwd(p, g, None) == -3  # head dim without a backward kernel
+    p.D = 64
+    p.dtype = _lib.DTYPE_F32
+    assert lib.fmlm_attn_bwd(p, g, None) == -2
+    p.dtype = _lib.DTYPE_BF16
+    assert lib.fmlm_attn_bwd(p, g, None) == -5  # no workspace
+    assert lib.fmlm_attn_bwd_workspace_bytes(p) == 256  # 2 floats per (head, row), rounded up
+    p.q = 264  # not 16-byte aligned
+    assert lib.fmlm_attn_bwd(p, g, None) == -4
     with pytest.raises(RuntimeError, match="invalid argument"):
         _lib.check(-1, "x")

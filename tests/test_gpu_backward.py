@@ -1,0 +1,264 @@
+"""GPU tests of the attention backward (fmlm_attn_bwd through torch.autograd on the three
+entry points; an extension: the reference's roadmap lists backpropagation,
+README.md:26-28).  Gradients of q, k, v and of the cached context are compared with the
+float64 oracle (oracle/attention_ref.py *_backward, itself pinned by finite differences
+in test_oracle_backward.py), and at a larger size with torch autograd of a float32
+per-sequence softmax attention.
+
+Tolerance: bf16/fp16 inputs with fp32 accumulation, and P and dS rounded to the input
+type before their products (as the forward rounds P), so each gradient is held to
+|gpu - ref| <= TOL * max|ref| + TOL * |ref| with TOL = 2e-2 per element (max|ref| over
+the whole gradient tensor, which must be nonzero).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flash_mlm import InferenceCache, build_pack_metadata, flash_attn_mlm, flash_attn_mlm_compressed, \
+    flash_attn_mlm_precompressed
+from oracle import attention_ref as ar
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _close(got, ref, what):
+    got = _np(got)
+    scale = float(np.abs(ref).max()) if ref.size else 0.0
+    assert scale > 0, f"{what}: reference gradient is zero"
+    err = np.abs(got - ref)
+    bound = TOL * scale + TOL * np.abs(ref)
+    worst = float((err - bound).max())
+    print(f"{what}: max err / max |ref| = {float(err.max()) / scale:.2e}")
+    assert worst <= 0, f"{what}: max err {float(err.max()):.3e} (ref max {scale:.3e})"
+
+
+def _leaf(shape, dtype, device, gen, mult=0.5):
+    return (torch.randn(shape, generator=gen) * mult).to(dtype).to(device).requires_grad_()
+
+
+def _packed_cache(ctx_lens, *, H, D, mla, dtype, device, gen):
+    cu = np.concatenate([[0], np.cumsum(ctx_lens)]).astype(np.int32)
+    total = int(cu[-1]) + 3  # spare rows per head
+    heads = 1 if mla else H
+    kc = _leaf((heads * total, D), dtype, device, gen)
+    vc = None if mla else _leaf((heads * total, D), dtype, device, gen)
+    cache = InferenceCache()
+    cache.prefill_kv_cache(0, k_cache=kc, v_cache=vc, total_context_len=total,
+                           cu_seqlens_kv=torch.from_numpy(cu).to(device), context_batch_size=len(ctx_lens),
+                           is_mla=mla, num_heads=H, head_dim=D)
+    return cache, kc, vc, cu, total
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("mla", [False, True])
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_compressed_with_context(dtype, D, mla, causal, device):
+    gen = torch.Generator().manual_seed(7000 + D + 2 * mla + causal)
+    lengths = [70, 1, 0, 133, 40]
+    B, H, N = len(lengths), 3, 140
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    cache, kc, vc, cu_kv, total = _packed_cache([129, 0, 64, 7, 90], H=H, D=D, mla=mla, dtype=dtype,
+                                                device=device, gen=gen)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, is_mla=mla, block_n=64,
+                                    causal_query_seq_attn=causal)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    # dout in padded form for the oracle
+    from flash_mlm import unpack_from_kernel
+    dout_pad = _np(unpack_from_kernel(dout, meta, H))
+    g = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(v), dout_pad, lengths, scale, is_mla=mla, causal_query_seq_attn=causal,
+        k_cache=_np(kc), v_cache=None if mla else _np(vc), cu_seqlens_kv=cu_kv, total_context_len=total,
+        context_batch_size=B)
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk")
+    if mla:
+        assert v.grad is None
+    else:
+        _close(v.grad, g[2], "dv")
+    _close(kc.grad, g[3], "dk_cache")
+    if not mla:
+        _close(vc.grad, g[4], "dv_cache")
+
+
+@pytest.mark.parametrize("D", [32, 256])
+def test_backward_compressed_head_dims(D, device):
+    gen = torch.Generator().manual_seed(7100 + D)
+    lengths = [33, 64, 5]
+    B, H, N, dtype = len(lengths), 2, 64, torch.bfloat16
+    scale = 0.3
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    cache, kc, vc, cu_kv, total = _packed_cache([20, 65, 1], H=H, D=D, mla=False, dtype=dtype, device=device, gen=gen)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    from flash_mlm import unpack_from_kernel
+    g = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)), lengths, scale, k_cache=_np(kc),
+        v_cache=_np(vc), cu_seqlens_kv=cu_kv, total_context_len=total, context_batch_size=B)
+    for got, ref, name in ((q.grad, g[0], "dq"), (k.grad, g[1], "dk"), (v.grad, g[2], "dv"),
+                           (kc.grad, g[3], "dkc"), (vc.grad, g[4], "dvc")):
+        _close(got, ref, name)
+
+
+def test_backward_context_index_and_frozen_cache(device):
+    """Two context batches shared by three sequences through context_index; the cache
+    does not require grad, so only q, k, v get gradients."""
+    gen = torch.Generator().manual_seed(7200)
+    lengths = [50, 17, 80]
+    B, H, N, D, dtype = len(lengths), 2, 80, 64, torch.float16
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    cache, kc, vc, cu_kv, total = _packed_cache([100, 33], H=H, D=D, mla=False, dtype=dtype, device=device, gen=gen)
+    kc.requires_grad_(False)
+    vc.requires_grad_(False)
+    idx = torch.tensor([1, 0, 1], dtype=torch.int32)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, 0.125, cache, 0, block_n=64, context_index=idx)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    from flash_mlm import unpack_from_kernel
+    g = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)), lengths, 0.125, k_cache=_np(kc),
+        v_cache=_np(vc), cu_seqlens_kv=cu_kv, total_context_len=total, context_batch_size=2,
+        context_index=idx.tolist())
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk")
+    _close(v.grad, g[2], "dv")
+    assert kc.grad is None and vc.grad is None
+
+
+@pytest.mark.parametrize("mla", [False, True])
+@pytest.mark.parametrize("cbs", [1, 3])
+def test_backward_dense_with_context(mla, cbs, device):
+    gen = torch.Generator().manual_seed(7300 + 2 * mla + cbs)
+    B, H, N, D, C, dtype = 3, 2, 96, 64, 70, torch.bfloat16
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    kc = _leaf((cbs * (1 if mla else H) * C, D), dtype, device, gen)
+    vc = None if mla else _leaf(kc.shape, dtype, device, gen)
+    cache = InferenceCache()
+    cache.prefill_kv_cache(0, k_cache=kc, v_cache=vc, context_batch_size=cbs, is_mla=mla, num_heads=H, head_dim=D)
+    out = flash_attn_mlm(q, k, v, scale, cache, 0, is_mla=mla)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    g = ar.mlm_attention_dense_backward(_np(q), _np(k), _np(v), _np(dout), scale, is_mla=mla, k_cache=_np(kc),
+                                        v_cache=None if mla else _np(vc), context_len=C, context_batch_size=cbs)
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk")
+    _close(kc.grad, g[3], "dk_cache")
+    if not mla:
+        _close(v.grad, g[2], "dv")
+        _close(vc.grad, g[4], "dv_cache")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_precompressed_matches_compressed(causal, device):
+    gen = torch.Generator().manual_seed(7400 + causal)
+    lengths = [40, 3, 77]
+    B, H, N, D, dtype = len(lengths), 2, 80, 128, torch.bfloat16
+    q0, k0, v0 = ((torch.randn((B, H, N, D), generator=gen) * 0.5).to(dtype).to(device) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    T = sum(lengths)
+    # packed copies as leaves
+    qp = torch.cat([q0[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D).contiguous().requires_grad_()
+    kp = torch.cat([k0[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D).contiguous().requires_grad_()
+    vp = torch.cat([v0[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D).contiguous().requires_grad_()
+    out = flash_attn_mlm_precompressed(qp, kp, vp, H, T, meta.cu_seqlens, meta.batch_ids_q, meta.q_tile_starts_q,
+                                       0.2, block_n=64, causal_query_seq_attn=causal)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    qd, kd, vd = (t.clone().requires_grad_() for t in (q0, k0, v0))
+    out2 = flash_attn_mlm_compressed(qd, kd, vd, H, meta, 0.2, block_n=64, causal_query_seq_attn=causal)
+    out2.backward(dout)
+
+    def packed(x):
+        return torch.cat([x[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D)
+
+    torch.testing.assert_close(qp.grad, packed(qd.grad), atol=1e-5, rtol=0)
+    torch.testing.assert_close(kp.grad, packed(kd.grad), atol=1e-5, rtol=0)
+    torch.testing.assert_close(vp.grad, packed(vd.grad), atol=1e-5, rtol=0)
+
+
+def test_backward_prefill_and_no_context(device):
+    gen = torch.Generator().manual_seed(7500)
+    lengths = [64, 9]
+    B, H, N, D, dtype = 2, 2, 64, 64, torch.bfloat16
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    cache = InferenceCache()
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, 0.25, cache, 0, block_n=64, prefill=True)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    from flash_mlm import unpack_from_kernel
+    g = ar.mlm_attention_packed_backward(_np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)), lengths,
+                                         0.25)
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk")
+    _close(v.grad, g[2], "dv")
+
+
+def test_backward_against_torch_fp32_autograd(device):
+    """Larger case (contexts and sequences of hundreds of keys) against torch autograd of a
+    float32 per-sequence softmax attention on the GPU."""
+    gen = torch.Generator().manual_seed(7600)
+    lengths = [256, 100, 193, 7]
+    ctx = [512, 300, 0, 64]
+    B, H, N, D, dtype = len(lengths), 4, 256, 128, torch.bfloat16
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    cache, kc, vc, cu_kv, total = _packed_cache(ctx, H=H, D=D, mla=False, dtype=dtype, device=device, gen=gen)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+
+    qf, kf, vf = (x.detach().float().requires_grad_() for x in (q, k, v))
+    kcf, vcf = (x.detach().float().requires_grad_() for x in (kc, vc))
+    T = sum(lengths)
+    cu_q = np.concatenate([[0], np.cumsum(lengths)])
+    loss = 0.0
+    doutf = dout.float()
+    for b in range(B):
+        L = lengths[b]
+        if L == 0:
+            continue
+        for h in range(H):
+            Kc = kcf[h * total + cu_kv[b]: h * total + cu_kv[b + 1]]
+            Vc = vcf[h * total + cu_kv[b]: h * total + cu_kv[b + 1]]
+            K = torch.cat([Kc, kf[b, h, :L]])
+            V = torch.cat([Vc, vf[b, h, :L]])
+            p = torch.softmax((qf[b, h, :L] @ K.t()) * scale, dim=-1)
+            o = p @ V
+            loss = loss + (o * doutf[h * T + cu_q[b]: h * T + cu_q[b] + L]).sum()
+    loss.backward()
+    for got, ref, name in ((q.grad, qf.grad, "dq"), (k.grad, kf.grad, "dk"), (v.grad, vf.grad, "dv"),
+                           (kc.grad, kcf.grad, "dkc"), (vc.grad, vcf.grad, "dvc")):
+        _close(got, ref.detach().cpu().numpy().astype(np.float64), name)
+
+
+def test_backward_unsupported_raise(device):
+    B, H, N, D = 1, 1, 8, 64
+    meta = build_pack_metadata(torch.tensor([8], device=device, dtype=torch.int32), N, block_n=64)
+    q = torch.randn((B, H, N, D), device=device, requires_grad=True)  # fp32
+    with pytest.raises(ValueError, match="bf16 or fp16"):
+        flash_attn_mlm_compressed(q, q.detach(), q.detach(), H, meta, 0.1, block_n=64)
+    q16 = torch.randn((B, H, N, 16), device=device).to(torch.bfloat16).requires_grad_()
+    with pytest.raises(ValueError, match="head_dim"):
+        flash_attn_mlm_compressed(q16, q16.detach(), q16.detach(), H, meta, 0.1, block_n=64)
+    # no grad wanted: the forward still runs for those shapes
+    with torch.no_grad():
+        flash_attn_mlm_compressed(q16, q16, q16, H, meta, 0.1, block_n=64)
