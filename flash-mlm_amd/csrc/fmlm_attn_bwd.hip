@@ -9,8 +9,9 @@
 //   dq = dS K,  dK = dS^T q,  dV = P^T dO.
 // Two kernels, no atomics, so every gradient row has exactly one writer:
 //   attn_bwd_dq_kernel   one workgroup per (query tile, head, sequence), as in the
-//     forward.  Pass 1 recomputes each row's log2-sum-exp over the key set, pass 2
-//     accumulates dq^T = K^T dS^T.  It stores lse and delta per row for the next kernel.
+//     forward.  One pass over the key set accumulates dq^T = K^T dS^T with an online
+//     softmax (running max, lazy rescale) and yields each row's log2-sum-exp, which it
+//     stores with delta for the next kernel.
 //   attn_bwd_dkv_kernel  one workgroup per 64-key tile of a key segment (the main keys of
 //     a sequence, the causal token range of a head, or a context batch), 16 keys per
 //     wave.  It walks every query row that attends to those keys in steps of 32 rows
@@ -28,8 +29,11 @@ namespace fmlm {
 namespace {
 
 constexpr int kBwdNW = 4;   // waves per workgroup
-constexpr int kBwdBK = 64;  // keys per dq-kernel tile and per dkv workgroup (16 per wave)
+constexpr int kBwdBK = 64;  // keys per dq-kernel tile
 constexpr int kBwdQS = 32;  // query rows per dkv step
+// lazy rescale of the dq kernel's online softmax: the running max moves only when a tile's
+// max exceeds it by more than this (log2 units), so 2^(z - m) <= 2^8 before rounding
+constexpr float kRescaleSlack = 8.0f;
 
 template <int D>
 struct BwdCfg {
@@ -42,6 +46,8 @@ struct BwdCfg {
   static constexpr int BQ = kBwdNW * QB * 16;     // query rows per dq workgroup
   static constexpr int NKB = kBwdBK / 16;
   static constexpr int NKS = kBwdBK / 32;
+  static constexpr int KB = D <= 64 ? 2 : 1;      // 16-key blocks per wave (dkv kernel)
+  static constexpr int DKV_KEYS = kBwdNW * 16 * KB;  // keys per dkv workgroup
   static constexpr int DQ_LDS = 2 * kBwdBK * RS * 2;                  // K and V tiles
   static constexpr int DKV_LDS = 2 * kBwdQS * RS * 2 + 2 * kBwdQS * 4;  // Q, dO, lse, delta
   static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
@@ -150,9 +156,10 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
   const int l16 = lane & 15, gq = lane >> 4;
   const float c = p.scale * kLog2e;  // scores in log2 units
 
-  BSeg seg[2];
-  seg[0] = ctx_seg(p, g, ctx_batch_of(p, b), h);
-  seg[1] = main_seg(p, g, b, h);
+  const BSeg sc = ctx_seg(p, g, ctx_batch_of(p, b), h);  // context, then main keys
+  const BSeg sm = main_seg(p, g, b, h);
+  const int nt0 = (sc.n + kBwdBK - 1) / kBwdBK;
+  const int nt = nt0 + (sm.n + kBwdBK - 1) / kBwdBK;
 
   // Q and dO fragments (B operands): lane (q + 16g), block qb, step kc holds row q's
   // columns kc*32 + 8g .. +8; delta = rowsum(dO * O) of the lane's row
@@ -186,19 +193,41 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
     delta[qb] = dsum;
   }
 
-  // stage keys [j0, j0 + 64) of a segment (and their values) in LDS; rows past the end are 0
-  auto load_tile = [&](const BSeg& s, int j0, bool with_v) {
+  // key tile t of [context || main] (64 keys; rows past a segment end are 0): fetch()
+  // loads it into registers, stage() writes the registers to LDS.  The next tile's loads
+  // are issued before the current tile's math.
+  constexpr int LPT = kBwdBK * C::C8 / C::NT;  // 16-byte chunks per thread per tensor
+  u32x4 kreg[LPT], vreg[LPT];
+  auto keys_in = [&](int t) {
+    return t < nt0 ? min(kBwdBK, sc.n - t * kBwdBK) : min(kBwdBK, sm.n - (t - nt0) * kBwdBK);
+  };
+  auto fetch = [&](int t, bool with_v) {
+    const bool m = t >= nt0;
+    const int j0 = (m ? t - nt0 : t) * kBwdBK, n = m ? sm.n : sc.n;
+    const char* kp = m ? sm.k : sc.k;
+    const char* vp = m ? sm.v : sc.v;
+    const int64_t kb = m ? sm.kbase : sc.kbase, vb = m ? sm.vbase : sc.vbase;
+    const int64_t ksn = m ? sm.ksn : sc.ksn, vsn = m ? sm.vsn : sc.vsn;
 #pragma unroll
-    for (int it = tid; it < kBwdBK * C::C8; it += C::NT) {
+    for (int li = 0; li < LPT; ++li) {
+      const int it = tid + li * C::NT;
       const int row = it / C::C8, c8 = it % C::C8;
       const int key = j0 + row;
-      u32x4 kv = u32x4{0u, 0u, 0u, 0u}, vv = kv;
-      if (key < s.n) {
-        kv = ld16(s.k, s.kbase + (int64_t)key * s.ksn + c8 * 8);
-        if (with_v) vv = ld16(s.v, s.vbase + (int64_t)key * s.vsn + c8 * 8);
+      kreg[li] = u32x4{0u, 0u, 0u, 0u};
+      vreg[li] = kreg[li];
+      if (key < n) {
+        kreg[li] = ld16(kp, kb + (int64_t)key * ksn + c8 * 8);
+        if (with_v) vreg[li] = ld16(vp, vb + (int64_t)key * vsn + c8 * 8);
       }
-      *(u32x4*)(Ks + row * C::RS + c8 * 8) = kv;
-      if (with_v) *(u32x4*)(Vs + row * C::RS + c8 * 8) = vv;
+    }
+  };
+  auto stage = [&](bool with_v) {
+#pragma unroll
+    for (int li = 0; li < LPT; ++li) {
+      const int it = tid + li * C::NT;
+      const int row = it / C::C8, c8 = it % C::C8;
+      *(u32x4*)(Ks + row * C::RS + c8 * 8) = kreg[li];
+      if (with_v) *(u32x4*)(Vs + row * C::RS + c8 * 8) = vreg[li];
     }
   };
   // S^T = K Q^T of the staged tile: lane (q + 16g) reg r = S[query q][key 16kb + 4g + r]
@@ -217,111 +246,116 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
       }
   };
 
-  // ---- pass 1: log2-sum-exp of each row over the whole key set
+  // ---- one pass over the key set.  With P_j = 2^(z_j - m) / l (z = scores in log2
+  // units, m a running max, l = sum_j 2^(z_j - m)):
+  //   dq = scale / l * sum_j 2^(z_j - m) (dP_j - delta) k_j,
+  // so dq^T accumulates K^T (2^(z - m) (dP - delta))^T like the forward's O^T and is
+  // rescaled with l whenever m moves (lazily: by more than kRescaleSlack).
+  f32x4 dq[C::NDB][QB];
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) dq[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_i[QB], l_i[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     m_i[qb] = -INFINITY;
     l_i[qb] = 0.f;
   }
-  for (int sg = 0; sg < 2; ++sg) {
-    for (int j0 = 0; j0 < seg[sg].n; j0 += kBwdBK) {
-      const int nk = min(kBwdBK, seg[sg].n - j0);
-      __syncthreads();
-      load_tile(seg[sg], j0, false);
-      __syncthreads();
-      f32x4 s[C::NKB][QB];
-      scores(s);
+  if (nt > 0) fetch(0, true);
+  for (int t = 0; t < nt; ++t) {
+    const int nk = keys_in(t);
+    __syncthreads();  // the previous tile's LDS reads are done
+    stage(true);
+    __syncthreads();
+    if (t + 1 < nt) fetch(t + 1, true);
+    f32x4 s[C::NKB][QB], dp[C::NKB][QB];
+    scores(s);
+    // dP^T = V dO^T, same layout as S^T
+#pragma unroll
+    for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc)
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb) {
+        const v8 a = *(const v8*)(Vs + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = Mfma<T>::run(a, df[qb][kc], dp[kb][qb]);
+      }
+    // running max (row-uniform after the xor steps) and lazy rescale
+    bool grow_any = false;
+    float m_new[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float z = kb * 16 + gq * 4 + r < nk ? s[kb][qb][r] * c : -INFINITY;
+          s[kb][qb][r] = z;
+          mx = fmaxf(mx, z);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const bool grow = mx > m_i[qb] + kRescaleSlack;
+      m_new[qb] = grow ? mx : m_i[qb];
+      grow_any = grow_any || grow;
+    }
+    if (__builtin_amdgcn_ballot_w64(grow_any)) {
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        float mx = -INFINITY;
+        const float alpha = m_i[qb] == -INFINITY ? 0.f : fast_exp2(m_i[qb] - m_new[qb]);
+        m_i[qb] = m_new[qb];
+        l_i[qb] *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float z = kb * 16 + gq * 4 + r < nk ? s[kb][qb][r] * c : -INFINITY;
-            s[kb][qb][r] = z;
-            mx = fmaxf(mx, z);
-          }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_i[qb], mx);
-        if (m_new == -INFINITY) continue;  // no key yet (row-uniform)
-        float rs = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) rs += fast_exp2(s[kb][qb][r] - m_new);
-        l_i[qb] = l_i[qb] * fast_exp2(m_i[qb] - m_new) + rs;
-        m_i[qb] = m_new;
+        for (int db = 0; db < C::NDB; ++db) dq[db][qb] *= alpha;
       }
     }
+    // 2^(z - m) (dP - delta), packed as B operands: element 4h + r of step ks is key
+    // 32ks + 16h + 4g + r
+    v8 dsf[C::NKS][QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float mref = m_i[qb] == -INFINITY ? 0.f : m_i[qb];  // no key yet: every z is -inf
+      float rs = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = fast_exp2(s[kb][qb][r] - mref);
+          rs += pv;
+          dsf[kb >> 1][qb][(kb & 1) * 4 + r] = (T)(pv * (dp[kb][qb][r] - delta[qb]));
+        }
+      l_i[qb] += rs;
+    }
+#pragma unroll
+    for (int ks = 0; ks < C::NKS; ++ks)
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db) {
+        const v8 a = tr_frag<T>(Ks, C::RS, ks * 32, db, l16, gq);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) dq[db][qb] = Mfma<T>::run(a, dsf[ks][qb], dq[db][qb]);
+      }
   }
-  float lse[QB];
+  // row statistics for the dK / dV kernel: lse = m + log2(l) (no keys: +inf, P = 0)
   float* const st_lse = (float*)g.workspace;
   float* const st_delta = st_lse + (int64_t)p.H * p.total_q;
+  float dq_mul[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     float l = l_i[qb];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    lse[qb] = l > 0.f ? m_i[qb] + __log2f(l) : INFINITY;  // no keys: P = 0
+    const bool any = l > 0.f;
+    dq_mul[qb] = any ? p.scale / l : 0.f;
     const int row = qpos0 + (wave * QB + qb) * 16 + l16;
     if (gq == 0 && row < si.len) {
       const int64_t at = (int64_t)h * p.total_q + si.q0 + row;
-      st_lse[at] = lse[qb];
+      st_lse[at] = any ? m_i[qb] + __log2f(l) : INFINITY;
       st_delta[at] = delta[qb];
-    }
-  }
-
-  // ---- pass 2: dq^T += K^T dS^T
-  f32x4 dq[C::NDB][QB];
-#pragma unroll
-  for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) dq[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int sg = 0; sg < 2; ++sg) {
-    for (int j0 = 0; j0 < seg[sg].n; j0 += kBwdBK) {
-      const int nk = min(kBwdBK, seg[sg].n - j0);
-      __syncthreads();
-      load_tile(seg[sg], j0, true);
-      __syncthreads();
-      f32x4 s[C::NKB][QB], dp[C::NKB][QB];
-      scores(s);
-      // dP^T = V dO^T, same layout as S^T
-#pragma unroll
-      for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < C::KC; ++kc)
-#pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb) {
-          const v8 a = *(const v8*)(Vs + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = Mfma<T>::run(a, df[qb][kc], dp[kb][qb]);
-        }
-      // dS = scale * P * (dP - delta), packed as B operands: element 4h + r of step ks is
-      // key 32ks + 16h + 4g + r
-      v8 dsf[C::NKS][QB];
-#pragma unroll
-      for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const bool ok = kb * 16 + gq * 4 + r < nk;
-            const float pv = ok ? fast_exp2(fmaf(s[kb][qb][r], c, -lse[qb])) : 0.f;
-            dsf[kb >> 1][qb][(kb & 1) * 4 + r] = (T)(pv * (dp[kb][qb][r] - delta[qb]) * p.scale);
-          }
-#pragma unroll
-      for (int ks = 0; ks < C::NKS; ++ks)
-#pragma unroll
-        for (int db = 0; db < C::NDB; ++db) {
-          const v8 a = tr_frag<T>(Ks, C::RS, ks * 32, db, l16, gq);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) dq[db][qb] = Mfma<T>::run(a, dsf[ks][qb], dq[db][qb]);
-        }
     }
   }
 
@@ -335,7 +369,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
     for (int db = 0; db < C::NDB; ++db) {
       T v4[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v4[r] = (T)dq[db][qb][r];
+      for (int r = 0; r < 4; ++r) v4[r] = (T)(dq[db][qb][r] * dq_mul[qb]);
       *(u32x2*)((char*)g.dq + (off + db * 16 + gq * 4) * 2) = *(const u32x2*)v4;
     }
   }
@@ -359,7 +393,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
   const bool mla = p.flags & FMLM_FLAG_MLA;
   const int32_t* cu = p.cu_seqlens_q;
   const int kh = blockIdx.y, slot = blockIdx.z;
-  const int j0 = blockIdx.x * kBwdBK;
+  const int j0 = blockIdx.x * C::DKV_KEYS;
   BSeg s;
   int b_lo, b_hi;  // sequences whose queries may attend to these keys
   bool shared;     // key rows shared by all heads (head stride 0)
@@ -386,109 +420,182 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
   const float* const st_lse = (const float*)g.workspace;
   const float* const st_delta = st_lse + (int64_t)p.H * p.total_q;
 
-  // this lane's key (B-operand column / accumulator column) and its K, V fragments:
-  // kf[kc] = K[key][kc*32 + 8g .. +8]
-  const int key = j0 + wave * 16 + l16;
-  const bool kok = key < s.n;
-  v8 kf[C::KC], vf[C::KC];
+  // this lane's keys (B-operand / accumulator column of each of the wave's KB 16-key
+  // blocks) and their K, V fragments: kf[kb][kc] = K[key][kc*32 + 8g .. +8]
+  constexpr int KB = C::KB;
+  int key[KB];
+  bool kok[KB];
+  v8 kf[KB][C::KC], vf[KB][C::KC];
 #pragma unroll
-  for (int kc = 0; kc < C::KC; ++kc) {
-    u32x4 rk = u32x4{0u, 0u, 0u, 0u}, rv = rk;
-    if (kok) {
-      rk = ld16(s.k, s.kbase + (int64_t)key * s.ksn + kc * 32 + gq * 8);
-      if (!mla) rv = ld16(s.v, s.vbase + (int64_t)key * s.vsn + kc * 32 + gq * 8);
+  for (int kb = 0; kb < KB; ++kb) {
+    key[kb] = j0 + (wave * KB + kb) * 16 + l16;
+    kok[kb] = key[kb] < s.n;
+#pragma unroll
+    for (int kc = 0; kc < C::KC; ++kc) {
+      u32x4 rk = u32x4{0u, 0u, 0u, 0u}, rv = rk;
+      if (kok[kb]) {
+        rk = ld16(s.k, s.kbase + (int64_t)key[kb] * s.ksn + kc * 32 + gq * 8);
+        if (!mla) rv = ld16(s.v, s.vbase + (int64_t)key[kb] * s.vsn + kc * 32 + gq * 8);
+      }
+      kf[kb][kc] = __builtin_bit_cast(v8, rk);
+      vf[kb][kc] = mla ? kf[kb][kc] : __builtin_bit_cast(v8, rv);
     }
-    kf[kc] = __builtin_bit_cast(v8, rk);
-    vf[kc] = mla ? kf[kc] : __builtin_bit_cast(v8, rv);
   }
-  f32x4 dkt[C::NDB], dvt[C::NDB];
+  f32x4 dkt[KB][C::NDB], dvt[KB][C::NDB];
 #pragma unroll
-  for (int db = 0; db < C::NDB; ++db) {
-    dkt[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    dvt[db] = dkt[db];
-  }
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) {
+      dkt[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dvt[kb][db] = dkt[kb][db];
+    }
 
+  // Query steps: (head hq, sequence b, rows [p0, p0 + 32)) over every sequence whose
+  // queries attend to these keys, heads outermost.  A step's rows are loaded into
+  // registers one step ahead and written to LDS between two barriers.
   const int hq_lo = shared ? 0 : kh, hq_hi = shared ? p.H : kh + 1;
-  for (int hq = hq_lo; hq < hq_hi; ++hq) {
-    for (int b = b_lo; b < b_hi; ++b) {
-      if (SEG == 2 && ctx_batch_of(p, b) != slot) continue;
-      const SeqInfo si = seq_info(p, b);
-      const int lim = SEG == 1 ? si.mainlen : 0x7fffffff;  // causal: tokens < cu[b+1]
-      if (lim <= j0) continue;
-      const bool kvalid = kok && key < lim;
-      for (int p0 = 0; p0 < si.len; p0 += kBwdQS) {
-        __syncthreads();  // the previous step's LDS reads are done
+  struct Step {
+    int hq, b, p0;
+  };
+  auto seq_ok = [&](int b) {
+    if (SEG == 2 && ctx_batch_of(p, b) != slot) return false;
+    const SeqInfo si = seq_info(p, b);
+    return si.len > 0 && (SEG != 1 || si.mainlen > j0);  // causal: tokens < cu[b+1]
+  };
+  auto first_from = [&](int hq, int b) {
+    while (hq < hq_hi) {
+      for (; b < b_hi; ++b)
+        if (seq_ok(b)) return Step{hq, b, 0};
+      ++hq;
+      b = b_lo;
+    }
+    return Step{hq_hi, b_lo, 0};
+  };
+  auto next_step = [&](const Step& st) {
+    if (st.p0 + kBwdQS < seq_info(p, st.b).len) return Step{st.hq, st.b, st.p0 + kBwdQS};
+    return first_from(st.hq, st.b + 1);
+  };
+  constexpr int QCH = kBwdQS * C::C8;             // 16-byte chunks per step and tensor
+  constexpr int QPT = (QCH + C::NT - 1) / C::NT;  // ... per thread
+  u32x4 qreg[QPT], dreg[QPT];
+  float lreg = INFINITY, dlreg = 0.f;
+  auto fetch = [&](const Step& st) {
+    const SeqInfo si = seq_info(p, st.b);
 #pragma unroll
-        for (int it = tid; it < kBwdQS * C::C8; it += C::NT) {
-          const int r = it / C::C8, c8 = it % C::C8;
-          const int pos = p0 + r;
-          u32x4 rq = u32x4{0u, 0u, 0u, 0u}, rd = rq;
-          if (pos < si.len) {
-            rq = ld16((const char*)p.q, row_at(p.q_layout, b, hq, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + c8 * 8);
-            rd = ld16((const char*)g.dout, row_at(p.o_layout, b, hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + c8 * 8);
-          }
-          *(u32x4*)(Qs + r * C::RS + c8 * 8) = rq;
-          *(u32x4*)(Os + r * C::RS + c8 * 8) = rd;
-        }
-        if (tid < kBwdQS) {
-          const int pos = p0 + tid;
-          const bool ok = pos < si.len;
-          const int64_t at = (int64_t)hq * p.total_q + si.q0 + pos;
-          lse_s[tid] = ok ? st_lse[at] : INFINITY;  // padding rows: P = 0
-          dl_s[tid] = ok ? st_delta[at] : 0.f;
-        }
-        __syncthreads();
+    for (int li = 0; li < QPT; ++li) {
+      const int it = tid + li * C::NT;
+      const int r = it / C::C8, c8 = it % C::C8;
+      const int pos = st.p0 + r;
+      qreg[li] = u32x4{0u, 0u, 0u, 0u};
+      dreg[li] = qreg[li];
+      if ((QCH % C::NT == 0 || it < QCH) && pos < si.len) {
+        qreg[li] = ld16((const char*)p.q, row_at(p.q_layout, st.b, st.hq, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + c8 * 8);
+        dreg[li] = ld16((const char*)g.dout,
+                        row_at(p.o_layout, st.b, st.hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + c8 * 8);
+      }
+    }
+    if (tid < kBwdQS) {
+      const int pos = st.p0 + tid;
+      const bool ok = pos < si.len;
+      const int64_t at = (int64_t)st.hq * p.total_q + si.q0 + pos;
+      lreg = ok ? st_lse[at] : INFINITY;  // padding rows: P = 0
+      dlreg = ok ? st_delta[at] : 0.f;
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int li = 0; li < QPT; ++li) {
+      const int it = tid + li * C::NT;
+      if (QCH % C::NT != 0 && it >= QCH) continue;
+      const int r = it / C::C8, c8 = it % C::C8;
+      *(u32x4*)(Qs + r * C::RS + c8 * 8) = qreg[li];
+      *(u32x4*)(Os + r * C::RS + c8 * 8) = dreg[li];
+    }
+    if (tid < kBwdQS) {
+      lse_s[tid] = lreg;
+      dl_s[tid] = dlreg;
+    }
+  };
 
-        // S and dP for the two 16-row halves: lane (key + 16g) reg r = row 16h + 4g + r;
-        // P and dS packed as B operands (element 4h + r)
-        v8 pb, dsb;
+  Step cur = first_from(hq_lo, b_lo);
+  if (cur.hq < hq_hi) fetch(cur);
+  while (cur.hq < hq_hi) {
+    const Step nxt = next_step(cur);
+    const int lim = SEG == 1 ? seq_info(p, cur.b).mainlen : 0x7fffffff;
+    __syncthreads();  // the previous step's LDS reads are done
+    stage();
+    __syncthreads();
+    if (nxt.hq < hq_hi) fetch(nxt);
+
+    // S and dP for the two 16-row halves: lane (key + 16g) reg r = row 16h + 4g + r;
+    // P and dS packed as B operands (element 4h + r).  Each fragment read from LDS feeds
+    // the KB key blocks.
+    v8 pb[KB], dsb[KB];
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = sc;
+    for (int hh = 0; hh < 2; ++hh) {
+      f32x4 sc[KB], dp[KB];
 #pragma unroll
-          for (int kc = 0; kc < C::KC; ++kc) {
-            const v8 aq = *(const v8*)(Qs + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
-            const v8 ao = *(const v8*)(Os + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
-            sc = Mfma<T>::run(aq, kf[kc], sc);
-            dp = Mfma<T>::run(ao, vf[kc], dp);
-          }
-          const f32x4 L4 = *(const f32x4*)(lse_s + hh * 16 + gq * 4);
-          const f32x4 D4 = *(const f32x4*)(dl_s + hh * 16 + gq * 4);
+      for (int kb = 0; kb < KB; ++kb) {
+        sc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[kb] = sc[kb];
+      }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float pv = kvalid ? fast_exp2(fmaf(sc[r], c, -L4[r])) : 0.f;
-            pb[hh * 4 + r] = (T)pv;
-            dsb[hh * 4 + r] = (T)(pv * (dp[r] - D4[r]) * p.scale);
-          }
+      for (int kc = 0; kc < C::KC; ++kc) {
+        const v8 aq = *(const v8*)(Qs + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
+        const v8 ao = *(const v8*)(Os + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          sc[kb] = Mfma<T>::run(aq, kf[kb][kc], sc[kb]);
+          dp[kb] = Mfma<T>::run(ao, vf[kb][kc], dp[kb]);
         }
-        // dV^T += dO^T P and dK^T += Q^T dS (MLA: both into dK)
+      }
+      const f32x4 L4 = *(const f32x4*)(lse_s + hh * 16 + gq * 4);
+      const f32x4 D4 = *(const f32x4*)(dl_s + hh * 16 + gq * 4);
 #pragma unroll
-        for (int db = 0; db < C::NDB; ++db) {
-          const v8 ao = tr_frag<T>(Os, C::RS, 0, db, l16, gq);
-          const v8 aq = tr_frag<T>(Qs, C::RS, 0, db, l16, gq);
-          if (mla) {
-            dkt[db] = Mfma<T>::run(ao, pb, dkt[db]);
-          } else {
-            dvt[db] = Mfma<T>::run(ao, pb, dvt[db]);
-          }
-          dkt[db] = Mfma<T>::run(aq, dsb, dkt[db]);
+      for (int kb = 0; kb < KB; ++kb) {
+        const bool kvalid = kok[kb] && key[kb] < lim;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = kvalid ? fast_exp2(fmaf(sc[kb][r], c, -L4[r])) : 0.f;
+          pb[kb][hh * 4 + r] = (T)pv;
+          dsb[kb][hh * 4 + r] = (T)(pv * (dp[kb][r] - D4[r]) * p.scale);
         }
       }
     }
+    // dV^T += dO^T P and dK^T += Q^T dS (MLA: both into dK)
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) {
+      const v8 ao = tr_frag<T>(Os, C::RS, 0, db, l16, gq);
+      const v8 aq = tr_frag<T>(Qs, C::RS, 0, db, l16, gq);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if (mla) {
+          dkt[kb][db] = Mfma<T>::run(ao, pb[kb], dkt[kb][db]);
+        } else {
+          dvt[kb][db] = Mfma<T>::run(ao, pb[kb], dvt[kb][db]);
+        }
+        dkt[kb][db] = Mfma<T>::run(aq, dsb[kb], dkt[kb][db]);
+      }
+    }
+    cur = nxt;
   }
 
   // ---- rows: lane (key + 16g) holds d?[key][16db + 4g .. +4]
-  if (!kok) return;
 #pragma unroll
-  for (int db = 0; db < C::NDB; ++db) {
-    T k4[4], v4[4];
+  for (int kb = 0; kb < KB; ++kb) {
+    if (!kok[kb]) continue;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      k4[r] = (T)dkt[db][r];
-      v4[r] = (T)dvt[db][r];
+    for (int db = 0; db < C::NDB; ++db) {
+      T k4[4], v4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        k4[r] = (T)dkt[kb][db][r];
+        v4[r] = (T)dvt[kb][db][r];
+      }
+      *(u32x2*)(s.dk + (s.dkbase + (int64_t)key[kb] * s.dksn + db * 16 + gq * 4) * 2) = *(const u32x2*)k4;
+      if (!mla)
+        *(u32x2*)(s.dv + (s.dvbase + (int64_t)key[kb] * s.dvsn + db * 16 + gq * 4) * 2) = *(const u32x2*)v4;
     }
-    *(u32x2*)(s.dk + (s.dkbase + (int64_t)key * s.dksn + db * 16 + gq * 4) * 2) = *(const u32x2*)k4;
-    if (!mla) *(u32x2*)(s.dv + (s.dvbase + (int64_t)key * s.dvsn + db * 16 + gq * 4) * 2) = *(const u32x2*)v4;
   }
 }
 
@@ -498,7 +605,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
 struct BwdFns {
   const void* dq;
   const void* dkv[3];
-  int dq_lds, dkv_lds, bq;
+  int dq_lds, dkv_lds, bq, dkv_keys;
 };
 
 template <typename T, int D>
@@ -509,7 +616,8 @@ static BwdFns bwd_fns() {
                  (const void*)attn_bwd_dkv_kernel<T, D, 2>},
                 C::DQ_LDS,
                 C::DKV_LDS,
-                C::BQ};
+                C::BQ,
+                C::DKV_KEYS};
 }
 
 template <typename T>
@@ -615,7 +723,7 @@ extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* 
   // 2. main keys
   const unsigned kheads = p.k_sh == 0 ? 1u : (unsigned)p.H;
   const int64_t mrows = causal ? p.total_q : maxlen;
-  e = hipLaunchKernel(causal ? f.dkv[1] : f.dkv[0], dim3((unsigned)((mrows + kBwdBK - 1) / kBwdBK), kheads, causal ? 1 : p.B),
+  e = hipLaunchKernel(causal ? f.dkv[1] : f.dkv[0], dim3((unsigned)((mrows + f.dkv_keys - 1) / f.dkv_keys), kheads, causal ? 1 : p.B),
                       dim3(kBwdNW * 64), args, (size_t)f.dkv_lds, s);
   if (e != hipSuccess) return (int)e;
   // 3. context keys
@@ -623,7 +731,7 @@ extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* 
     const int64_t crows = p.cu_seqlens_kv ? p.ctx_rows : p.ctx_len;
     const int cbs = (p.cu_seqlens_kv || p.ctx_index) ? p.ctx_batch : (p.ctx_batch > 1 ? p.ctx_batch : 1);
     if (crows > 0) {
-      e = hipLaunchKernel(f.dkv[2], dim3((unsigned)((crows + kBwdBK - 1) / kBwdBK), p.c_sh == 0 ? 1u : (unsigned)p.H, cbs),
+      e = hipLaunchKernel(f.dkv[2], dim3((unsigned)((crows + f.dkv_keys - 1) / f.dkv_keys), p.c_sh == 0 ? 1u : (unsigned)p.H, cbs),
                           dim3(kBwdNW * 64), args, (size_t)f.dkv_lds, s);
       if (e != hipSuccess) return (int)e;
     }
