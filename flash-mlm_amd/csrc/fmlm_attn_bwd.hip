@@ -30,7 +30,6 @@ namespace {
 
 constexpr int kBwdNW = 4;   // waves per workgroup
 constexpr int kBwdBK = 64;  // keys per dq-kernel tile
-constexpr int kBwdQS = 32;  // query rows per dkv step
 // lazy rescale of the dq kernel's online softmax: the running max moves only when a tile's
 // max exceeds it by more than this (log2 units), so 2^(z - m) <= 2^8 before rounding
 constexpr float kRescaleSlack = 8.0f;
@@ -42,14 +41,22 @@ struct BwdCfg {
   static constexpr int NDB = D / 16;              // 16-wide column blocks
   static constexpr int RS = D + 16;               // LDS row stride (elements)
   static constexpr int C8 = D / 8;                // 16-byte chunks per row
-  static constexpr int QB = D >= 128 ? 1 : 2;     // 16-row query blocks per wave (dq kernel)
+  static constexpr int QB = D >= 256 ? 1 : 2;     // 16-row query blocks per wave (dq kernel)
+  // dq kernel: load the next key tile into registers during the current one's math
+  // (off where those registers would not fit beside QB = 2)
+  static constexpr bool PF = D <= 64;
   static constexpr int BQ = kBwdNW * QB * 16;     // query rows per dq workgroup
   static constexpr int NKB = kBwdBK / 16;
   static constexpr int NKS = kBwdBK / 32;
-  static constexpr int KB = D <= 64 ? 2 : 1;      // 16-key blocks per wave (dkv kernel)
+  // dkv kernel: 16-key blocks per wave, and whether the next query step is loaded ahead
+  // (the register budget allows both only up to D = 64; at D = 128 two blocks spill,
+  // which measured slower than one block with the load ahead)
+  static constexpr int KB = D <= 64 ? 2 : 1;
+  static constexpr bool DKV_PF = D <= 128;
   static constexpr int DKV_KEYS = kBwdNW * 16 * KB;  // keys per dkv workgroup
+  static constexpr int QS = D >= 256 ? 32 : 64;   // query rows per dkv step (32-row groups)
   static constexpr int DQ_LDS = 2 * kBwdBK * RS * 2;                  // K and V tiles
-  static constexpr int DKV_LDS = 2 * kBwdQS * RS * 2 + 2 * kBwdQS * 4;  // Q, dO, lse, delta
+  static constexpr int DKV_LDS = 2 * QS * RS * 2 + 2 * QS * 4;  // Q, dO, lse, delta
   static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
 };
 
@@ -194,8 +201,8 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
   }
 
   // key tile t of [context || main] (64 keys; rows past a segment end are 0): fetch()
-  // loads it into registers, stage() writes the registers to LDS.  The next tile's loads
-  // are issued before the current tile's math.
+  // loads it into registers, stage() writes the registers to LDS.  With PF the next
+  // tile's loads are issued before the current tile's math.
   constexpr int LPT = kBwdBK * C::C8 / C::NT;  // 16-byte chunks per thread per tensor
   u32x4 kreg[LPT], vreg[LPT];
   auto keys_in = [&](int t) {
@@ -262,13 +269,14 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
     m_i[qb] = -INFINITY;
     l_i[qb] = 0.f;
   }
-  if (nt > 0) fetch(0, true);
+  if (C::PF && nt > 0) fetch(0, true);
   for (int t = 0; t < nt; ++t) {
     const int nk = keys_in(t);
     __syncthreads();  // the previous tile's LDS reads are done
+    if (!C::PF) fetch(t, true);
     stage(true);
     __syncthreads();
-    if (t + 1 < nt) fetch(t + 1, true);
+    if (C::PF && t + 1 < nt) fetch(t + 1, true);
     f32x4 s[C::NKB][QB], dp[C::NKB][QB];
     scores(s);
     // dP^T = V dO^T, same layout as S^T
@@ -386,9 +394,9 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
   T* const Qs = (T*)smem_raw;
-  T* const Os = Qs + kBwdQS * C::RS;  // dO rows
-  float* const lse_s = (float*)(Os + kBwdQS * C::RS);
-  float* const dl_s = lse_s + kBwdQS;
+  T* const Os = Qs + C::QS * C::RS;  // dO rows
+  float* const lse_s = (float*)(Os + C::QS * C::RS);
+  float* const dl_s = lse_s + C::QS;
 
   const bool mla = p.flags & FMLM_FLAG_MLA;
   const int32_t* cu = p.cu_seqlens_q;
@@ -450,9 +458,9 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
       dvt[kb][db] = dkt[kb][db];
     }
 
-  // Query steps: (head hq, sequence b, rows [p0, p0 + 32)) over every sequence whose
+  // Query steps: (head hq, sequence b, rows [p0, p0 + QS)) over every sequence whose
   // queries attend to these keys, heads outermost.  A step's rows are loaded into
-  // registers one step ahead and written to LDS between two barriers.
+  // registers (one step ahead with DKV_PF) and written to LDS between two barriers.
   const int hq_lo = shared ? 0 : kh, hq_hi = shared ? p.H : kh + 1;
   struct Step {
     int hq, b, p0;
@@ -472,10 +480,10 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
     return Step{hq_hi, b_lo, 0};
   };
   auto next_step = [&](const Step& st) {
-    if (st.p0 + kBwdQS < seq_info(p, st.b).len) return Step{st.hq, st.b, st.p0 + kBwdQS};
+    if (st.p0 + C::QS < seq_info(p, st.b).len) return Step{st.hq, st.b, st.p0 + C::QS};
     return first_from(st.hq, st.b + 1);
   };
-  constexpr int QCH = kBwdQS * C::C8;             // 16-byte chunks per step and tensor
+  constexpr int QCH = C::QS * C::C8;             // 16-byte chunks per step and tensor
   constexpr int QPT = (QCH + C::NT - 1) / C::NT;  // ... per thread
   u32x4 qreg[QPT], dreg[QPT];
   float lreg = INFINITY, dlreg = 0.f;
@@ -494,7 +502,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
                         row_at(p.o_layout, st.b, st.hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + c8 * 8);
       }
     }
-    if (tid < kBwdQS) {
+    if (tid < C::QS) {
       const int pos = st.p0 + tid;
       const bool ok = pos < si.len;
       const int64_t at = (int64_t)st.hq * p.total_q + si.q0 + pos;
@@ -511,25 +519,28 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
       *(u32x4*)(Qs + r * C::RS + c8 * 8) = qreg[li];
       *(u32x4*)(Os + r * C::RS + c8 * 8) = dreg[li];
     }
-    if (tid < kBwdQS) {
+    if (tid < C::QS) {
       lse_s[tid] = lreg;
       dl_s[tid] = dlreg;
     }
   };
 
   Step cur = first_from(hq_lo, b_lo);
-  if (cur.hq < hq_hi) fetch(cur);
+  if (C::DKV_PF && cur.hq < hq_hi) fetch(cur);
   while (cur.hq < hq_hi) {
     const Step nxt = next_step(cur);
     const int lim = SEG == 1 ? seq_info(p, cur.b).mainlen : 0x7fffffff;
     __syncthreads();  // the previous step's LDS reads are done
+    if (!C::DKV_PF) fetch(cur);
     stage();
     __syncthreads();
-    if (nxt.hq < hq_hi) fetch(nxt);
+    if (C::DKV_PF && nxt.hq < hq_hi) fetch(nxt);
 
-    // S and dP for the two 16-row halves: lane (key + 16g) reg r = row 16h + 4g + r;
-    // P and dS packed as B operands (element 4h + r).  Each fragment read from LDS feeds
-    // the KB key blocks.
+    // per 32-row group: S and dP for its two 16-row halves (lane (key + 16g) reg r = row
+    // 32grp + 16h + 4g + r), P and dS packed as B operands (element 4h + r), then the
+    // dV / dK products.  Each fragment read from LDS feeds the KB key blocks.
+#pragma unroll
+    for (int grp = 0; grp < C::QS / 32; ++grp) {
     v8 pb[KB], dsb[KB];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -541,16 +552,16 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
       }
 #pragma unroll
       for (int kc = 0; kc < C::KC; ++kc) {
-        const v8 aq = *(const v8*)(Qs + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
-        const v8 ao = *(const v8*)(Os + (hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
+        const v8 aq = *(const v8*)(Qs + (grp * 32 + hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
+        const v8 ao = *(const v8*)(Os + (grp * 32 + hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           sc[kb] = Mfma<T>::run(aq, kf[kb][kc], sc[kb]);
           dp[kb] = Mfma<T>::run(ao, vf[kb][kc], dp[kb]);
         }
       }
-      const f32x4 L4 = *(const f32x4*)(lse_s + hh * 16 + gq * 4);
-      const f32x4 D4 = *(const f32x4*)(dl_s + hh * 16 + gq * 4);
+      const f32x4 L4 = *(const f32x4*)(lse_s + grp * 32 + hh * 16 + gq * 4);
+      const f32x4 D4 = *(const f32x4*)(dl_s + grp * 32 + hh * 16 + gq * 4);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const bool kvalid = kok[kb] && key[kb] < lim;
@@ -565,8 +576,8 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
     // dV^T += dO^T P and dK^T += Q^T dS (MLA: both into dK)
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db) {
-      const v8 ao = tr_frag<T>(Os, C::RS, 0, db, l16, gq);
-      const v8 aq = tr_frag<T>(Qs, C::RS, 0, db, l16, gq);
+      const v8 ao = tr_frag<T>(Os, C::RS, grp * 32, db, l16, gq);
+      const v8 aq = tr_frag<T>(Qs, C::RS, grp * 32, db, l16, gq);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         if (mla) {
@@ -576,6 +587,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
         }
         dkt[kb][db] = Mfma<T>::run(aq, dsb[kb], dkt[kb][db]);
       }
+    }
     }
     cur = nxt;
   }
