@@ -450,6 +450,10 @@ class InferenceCache:
                 raise ValueError(message)
         return entry
 
+    def layer_entry(self, layer_id: int | str) -> LayerKVEntry | None:
+        """The entry of ``layer_id`` as stored, or None (no shape or mode checks)."""
+        return self._layer_kv.get(self._layer_key(layer_id))
+
     def clear_layer(self, layer_id: int | str) -> None:
         self._layer_kv.pop(self._layer_key(layer_id), None)
 

@@ -99,7 +99,7 @@ def _cache_tensors(inference_cache, layer_id, prefill: bool):
     """The cached context tensors a call reads, (None, None) without a context."""
     if prefill or inference_cache is None or layer_id is None:
         return None, None, None
-    entry = inference_cache._layer_kv.get(inference_cache._layer_key(layer_id))
+    entry = inference_cache.layer_entry(layer_id)
     if entry is None:
         return None, None, None
     return entry.k_cache, entry.v_cache, entry

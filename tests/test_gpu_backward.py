@@ -262,3 +262,34 @@ def test_backward_unsupported_raise(device):
     # no grad wanted: the forward still runs for those shapes
     with torch.no_grad():
         flash_attn_mlm_compressed(q16, q16, q16, H, meta, 0.1, block_n=64)
+
+
+def test_backward_mla_shared_tensor_and_strided_views(device):
+    """MLA called as (q, k, k) with one tensor (its gradient is the latent's), and q/k/v
+    given as non-contiguous views of [B, N, H, D] buffers."""
+    gen = torch.Generator().manual_seed(7700)
+    lengths = [48, 20]
+    B, H, N, D, dtype = 2, 4, 48, 64, torch.bfloat16
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    from flash_mlm import unpack_from_kernel
+
+    q = _leaf((B, H, N, D), dtype, device, gen)
+    k = _leaf((B, H, N, D), dtype, device, gen)
+    out = flash_attn_mlm_compressed(q, k, k, H, meta, 0.2, is_mla=True, block_n=64)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    g = ar.mlm_attention_packed_backward(_np(q), _np(k), _np(k), _np(unpack_from_kernel(dout, meta, H)), lengths,
+                                         0.2, is_mla=True)
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk (latent = head 0)")
+    assert torch.count_nonzero(k.grad[:, 1:]) == 0  # only head 0 is read
+
+    base = [(torch.randn((B, N, H, D), generator=gen) * 0.5).to(dtype).to(device).requires_grad_() for _ in range(3)]
+    qv, kv, vv = (t.transpose(1, 2) for t in base)  # [B, H, N, D] views, not contiguous
+    out = flash_attn_mlm_compressed(qv, kv, vv, H, meta, 0.2, block_n=64)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    g = ar.mlm_attention_packed_backward(_np(qv), _np(kv), _np(vv), _np(unpack_from_kernel(dout, meta, H)),
+                                         lengths, 0.2)
+    for t, ref, name in zip(base, g[:3], ("dq", "dk", "dv")):
+        _close(t.grad.transpose(1, 2), ref, name + " (strided)")

@@ -136,6 +136,17 @@ def test_paged_context_longer_than_64_pages(mla, device):
     assert torch.equal(out, out_flat)
 
 
+def test_paged_context_has_no_backward(device):
+    cache = _paged([70, 10], H=2, D=64, mla=False, dtype=torch.bfloat16, device=device)[0]
+    lengths = [5, 9]
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), 9, block_n=64)
+    q = torch.randn((2, 2, 9, 64), device=device).to(torch.bfloat16).requires_grad_()
+    with pytest.raises(ValueError, match="paged KV contexts have no attention backward"):
+        flash_attn_mlm_compressed(q, q.detach(), q.detach(), 2, meta, 0.1, cache, 0, block_n=64)
+    with torch.no_grad():  # the forward alone is fine
+        flash_attn_mlm_compressed(q, q, q, 2, meta, 0.1, cache, 0, block_n=64)
+
+
 def test_paged_context_errors(device):
     B, H, N, D = 2, 2, 32, 64
     q, k, v = (torch.randn((B, H, N, D), device=device).to(torch.bfloat16) for _ in range(3))

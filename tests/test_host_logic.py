@@ -266,3 +266,13 @@ def test_compute_paths_refuse_cpu_tensors():
         hu.pack_for_kernel(q, meta)
     with pytest.raises(ValueError, match="no CPU compute path"):
         hu.unpack_from_kernel(torch.zeros(8, 16), meta, 2)
+
+
+def test_layer_entry_returns_the_stored_tensors():
+    cache = InferenceCache()
+    k = torch.zeros(6, 4, requires_grad=True)
+    v = torch.zeros(6, 4)
+    cache.prefill_kv_cache("x", k_cache=k, v_cache=v, context_batch_size=1, is_mla=False, num_heads=2, head_dim=4)
+    entry = cache.layer_entry("x")
+    assert entry.k_cache is k and entry.v_cache is v  # gradients reach the caller's tensors
+    assert cache.layer_entry("y") is None
