@@ -143,7 +143,68 @@ FMLM_DEV typename Mfma<T>::v8 tr_frag(const T* tile, int rs, int row0, int db, i
 }
 
 // ---------------------------------------------------------------------------
-// dq kernel: grid (query tiles, H, B), kBwdNW waves, QB blocks of 16 rows per wave.
+// Unit tables.  The workspace holds, after the row statistics (2*H*total_q floats), three
+// exclusive prefix sums of tile counts: query tiles of BQ rows per sequence (B + 1),
+// key tiles of DKV_KEYS rows per sequence (B + 1) and per context batch (n_ctx + 1).  A
+// workgroup maps its linear unit id to (sequence or batch, tile) by binary search, so
+// the grids hold only real tiles plus a bound of one per sequence / batch.
+// ---------------------------------------------------------------------------
+struct UnitTables {
+  int32_t* q;  // [B + 1]
+  int32_t* k;  // [B + 1]
+  int32_t* c;  // [n_ctx + 1]
+};
+
+FMLM_DEV UnitTables unit_tables(const fmlm_attn_params& p, const fmlm_attn_grads& g) {
+  UnitTables t;
+  t.q = (int32_t*)((char*)g.workspace + 2 * (int64_t)p.H * p.total_q * 4);
+  t.k = t.q + p.B + 1;
+  t.c = t.k + p.B + 1;
+  return t;
+}
+
+constexpr int kScanThreads = 1024;
+
+// exclusive prefix sums of ceil(len / tile) over n entries, one workgroup
+template <typename LenFn>
+FMLM_DEV void scan_tiles(int n, int tile, LenFn len, int32_t* out, int32_t* part) {
+  const int tid = threadIdx.x;
+  const int per = (n + kScanThreads - 1) / kScanThreads;
+  const int i0 = min(tid * per, n), i1 = min(i0 + per, n);
+  int sum = 0;
+  for (int i = i0; i < i1; ++i) sum += (max(len(i), 0) + tile - 1) / tile;
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kScanThreads; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int run = tid > 0 ? part[tid - 1] : 0;
+  for (int i = i0; i < i1; ++i) {
+    out[i] = run;
+    run += (max(len(i), 0) + tile - 1) / tile;
+  }
+  if (tid == kScanThreads - 1) out[n] = part[tid];
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kScanThreads) void bwd_units_kernel(const fmlm_attn_params p, const fmlm_attn_grads g,
+                                                                 int bq, int bk, int n_ctx) {
+  __shared__ int32_t part[kScanThreads];
+  const UnitTables t = unit_tables(p, g);
+  scan_tiles(p.B, bq, [&](int b) { return seq_info(p, b).len; }, t.q, part);
+  scan_tiles(p.B, bk, [&](int b) { return seq_info(p, b).len; }, t.k, part);
+  scan_tiles(n_ctx, bk, [&](int cb) {
+    int c0, c1;
+    ctx_range(p, cb, c0, c1);
+    return c1 - c0;
+  }, t.c, part);
+}
+
+// ---------------------------------------------------------------------------
+// dq kernel: grid (query-tile units, H), kBwdNW waves, QB blocks of 16 rows per wave.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_attn_params p,
@@ -155,9 +216,12 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
   T* const Ks = (T*)smem_raw;
   T* const Vs = Ks + kBwdBK * C::RS;
 
-  const int b = blockIdx.z, h = blockIdx.y;
+  const UnitTables ut = unit_tables(p, g);
+  const int u = blockIdx.x, h = blockIdx.y;
+  if (u >= ut.q[p.B]) return;
+  const int b = find_seq(ut.q, p.B, u);
   const SeqInfo si = seq_info(p, b);
-  const int qpos0 = blockIdx.x * C::BQ;
+  const int qpos0 = (u - ut.q[b]) * C::BQ;
   if (qpos0 >= si.len) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
@@ -384,12 +448,15 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV kernel.  SEG: 0 = main keys of sequence blockIdx.z, 1 = causal token range,
-// 2 = context batch blockIdx.z.  grid (key tiles, key heads, slots).
+// dK / dV kernel, context keys and main keys in one grid (units, key heads): the first
+// units are key tiles of the context batches (unit table), the following ones key tiles
+// of the main keys (per sequence from the unit table, or with CAUSAL the tiles of the
+// causal token range).  Context tiles go first: a shared context's tiles take the
+// queries of every sequence and are the longest units.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int SEG>
+template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm_attn_params p,
-                                                                      const fmlm_attn_grads g) {
+                                                                      const fmlm_attn_grads g, int n_ctx) {
   typedef BwdCfg<D> C;
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
@@ -400,17 +467,37 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
 
   const bool mla = p.flags & FMLM_FLAG_MLA;
   const int32_t* cu = p.cu_seqlens_q;
-  const int kh = blockIdx.y, slot = blockIdx.z;
-  const int j0 = blockIdx.x * C::DKV_KEYS;
+  const int kh = blockIdx.y;
+  const UnitTables ut = unit_tables(p, g);
+  const int n_main = CAUSAL ? (min(cu[p.B], p.total_q) + C::DKV_KEYS - 1) / C::DKV_KEYS : ut.k[p.B];
+  const int n_cunits = n_ctx > 0 ? ut.c[n_ctx] : 0;
+  const int u = blockIdx.x;
+  const bool is_ctx = u < n_cunits;
+  int slot, j0;
+  if (is_ctx) {
+    slot = find_seq(ut.c, n_ctx, u);
+    j0 = (u - ut.c[slot]) * C::DKV_KEYS;
+  } else {
+    const int um = u - n_cunits;
+    if (um >= n_main) return;
+    if (CAUSAL) {
+      slot = 0;
+      j0 = um * C::DKV_KEYS;
+    } else {
+      slot = find_seq(ut.k, p.B, um);
+      j0 = (um - ut.k[slot]) * C::DKV_KEYS;
+    }
+  }
+  const bool causal_main = CAUSAL && !is_ctx;
   BSeg s;
   int b_lo, b_hi;  // sequences whose queries may attend to these keys
   bool shared;     // key rows shared by all heads (head stride 0)
-  if (SEG == 2) {
+  if (is_ctx) {
     s = ctx_seg(p, g, slot, kh);
     b_lo = 0;
     b_hi = p.B;
     shared = p.c_sh == 0;
-  } else if (SEG == 1) {
+  } else if (CAUSAL) {
     s = main_seg(p, g, -1, kh);
     b_lo = j0 < s.n ? find_seq(cu, p.B, j0) : p.B;
     b_hi = p.B;
@@ -421,7 +508,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
     b_hi = slot + 1;
     shared = p.k_sh == 0;
   }
-  if (j0 >= s.n) return;
+  if (j0 >= s.n || (shared && kh > 0)) return;  // the grid covers the larger segment kind
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
   const float c = p.scale * kLog2e;
@@ -466,9 +553,9 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
     int hq, b, p0;
   };
   auto seq_ok = [&](int b) {
-    if (SEG == 2 && ctx_batch_of(p, b) != slot) return false;
+    if (is_ctx && ctx_batch_of(p, b) != slot) return false;
     const SeqInfo si = seq_info(p, b);
-    return si.len > 0 && (SEG != 1 || si.mainlen > j0);  // causal: tokens < cu[b+1]
+    return si.len > 0 && (!causal_main || si.mainlen > j0);  // causal: tokens < cu[b+1]
   };
   auto first_from = [&](int hq, int b) {
     while (hq < hq_hi) {
@@ -529,7 +616,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
   if (C::DKV_PF && cur.hq < hq_hi) fetch(cur);
   while (cur.hq < hq_hi) {
     const Step nxt = next_step(cur);
-    const int lim = SEG == 1 ? seq_info(p, cur.b).mainlen : 0x7fffffff;
+    const int lim = causal_main ? seq_info(p, cur.b).mainlen : 0x7fffffff;
     __syncthreads();  // the previous step's LDS reads are done
     if (!C::DKV_PF) fetch(cur);
     stage();
@@ -616,7 +703,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
 // ---------------------------------------------------------------------------
 struct BwdFns {
   const void* dq;
-  const void* dkv[3];
+  const void* dkv[2];  // main keys per sequence / causal token range (+ context)
   int dq_lds, dkv_lds, bq, dkv_keys;
 };
 
@@ -624,8 +711,7 @@ template <typename T, int D>
 static BwdFns bwd_fns() {
   typedef BwdCfg<D> C;
   return BwdFns{(const void*)attn_bwd_dq_kernel<T, D>,
-                {(const void*)attn_bwd_dkv_kernel<T, D, 0>, (const void*)attn_bwd_dkv_kernel<T, D, 1>,
-                 (const void*)attn_bwd_dkv_kernel<T, D, 2>},
+                {(const void*)attn_bwd_dkv_kernel<T, D, false>, (const void*)attn_bwd_dkv_kernel<T, D, true>},
                 C::DQ_LDS,
                 C::DKV_LDS,
                 C::BQ,
@@ -704,8 +790,9 @@ using namespace fmlm;
 extern "C" int fmlm_attn_grads_size(void) { return (int)sizeof(fmlm_attn_grads); }
 
 extern "C" int64_t fmlm_attn_bwd_workspace_bytes(const fmlm_attn_params* p) {
-  if (!p || p->H < 0 || p->total_q < 0) return FMLM_E_ARG;
-  const int64_t bytes = 2 * (int64_t)p->H * p->total_q * 4;
+  if (!p || p->H < 0 || p->total_q < 0 || p->B < 0 || p->ctx_batch < 0) return FMLM_E_ARG;
+  // row statistics, then the unit tables (B + 1, B + 1, context batches + 1 ints)
+  const int64_t bytes = 2 * (int64_t)p->H * p->total_q * 4 + 4 * (2 * ((int64_t)p->B + 1) + (p->ctx_batch > 1 ? p->ctx_batch : 1) + 1);
   return (bytes + 255) / 256 * 256;
 }
 
@@ -718,35 +805,35 @@ extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* 
   if (rc) return rc;
   if (p.B == 0 || p.H == 0 || p.total_q == 0) return 0;
   if (!g.workspace || g.workspace_bytes < fmlm_attn_bwd_workspace_bytes(pp)) return FMLM_E_WORKSPACE;
-  if (p.B > 65535 || p.H > 65535 || p.ctx_batch > 65535) return FMLM_E_ARG;
+  if (p.H > 65535) return FMLM_E_ARG;
   hipStream_t s = (hipStream_t)stream;
   const bool prefill = p.flags & FMLM_FLAG_PREFILL;
   const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
-  const int64_t maxlen = p.N > 0 ? p.N : p.total_q;
   fmlm_attn_params pc = p;
   fmlm_attn_grads gc = g;
   void* args[] = {(void*)&pc, (void*)&gc};
 
-  // 1. dq (+ the row statistics)
+  const bool ctx_grads = g.dk_ctx && !prefill && p.k_ctx;
+  int n_ctx = ctx_grads ? (p.ctx_batch > 1 ? p.ctx_batch : 1) : 0;
+  // 0. unit tables
+  hipLaunchKernelGGL(bwd_units_kernel, dim3(1), dim3(kScanThreads), 0, s, p, g, f.bq, f.dkv_keys, n_ctx);
+  if ((rc = launch_status())) return rc;
+  // 1. dq (+ the row statistics): at most total_q / BQ + B query tiles per head
   if ((rc = raise_lds(f.dq, f.dq_lds))) return rc;
-  hipError_t e = hipLaunchKernel(f.dq, dim3((unsigned)((maxlen + f.bq - 1) / f.bq), p.H, p.B), dim3(kBwdNW * 64),
-                                 args, (size_t)f.dq_lds, s);
+  const int64_t qunits = (int64_t)p.total_q / f.bq + p.B;
+  if (qunits > 0x7fffffff) return FMLM_E_ARG;
+  hipError_t e = hipLaunchKernel(f.dq, dim3((unsigned)qunits, p.H), dim3(kBwdNW * 64), args, (size_t)f.dq_lds, s);
   if (e != hipSuccess) return (int)e;
-  // 2. main keys
-  const unsigned kheads = p.k_sh == 0 ? 1u : (unsigned)p.H;
-  const int64_t mrows = causal ? p.total_q : maxlen;
-  e = hipLaunchKernel(causal ? f.dkv[1] : f.dkv[0], dim3((unsigned)((mrows + f.dkv_keys - 1) / f.dkv_keys), kheads, causal ? 1 : p.B),
-                      dim3(kBwdNW * 64), args, (size_t)f.dkv_lds, s);
+  // 2. dK / dV, context keys then main keys in one launch
+  const int64_t munits = causal ? ((int64_t)p.total_q + f.dkv_keys - 1) / f.dkv_keys : (int64_t)p.total_q / f.dkv_keys + p.B;
+  const int64_t crows = !ctx_grads ? 0 : (p.cu_seqlens_kv ? p.ctx_rows : (int64_t)n_ctx * p.ctx_len);
+  const int64_t cunits = ctx_grads ? crows / f.dkv_keys + n_ctx : 0;
+  if (munits + cunits > 0x7fffffff) return FMLM_E_ARG;
+  const unsigned kheads = (p.k_sh == 0 && (n_ctx == 0 || p.c_sh == 0)) ? 1u : (unsigned)p.H;
+  void* kargs[] = {(void*)&pc, (void*)&gc, (void*)&n_ctx};
+  if ((rc = raise_lds(f.dkv[causal ? 1 : 0], f.dkv_lds))) return rc;
+  e = hipLaunchKernel(f.dkv[causal ? 1 : 0], dim3((unsigned)(munits + cunits), kheads), dim3(kBwdNW * 64), kargs,
+                      (size_t)f.dkv_lds, s);
   if (e != hipSuccess) return (int)e;
-  // 3. context keys
-  if (g.dk_ctx && !prefill && p.k_ctx) {
-    const int64_t crows = p.cu_seqlens_kv ? p.ctx_rows : p.ctx_len;
-    const int cbs = (p.cu_seqlens_kv || p.ctx_index) ? p.ctx_batch : (p.ctx_batch > 1 ? p.ctx_batch : 1);
-    if (crows > 0) {
-      e = hipLaunchKernel(f.dkv[2], dim3((unsigned)((crows + f.dkv_keys - 1) / f.dkv_keys), p.c_sh == 0 ? 1u : (unsigned)p.H, cbs),
-                          dim3(kBwdNW * 64), args, (size_t)f.dkv_lds, s);
-      if (e != hipSuccess) return (int)e;
-    }
-  }
   return launch_status();
 }

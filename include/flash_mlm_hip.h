@@ -241,7 +241,8 @@ FMLM_API int fmlm_attn_fwd(const fmlm_attn_params* p, void* stream);
  * Rows not listed are not written.  dout is laid out like o (o_layout).
  * bf16 / f16, D in {32, 64, 128, 256}; contiguous (non-paged) contexts; with
  * FMLM_FLAG_CAUSAL_SEQ the main keys must be packed (kv_layout PACKED).
- * workspace: fmlm_attn_bwd_workspace_bytes(p) bytes (per-row softmax statistics).
+ * workspace: fmlm_attn_bwd_workspace_bytes(p) bytes (per-row softmax statistics and the
+ *           tile tables of the two kernels).
  * ------------------------------------------------------------------------- */
 typedef struct fmlm_attn_grads {
   const void* dout; int64_t do_sb, do_sh, do_sn;
