@@ -17,6 +17,8 @@ the padded prefill length; the HIP kernel picks its own tiles from the head dim.
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from flash_mlm import _lib
@@ -109,13 +111,29 @@ def _wants_grad(*tensors) -> bool:
     return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
 
 
-def _check_backward_supported(q: torch.Tensor, d: int, entry) -> None:
+def _backward_unsupported(q: torch.Tensor, d: int, entry) -> str | None:
+    """Why this call has no backward, or None."""
     if q.dtype not in (torch.bfloat16, torch.float16):
-        raise ValueError("the attention backward needs bf16 or fp16 inputs")
+        return "the attention backward needs bf16 or fp16 inputs"
     if d not in _BWD_HEAD_DIMS:
-        raise ValueError("the attention backward supports head_dim 32, 64, 128 or 256")
+        return "the attention backward supports head_dim 32, 64, 128 or 256"
     if entry is not None and entry.block_table is not None:
-        raise ValueError("paged KV contexts have no attention backward")
+        return "paged KV contexts have no attention backward"
+    return None
+
+
+def _run(impl, q, k, v, inference_cache, layer_id, prefill: bool):
+    """Run one attention call, through autograd when an input requires grad.  A call
+    without a backward (see _backward_unsupported) returns its output without a graph,
+    as the reference's kernels do, and warns that no gradient will flow."""
+    kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
+    if not _wants_grad(q, k, v, kc, vc):
+        return impl()[0]
+    why = _backward_unsupported(q, int(q.shape[-1]), entry)
+    if why is not None:
+        warnings.warn(f"flash_mlm: {why}; the output carries no gradient", stacklevel=3)
+        return impl()[0]
+    return _Attention.apply(impl, q, k, v, kc, vc)
 
 
 class _Attention(torch.autograd.Function):
@@ -362,11 +380,7 @@ def flash_attn_mlm(
             context_index=context_index,
         )
 
-    kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
-    if _wants_grad(q, k, v, kc, vc):
-        _check_backward_supported(q, int(q.shape[-1]), entry)
-        return _Attention.apply(impl, q, k, v, kc, vc)
-    return impl()[0]
+    return _run(impl, q, k, v, inference_cache, layer_id, prefill)
 
 
 def _dense_impl(
@@ -537,11 +551,7 @@ def flash_attn_mlm_compressed(
             block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, context_index=context_index,
         )
 
-    kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
-    if _wants_grad(q, k, v, kc, vc):
-        _check_backward_supported(q, int(q.shape[-1]), entry)
-        return _Attention.apply(impl, q, k, v, kc, vc)
-    return impl()[0]
+    return _run(impl, q, k, v, inference_cache, layer_id, prefill)
 
 
 def _compressed_impl(
@@ -756,11 +766,7 @@ def flash_attn_mlm_precompressed(
             layer_id, is_mla, context_batch_size, prefill, causal_query_seq_attn, context_index,
         )
 
-    kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
-    if _wants_grad(q, k, v, kc, vc):
-        _check_backward_supported(q, int(q.shape[-1]), entry)
-        return _Attention.apply(impl, q, k, v, kc, vc)
-    return impl()[0]
+    return _run(impl, q, k, v, inference_cache, layer_id, prefill)
 
 
 def _precompressed_impl(

@@ -250,17 +250,20 @@ def test_backward_against_torch_fp32_autograd(device):
         _close(got, ref.detach().cpu().numpy().astype(np.float64), name)
 
 
-def test_backward_unsupported_raise(device):
+def test_backward_unsupported_warns_and_returns_plain_output(device):
+    """fp32 and head dims without a backward kernel: the forward runs as in the reference
+    (no graph on the output) and a warning says no gradient will flow."""
     B, H, N, D = 1, 1, 8, 64
     meta = build_pack_metadata(torch.tensor([8], device=device, dtype=torch.int32), N, block_n=64)
     q = torch.randn((B, H, N, D), device=device, requires_grad=True)  # fp32
-    with pytest.raises(ValueError, match="bf16 or fp16"):
-        flash_attn_mlm_compressed(q, q.detach(), q.detach(), H, meta, 0.1, block_n=64)
+    with pytest.warns(UserWarning, match="bf16 or fp16"):
+        out = flash_attn_mlm_compressed(q, q.detach(), q.detach(), H, meta, 0.1, block_n=64)
+    assert out.grad_fn is None and not out.requires_grad
     q16 = torch.randn((B, H, N, 16), device=device).to(torch.bfloat16).requires_grad_()
-    with pytest.raises(ValueError, match="head_dim"):
-        flash_attn_mlm_compressed(q16, q16.detach(), q16.detach(), H, meta, 0.1, block_n=64)
-    # no grad wanted: the forward still runs for those shapes
-    with torch.no_grad():
+    with pytest.warns(UserWarning, match="head_dim"):
+        out = flash_attn_mlm_compressed(q16, q16.detach(), q16.detach(), H, meta, 0.1, block_n=64)
+    assert out.grad_fn is None
+    with torch.no_grad():  # no gradient wanted: no warning either
         flash_attn_mlm_compressed(q16, q16, q16, H, meta, 0.1, block_n=64)
 
 
