@@ -142,8 +142,10 @@ def test_backward_context_index_and_frozen_cache(device):
 
 
 @pytest.mark.parametrize("mla", [False, True])
-@pytest.mark.parametrize("cbs", [1, 3])
+@pytest.mark.parametrize("cbs", [1, 3, 2])
 def test_backward_dense_with_context(mla, cbs, device):
+    """cbs 1: shared context; 3: one per sequence; 2: two contexts for three sequences
+    through context_index."""
     gen = torch.Generator().manual_seed(7300 + 2 * mla + cbs)
     B, H, N, D, C, dtype = 3, 2, 96, 64, 70, torch.bfloat16
     scale = 1.0 / math.sqrt(D)
@@ -152,11 +154,13 @@ def test_backward_dense_with_context(mla, cbs, device):
     vc = None if mla else _leaf(kc.shape, dtype, device, gen)
     cache = InferenceCache()
     cache.prefill_kv_cache(0, k_cache=kc, v_cache=vc, context_batch_size=cbs, is_mla=mla, num_heads=H, head_dim=D)
-    out = flash_attn_mlm(q, k, v, scale, cache, 0, is_mla=mla)
+    idx = torch.tensor([1, 0, 1], dtype=torch.int32) if cbs == 2 else None
+    out = flash_attn_mlm(q, k, v, scale, cache, 0, is_mla=mla, context_index=idx)
     dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
     out.backward(dout)
     g = ar.mlm_attention_dense_backward(_np(q), _np(k), _np(v), _np(dout), scale, is_mla=mla, k_cache=_np(kc),
-                                        v_cache=None if mla else _np(vc), context_len=C, context_batch_size=cbs)
+                                        v_cache=None if mla else _np(vc), context_len=C, context_batch_size=cbs,
+                                        context_index=None if idx is None else idx.tolist())
     _close(q.grad, g[0], "dq")
     _close(k.grad, g[1], "dk")
     _close(kc.grad, g[3], "dk_cache")
@@ -167,6 +171,8 @@ def test_backward_dense_with_context(mla, cbs, device):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_backward_precompressed_matches_compressed(causal, device):
+    """Same call through the precompressed and the compressed entry points, each with its
+    own copy of a cached context: equal gradients for q, k, v and the context."""
     gen = torch.Generator().manual_seed(7400 + causal)
     lengths = [40, 3, 77]
     B, H, N, D, dtype = len(lengths), 2, 80, 128, torch.bfloat16
@@ -177,13 +183,22 @@ def test_backward_precompressed_matches_compressed(causal, device):
     qp = torch.cat([q0[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D).contiguous().requires_grad_()
     kp = torch.cat([k0[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D).contiguous().requires_grad_()
     vp = torch.cat([v0[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D).contiguous().requires_grad_()
+    cache1, kc1, vc1, _, _ = _packed_cache([30, 0, 100], H=H, D=D, mla=False, dtype=dtype, device=device, gen=gen)
+    cache2, kc2, vc2, _, _ = _packed_cache([30, 0, 100], H=H, D=D, mla=False, dtype=dtype, device=device,
+                                           gen=torch.Generator().manual_seed(0))
+    with torch.no_grad():
+        kc2.copy_(kc1)
+        vc2.copy_(vc1)
     out = flash_attn_mlm_precompressed(qp, kp, vp, H, T, meta.cu_seqlens, meta.batch_ids_q, meta.q_tile_starts_q,
-                                       0.2, block_n=64, causal_query_seq_attn=causal)
+                                       0.2, cache1, 0, block_n=64, causal_query_seq_attn=causal)
     dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
     out.backward(dout)
     qd, kd, vd = (t.clone().requires_grad_() for t in (q0, k0, v0))
-    out2 = flash_attn_mlm_compressed(qd, kd, vd, H, meta, 0.2, block_n=64, causal_query_seq_attn=causal)
+    out2 = flash_attn_mlm_compressed(qd, kd, vd, H, meta, 0.2, cache2, 0, block_n=64, causal_query_seq_attn=causal)
     out2.backward(dout)
+    torch.testing.assert_close(kc1.grad, kc2.grad, atol=1e-5, rtol=0)
+    torch.testing.assert_close(vc1.grad, vc2.grad, atol=1e-5, rtol=0)
+    assert torch.count_nonzero(kc1.grad) > 0
 
     def packed(x):
         return torch.cat([x[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(H * T, D)
