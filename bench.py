@@ -445,8 +445,8 @@ def backward_kernels(case: Case, reps: int = 20) -> dict | None:
     from flash_mlm.host import host as hh
 
     plan = case.attention
-    if plan is None or case.dtype not in (torch.bfloat16, torch.float16) or case.D not in (32, 64, 128, 256) \
-            or plan.params.ctx_block_table:
+    if plan is None or case.dtype not in (torch.bfloat16, torch.float16) or plan.params.ctx_block_table \
+            or not (case.D in (32, 64, 128, 256) or (case.D == 512 and case.is_mla)):
         return None
     plan()  # the forward output the backward reads
     out = plan.keep[1]
@@ -457,7 +457,7 @@ def backward_kernels(case: Case, reps: int = 20) -> dict | None:
     peak = MFMA_PEAK_TFLOPS[case.dtype]
     return {"ms": round(ms, 5), "effective_gflop": round(F / 1e9, 4), "tflops": round(F / (ms * 1e-3) / 1e12, 3),
             "frac": round(F / (ms * 1e-3) / 1e12 / peak, 5),
-            "grads": "q, k, v" + (", context" if g.dk_ctx else "")}
+            "grads": ("q, latent k" if case.is_mla else "q, k, v") + (", context" if g.dk_ctx else "")}
 
 
 def cpu_baseline(case: Case, budget_s: float = 20.0) -> dict:

@@ -57,7 +57,11 @@ struct BwdCfg {
   static constexpr int QS = D >= 256 ? 32 : 64;   // query rows per dkv step (32-row groups)
   static constexpr int DQ_LDS = 2 * kBwdBK * RS * 2;                  // K and V tiles
   static constexpr int DKV_LDS = 2 * QS * RS * 2 + 2 * QS * 4;  // Q, dO, lse, delta
-  static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
+  // waves per SIMD the kernels are built for: the 512-wide latent needs more than 256
+  // registers per wave, which gfx950 gives a wave (VGPRs + AGPRs) only at one wave per SIMD
+  static constexpr int WPS = D >= 512 ? 1 : 2;
+  static constexpr bool MLA_ONLY = D >= 512;  // the 512-wide head dim exists for the MLA latent only
+  static_assert(D % 32 == 0 && D >= 32 && D <= 512, "head dim");
 };
 
 // element offset of row (sequence b, head h, position pos) in a tensor of `layout`
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(kScanThreads) void bwd_units_kernel(const fmlm_attn
 // dq kernel: grid (query-tile units, H), kBwdNW waves, QB blocks of 16 rows per wave.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_attn_params p,
+__global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kernel(const fmlm_attn_params p,
                                                                      const fmlm_attn_grads g) {
   typedef BwdCfg<D> C;
   typedef typename Mfma<T>::v8 v8;
@@ -455,7 +459,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dq_kernel(const fmlm_
 // queries of every sequence and are the longest units.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm_attn_params p,
+__global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kernel(const fmlm_attn_params p,
                                                                       const fmlm_attn_grads g, int n_ctx) {
   typedef BwdCfg<D> C;
   typedef typename Mfma<T>::v8 v8;
@@ -465,7 +469,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
   float* const lse_s = (float*)(Os + C::QS * C::RS);
   float* const dl_s = lse_s + C::QS;
 
-  const bool mla = p.flags & FMLM_FLAG_MLA;
+  const bool mla = C::MLA_ONLY || (p.flags & FMLM_FLAG_MLA);
   const int32_t* cu = p.cu_seqlens_q;
   const int kh = blockIdx.y;
   const UnitTables ut = unit_tables(p, g);
@@ -536,13 +540,13 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
       vf[kb][kc] = mla ? kf[kb][kc] : __builtin_bit_cast(v8, rv);
     }
   }
-  f32x4 dkt[KB][C::NDB], dvt[KB][C::NDB];
+  f32x4 dkt[KB][C::NDB], dvt[KB][C::MLA_ONLY ? 1 : C::NDB];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db) {
       dkt[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-      dvt[kb][db] = dkt[kb][db];
+      if (!C::MLA_ONLY) dvt[kb][db] = dkt[kb][db];
     }
 
   // Query steps: (head hq, sequence b, rows [p0, p0 + QS)) over every sequence whose
@@ -669,7 +673,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
       for (int kb = 0; kb < KB; ++kb) {
         if (mla) {
           dkt[kb][db] = Mfma<T>::run(ao, pb[kb], dkt[kb][db]);
-        } else {
+        } else if constexpr (!C::MLA_ONLY) {
           dvt[kb][db] = Mfma<T>::run(ao, pb[kb], dvt[kb][db]);
         }
         dkt[kb][db] = Mfma<T>::run(aq, dsb[kb], dkt[kb][db]);
@@ -689,7 +693,7 @@ __global__ __launch_bounds__(kBwdNW * 64, 2) void attn_bwd_dkv_kernel(const fmlm
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         k4[r] = (T)dkt[kb][db][r];
-        v4[r] = (T)dvt[kb][db][r];
+        v4[r] = C::MLA_ONLY ? (T)0.f : (T)dvt[kb][db][r];
       }
       *(u32x2*)(s.dk + (s.dkbase + (int64_t)key[kb] * s.dksn + db * 16 + gq * 4) * 2) = *(const u32x2*)k4;
       if (!mla)
@@ -725,6 +729,7 @@ static bool pick_bwd(int D, BwdFns& f) {
     case 64: f = bwd_fns<T, 64>(); return true;
     case 128: f = bwd_fns<T, 128>(); return true;
     case 256: f = bwd_fns<T, 256>(); return true;
+    case 512: f = bwd_fns<T, 512>(); return true;  // MLA latent only (checked by the caller)
     default: return false;
   }
 }
@@ -760,6 +765,7 @@ static int check_bwd(const fmlm_attn_params& p, const fmlm_attn_grads& g, BwdFns
   } else {
     return FMLM_E_DTYPE;
   }
+  if (p.D == 512 && !mla) return FMLM_E_HEAD_DIM;  // the 512-wide head dim is the MLA latent
   const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
   if (causal && (!p.cu_seqlens_q || p.kv_layout != FMLM_LAYOUT_PACKED)) return FMLM_E_ARG;
   if (p.ctx_block_table) return FMLM_E_ARG;  // paged contexts: forward only

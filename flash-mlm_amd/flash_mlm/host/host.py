@@ -111,25 +111,25 @@ def _wants_grad(*tensors) -> bool:
     return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
 
 
-def _backward_unsupported(q: torch.Tensor, d: int, entry) -> str | None:
+def _backward_unsupported(q: torch.Tensor, d: int, entry, is_mla: bool) -> str | None:
     """Why this call has no backward, or None."""
     if q.dtype not in (torch.bfloat16, torch.float16):
         return "the attention backward needs bf16 or fp16 inputs"
-    if d not in _BWD_HEAD_DIMS:
-        return "the attention backward supports head_dim 32, 64, 128 or 256"
+    if d not in _BWD_HEAD_DIMS and not (is_mla and d == 512):
+        return "the attention backward supports head_dim 32, 64, 128 or 256 (and a 512-wide MLA latent)"
     if entry is not None and entry.block_table is not None:
         return "paged KV contexts have no attention backward"
     return None
 
 
-def _run(impl, q, k, v, inference_cache, layer_id, prefill: bool):
+def _run(impl, q, k, v, inference_cache, layer_id, prefill: bool, is_mla: bool):
     """Run one attention call, through autograd when an input requires grad.  A call
     without a backward (see _backward_unsupported) returns its output without a graph,
     as the reference's kernels do, and warns that no gradient will flow."""
     kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
     if not _wants_grad(q, k, v, kc, vc):
         return impl()[0]
-    why = _backward_unsupported(q, int(q.shape[-1]), entry)
+    why = _backward_unsupported(q, int(q.shape[-1]), entry, is_mla)
     if why is not None:
         warnings.warn(f"flash_mlm: {why}; the output carries no gradient", stacklevel=3)
         return impl()[0]
@@ -380,7 +380,7 @@ def flash_attn_mlm(
             context_index=context_index,
         )
 
-    return _run(impl, q, k, v, inference_cache, layer_id, prefill)
+    return _run(impl, q, k, v, inference_cache, layer_id, prefill, is_mla)
 
 
 def _dense_impl(
@@ -551,7 +551,7 @@ def flash_attn_mlm_compressed(
             block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, context_index=context_index,
         )
 
-    return _run(impl, q, k, v, inference_cache, layer_id, prefill)
+    return _run(impl, q, k, v, inference_cache, layer_id, prefill, is_mla)
 
 
 def _compressed_impl(
@@ -766,7 +766,7 @@ def flash_attn_mlm_precompressed(
             layer_id, is_mla, context_batch_size, prefill, causal_query_seq_attn, context_index,
         )
 
-    return _run(impl, q, k, v, inference_cache, layer_id, prefill)
+    return _run(impl, q, k, v, inference_cache, layer_id, prefill, is_mla)
 
 
 def _precompressed_impl(

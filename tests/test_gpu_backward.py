@@ -311,3 +311,29 @@ def test_backward_mla_shared_tensor_and_strided_views(device):
                                          lengths, 0.2)
     for t, ref, name in zip(base, g[:3], ("dq", "dk", "dv")):
         _close(t.grad.transpose(1, 2), ref, name + " (strided)")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_mla_latent_512(causal, device):
+    """The 512-wide MLA latent (the BASELINE MLA shape) with a cached latent context."""
+    gen = torch.Generator().manual_seed(7800 + causal)
+    lengths = [70, 1, 0, 33]
+    B, H, N, D, dtype = len(lengths), 4, 72, 512, torch.bfloat16
+    scale = 1.0 / math.sqrt(D)
+    q = _leaf((B, H, N, D), dtype, device, gen)
+    k = _leaf((B, H, N, D), dtype, device, gen)
+    cache, kc, _, cu_kv, total = _packed_cache([65, 0, 130, 7], H=H, D=D, mla=True, dtype=dtype, device=device,
+                                               gen=gen)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, k, H, meta, scale, cache, 0, is_mla=True, block_n=64,
+                                    causal_query_seq_attn=causal)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    from flash_mlm import unpack_from_kernel
+    g = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(k), _np(unpack_from_kernel(dout, meta, H)), lengths, scale, is_mla=True,
+        causal_query_seq_attn=causal, k_cache=_np(kc), cu_seqlens_kv=cu_kv, total_context_len=total,
+        context_batch_size=B)
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk (latent)")
+    _close(kc.grad, g[3], "dk_cache (latent)")
