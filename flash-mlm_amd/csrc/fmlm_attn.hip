@@ -766,8 +766,6 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  const int32_t* cu = p.cu_seqlens_q;
-  const int B = p.B;
   // ---- Q fragments (B operand of S^T): lane (q + 16g), block qb, step kc, pre-scaled by
   // scale*log2(e) (one rounding to the input type) so that S comes out of the MFMAs in
   // log2 units

@@ -9,7 +9,6 @@ there is no CPU compute path, so these functions require device tensors.
 
 from __future__ import annotations
 
-import ctypes
 from dataclasses import dataclass
 from typing import TYPE_CHECKING
 

@@ -99,7 +99,6 @@ def test_paged_context_mla512_index_and_precompressed(device):
     np.testing.assert_allclose(_np(unpack_from_kernel(out, meta, H)), ref, atol=1e-2, rtol=1e-2)
     out_flat = flash_attn_mlm_compressed(q, k, k, H, meta, scale, flat, 0, is_mla=True, block_n=64, context_index=idx)
     assert torch.equal(out, out_flat)
-    from flash_mlm.host.host_utils import pack_for_kernel  # noqa: F401  (prepacked inputs below)
     qp = torch.cat([q[b, :, : lengths[b]] for b in range(B)], dim=1).reshape(-1, D).contiguous()
     kp = torch.cat([k[b, 0, : lengths[b]] for b in range(B)], dim=0).contiguous()
     pre = flash_attn_mlm_precompressed(
