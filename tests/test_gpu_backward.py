@@ -337,3 +337,39 @@ def test_backward_mla_latent_512(causal, device):
     _close(q.grad, g[0], "dq")
     _close(k.grad, g[1], "dk (latent)")
     _close(kc.grad, g[3], "dk_cache (latent)")
+
+
+def test_backward_through_projections_matches_torch(device):
+    """Training use: q, k, v are projections of activations (non-leaf tensors, permuted
+    views); the gradients of the projection weights and the activations through the HIP
+    attention match torch autograd of float32 per-sequence attention."""
+    gen = torch.Generator().manual_seed(7900)
+    lengths = [40, 64, 9]
+    B, H, N, D, dm, dtype = len(lengths), 2, 64, 64, 96, torch.bfloat16
+    x0 = (torch.randn((B, N, dm), generator=gen) * 0.5).to(dtype).to(device)
+    w0 = [(torch.randn((dm, H * D), generator=gen) / math.sqrt(dm)).to(dtype).to(device) for _ in range(3)]
+    y = torch.randn((H * sum(lengths), D), generator=gen).to(dtype).to(device)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+
+    x = x0.clone().requires_grad_()
+    w = [t.clone().requires_grad_() for t in w0]
+    q, k, v = ((x @ wi).view(B, N, H, D).permute(0, 2, 1, 3) for wi in w)  # [B, H, N, D] views
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, 0.125, block_n=64)
+    (out.float() * y.float()).sum().backward()
+
+    xf = x0.float().requires_grad_()
+    wf = [t.float().requires_grad_() for t in w0]
+    qf, kf, vf = ((xf @ wi).view(B, N, H, D).permute(0, 2, 1, 3) for wi in wf)
+    T = sum(lengths)
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    loss = 0.0
+    for b, L in enumerate(lengths):
+        for h in range(H):
+            # keys rounded like the kernel's bf16 inputs, math in fp32
+            qb, kb, vb = (t[b, h, :L].to(dtype).float() for t in (qf, kf, vf))
+            o = torch.softmax(qb @ kb.t() * 0.125, dim=-1) @ vb
+            loss = loss + (o * y[h * T + cu[b]: h * T + cu[b] + L].float()).sum()
+    loss.backward()
+    _close(x.grad, xf.grad.detach().cpu().numpy().astype(np.float64), "dx")
+    for i, name in enumerate(("dWq", "dWk", "dWv")):
+        _close(w[i].grad, wf[i].grad.detach().cpu().numpy().astype(np.float64), name)
