@@ -51,7 +51,7 @@ struct BwdCfg {
   // dkv kernel: 16-key blocks per wave, and whether the next query step is loaded ahead
   // (the register budget allows both only up to D = 64; at D = 128 two blocks spill,
   // which measured slower than one block with the load ahead)
-  static constexpr int KB = D <= 64 ? 2 : 1;
+  static constexpr int KB = (D <= 64 || D >= 512) ? 2 : 1;
   static constexpr bool DKV_PF = D <= 128;
   static constexpr int DKV_KEYS = kBwdNW * 16 * KB;  // keys per dkv workgroup
   static constexpr int QS = D >= 256 ? 32 : 64;   // query rows per dkv step (32-row groups)
@@ -230,6 +230,9 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
   const float c = p.scale * kLog2e;  // scores in log2 units
+  // MLA: V is K, so the K tile serves both products and no V tile is staged
+  const bool kv_same = C::MLA_ONLY || (p.flags & FMLM_FLAG_MLA);
+  const T* const Vt = kv_same ? Ks : Vs;
 
   const BSeg sc = ctx_seg(p, g, ctx_batch_of(p, b), h);  // context, then main keys
   const BSeg sm = main_seg(p, g, b, h);
@@ -337,14 +340,14 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     m_i[qb] = -INFINITY;
     l_i[qb] = 0.f;
   }
-  if (C::PF && nt > 0) fetch(0, true);
+  if (C::PF && nt > 0) fetch(0, !kv_same);
   for (int t = 0; t < nt; ++t) {
     const int nk = keys_in(t);
     __syncthreads();  // the previous tile's LDS reads are done
-    if (!C::PF) fetch(t, true);
-    stage(true);
+    if (!C::PF) fetch(t, !kv_same);
+    stage(!kv_same);
     __syncthreads();
-    if (C::PF && t + 1 < nt) fetch(t + 1, true);
+    if (C::PF && t + 1 < nt) fetch(t + 1, !kv_same);
     f32x4 s[C::NKB][QB], dp[C::NKB][QB];
     scores(s);
     // dP^T = V dO^T, same layout as S^T
@@ -356,7 +359,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     for (int kc = 0; kc < C::KC; ++kc)
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb) {
-        const v8 a = *(const v8*)(Vs + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
+        const v8 a = *(const v8*)(Vt + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = Mfma<T>::run(a, df[qb][kc], dp[kb][qb]);
       }
