@@ -373,3 +373,38 @@ def test_backward_through_projections_matches_torch(device):
     _close(x.grad, xf.grad.detach().cpu().numpy().astype(np.float64), "dx")
     for i, name in enumerate(("dWq", "dWk", "dWv")):
         _close(w[i].grad, wf[i].grad.detach().cpu().numpy().astype(np.float64), name)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_long_sequences_against_torch(causal, device):
+    """Thousands of keys per row (long sequences and contexts, many tiles accumulated per
+    gradient row) against torch autograd of float32 attention on the GPU."""
+    gen = torch.Generator().manual_seed(8000 + causal)
+    lengths = [2048, 1500]
+    ctx = [4096, 0] if not causal else [3000, 100]
+    B, H, N, D, dtype = len(lengths), 2, 2048, 128, torch.bfloat16
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    cache, kc, vc, cu_kv, total = _packed_cache(ctx, H=H, D=D, mla=False, dtype=dtype, device=device, gen=gen)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=causal)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+
+    qf, kf, vf, kcf, vcf = (x.detach().float().requires_grad_() for x in (q, k, v, kc, vc))
+    T = sum(lengths)
+    cu_q = np.concatenate([[0], np.cumsum(lengths)])
+    loss = 0.0
+    for b, L in enumerate(lengths):
+        for h in range(H):
+            Kc = kcf[h * total + cu_kv[b]: h * total + cu_kv[b + 1]]
+            Vc = vcf[h * total + cu_kv[b]: h * total + cu_kv[b + 1]]
+            seqs = range(b + 1) if causal else (b,)
+            Km = torch.cat([kf[s, h, : lengths[s]] for s in seqs])
+            Vm = torch.cat([vf[s, h, : lengths[s]] for s in seqs])
+            p = torch.softmax((qf[b, h, :L] @ torch.cat([Kc, Km]).t()) * scale, dim=-1)
+            loss = loss + ((p @ torch.cat([Vc, Vm])) * dout[h * T + cu_q[b]: h * T + cu_q[b] + L].float()).sum()
+    loss.backward()
+    for got, ref, name in ((q.grad, qf.grad, "dq"), (k.grad, kf.grad, "dk"), (v.grad, vf.grad, "dv"),
+                           (kc.grad, kcf.grad, "dkc"), (vc.grad, vcf.grad, "dvc")):
+        _close(got, ref.detach().cpu().numpy().astype(np.float64), name)
