@@ -59,10 +59,16 @@ class Case:
     causal: bool
     prefill: bool
     is_mla: bool
-    step: Callable[[], torch.Tensor]  # one pass of the hot path
+    call: Callable[[], torch.Tensor]  # the attention entry point of one step
     attention: Callable[[], None]  # the attention kernel alone (prepared ABI call)
     tensors: dict = field(default_factory=dict)  # inputs, kept for checks
     config: dict = field(default_factory=dict)
+    post: Callable[[torch.Tensor], torch.Tensor] | None = None  # the rest of the step
+
+    def step(self) -> torch.Tensor:
+        """One pass of the hot path: the attention call, then (packed paths) the unpack."""
+        out = self.call()
+        return self.post(out) if self.post is not None else out
 
     @property
     def flops(self) -> float:
@@ -157,7 +163,7 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
         return Case(
             cfg, "cfg1 dense flash_attn_mlm fp32 [2,8,128,64], no cache", dt, H, D, [N] * B, [0] * B,
             False, False, False,
-            step=lambda: fm.flash_attn_mlm(q, k, v, scale),
+            call=lambda: fm.flash_attn_mlm(q, k, v, scale),
             attention=out_plan[1],
             tensors=dict(q=q, k=k, v=v, scale=scale),
             config=dict(B=B, H=H, N=N, D=D, seed=seed),
@@ -175,7 +181,7 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
         return Case(
             cfg, "cfg2 dense flash_attn_mlm bf16 [8,16,512,64] + shared prefilled ctx 2048", dt, H, D,
             [N] * B, [C] * B, False, False, False,
-            step=lambda: fm.flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0),
+            call=lambda: fm.flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0),
             attention=plan,
             tensors=dict(q=q, k=k, v=v, k0=k0, v0=v0, scale=scale, cache=cache),
             config=dict(B=B, H=H, N=N, D=D, context=C, seed=seed, unique_ctx_tokens=C),
@@ -223,9 +229,8 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
         meta = cache.packing.get_pack_metadata(lq.to(device=device, dtype=torch.int32), N=N, block_n=bn)
         kw = dict(is_mla=mla, block_n=bn, causal_query_seq_attn=causal)
 
-        def step():
-            out = fm.flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, prefill=prefill, **kw)
-            return fm.unpack_from_kernel(out, meta, H)
+        def call():
+            return fm.flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, prefill=prefill, **kw)
 
         # the attention launch alone; prefill replaces the layer entry, so plan it on a copy
         plan_cache = cache
@@ -245,7 +250,8 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
             cfg, names[cfg] + (" (prefill=True)" if prefill else "") + (f" ({variant} KV context)" if variant.startswith("paged") else ""),
             dt, H, D,
             [int(x) for x in lq], lengths_ctx, causal, prefill, mla,
-            step=step,
+            call=call,
+            post=lambda out: fm.unpack_from_kernel(out, meta, H),
             attention=plan,
             tensors=dict(q=q, k=k, v=v, k_cache=k_cache, v_cache=v_cache, cu_kv=cu_kv, meta=meta,
                          scale=scale, cache=cache, cbs=cbs, Tc=Tc),
@@ -255,15 +261,25 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
     raise ValueError(f"unknown config {cfg}")
 
 
-def _time_steps(fn, steps: int, warmup: int) -> float:
+def _time_steps(case: "Case", steps: int, warmup: int) -> tuple[float, float]:
+    """(ms per step, mean attention-call ms): K steps back to back between two device
+    synchronisations, with HIP events on the launch stream around the attention call of
+    every timed step (the kernel, plus the split merge where there is one)."""
     for _ in range(warmup):
-        fn()
+        case.step()
+    stream = torch.cuda.current_stream()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        fn()
+    for e0, e1 in events:
+        e0.record(stream)
+        out = case.call()
+        e1.record(stream)
+        if case.post is not None:
+            case.post(out)
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return ms, sum(e0.elapsed_time(e1) for e0, e1 in events) / steps
 
 
 FLUSH_BYTES = 512 << 20  # > the 256 MB MALL (and the 4 MB L2s)
@@ -527,11 +543,12 @@ def main() -> None:
         print(f"[bench] profiled {args.steps} attention launches", file=sys.stderr, flush=True)
         return
 
-    ms = _time_steps(case.step, args.steps, args.warmup)
-    print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step", file=sys.stderr, flush=True)
-    kms, kmean = _kernel_ms(case.attention, args.kernel_reps)
-    print(f"[bench] attention kernel: median {kms:.4f} ms, mean {kmean:.4f} ms over {args.kernel_reps} "
-          f"flushed launches", file=sys.stderr, flush=True)
+    ms, kms = _time_steps(case, args.steps, args.warmup)
+    print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step, attention call {kms:.4f} ms (mean)",
+          file=sys.stderr, flush=True)
+    fms, fmean = _kernel_ms(case.attention, args.kernel_reps)
+    print(f"[bench] attention kernel with cold caches: median {fms:.4f} ms, mean {fmean:.4f} ms over "
+          f"{args.kernel_reps} flushed launches", file=sys.stderr, flush=True)
 
     F = case.flops
     value = F / (ms * 1e-3) / 1e12
@@ -545,9 +562,13 @@ def main() -> None:
         "frac": round(k_tflops / peak, 5),
         "traffic": None if traffic is None else round(traffic["bytes"]),
         "kernel_ms": round(kms, 5),
-        "kernel_ms_mean": round(kmean, 5),
-        "kernel_timing": f"HIP events on the launch stream, median of {args.kernel_reps} launches, "
-                         "L2/MALL flushed (512 MiB write) before each",
+        "kernel_timing": f"HIP events on the launch stream around the attention call of each of the "
+                         f"{args.steps} timed steps (mean)",
+        "kernel_ms_cold": round(fms, 5),
+        "kernel_ms_cold_mean": round(fmean, 5),
+        "kernel_cold_timing": f"the same kernel launched alone {args.kernel_reps} times, L2/MALL flushed "
+                              "(512 MiB write) before each (median)",
+        "frac_cold": round(F / (fms * 1e-3) / 1e12 / peak, 5),
         "algorithmic_bytes": case.attention_bytes,
     }
     if traffic is not None:
