@@ -80,7 +80,21 @@ struct BSeg {
   int64_t kbase, vbase, ksn, vsn;
   int64_t dkbase, dvbase, dksn, dvsn;
   int n;
+  // paged context: key j is row j % FMLM_PAGE_ROWS of page pages[j / FMLM_PAGE_ROWS]
+  // (ids clamped to the pool), base + page * page_elems + row * sn; the gradients are
+  // float32 and accumulated atomically (a page may serve several context batches)
+  const int32_t* pages;
+  int64_t page_elems;
+  int npool, ntab;
 };
+
+// element offset of key `key` of a segment, from `base` with row stride `sn`
+FMLM_DEV int64_t key_elem(const BSeg& s, int64_t base, int64_t sn, int key) {
+  if (!s.pages) return base + (int64_t)key * sn;
+  int pg = s.pages[min(key / FMLM_PAGE_ROWS, max(s.ntab - 1, 0))];
+  pg = min(max(pg, 0), max(s.npool - 1, 0));
+  return base + (int64_t)pg * s.page_elems + (int64_t)(key % FMLM_PAGE_ROWS) * sn;
+}
 
 // context rows of context batch cb (mlm_kernel_impl.py:297-313 packed, :132-141 dense)
 FMLM_DEV BSeg ctx_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int cb, int h) {
@@ -93,7 +107,18 @@ FMLM_DEV BSeg ctx_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int c
   s.v = (const char*)(mla ? p.k_ctx : p.v_ctx);
   s.dk = (char*)g.dk_ctx;
   s.dv = (char*)(mla ? g.dk_ctx : g.dv_ctx);
-  s.kbase = s.vbase = (int64_t)cb * p.c_sb + (int64_t)h * p.c_sh + (int64_t)c0 * p.c_sn;
+  s.pages = nullptr;
+  s.page_elems = 0;
+  s.npool = s.ntab = 0;
+  if (p.ctx_block_table) {  // paged: rows come from the batch's pages
+    s.pages = p.ctx_block_table + (int64_t)cb * p.ctx_pages_per_batch;
+    s.page_elems = p.ctx_page_stride;
+    s.npool = p.ctx_rows;
+    s.ntab = p.ctx_pages_per_batch;
+    s.kbase = s.vbase = (int64_t)h * p.c_sh;
+  } else {
+    s.kbase = s.vbase = (int64_t)cb * p.c_sb + (int64_t)h * p.c_sh + (int64_t)c0 * p.c_sn;
+  }
   s.dkbase = s.dvbase = s.kbase;
   s.ksn = s.vsn = s.dksn = s.dvsn = p.c_sn;
   return s;
@@ -107,6 +132,9 @@ FMLM_DEV BSeg main_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int 
   const int64_t v_sb = mla ? p.k_sb : p.v_sb, v_sh = mla ? p.k_sh : p.v_sh, v_sn = mla ? p.k_sn : p.v_sn;
   const int64_t dv_sb = mla ? g.dk_sb : g.dv_sb, dv_sh = mla ? g.dk_sh : g.dv_sh, dv_sn = mla ? g.dk_sn : g.dv_sn;
   BSeg s;
+  s.pages = nullptr;
+  s.page_elems = 0;
+  s.npool = s.ntab = 0;
   s.k = (const char*)p.k;
   s.v = (const char*)(mla ? p.k : p.v);
   s.dk = (char*)g.dk;
@@ -284,18 +312,19 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     const int j0 = (m ? t - nt0 : t) * kBwdBK, n = m ? sm.n : sc.n;
     const char* kp = m ? sm.k : sc.k;
     const char* vp = m ? sm.v : sc.v;
-    const int64_t kb = m ? sm.kbase : sc.kbase, vb = m ? sm.vbase : sc.vbase;
     const int64_t ksn = m ? sm.ksn : sc.ksn, vsn = m ? sm.vsn : sc.vsn;
+    // row 0 of the tile (a paged context tile is one page)
+    const int64_t kt = m ? sm.kbase + (int64_t)j0 * ksn : key_elem(sc, sc.kbase, ksn, j0);
+    const int64_t vt = m ? sm.vbase + (int64_t)j0 * vsn : key_elem(sc, sc.vbase, vsn, j0);
 #pragma unroll
     for (int li = 0; li < LPT; ++li) {
       const int it = tid + li * C::NT;
       const int row = it / C::C8, c8 = it % C::C8;
-      const int key = j0 + row;
       kreg[li] = u32x4{0u, 0u, 0u, 0u};
       vreg[li] = kreg[li];
-      if (key < n) {
-        kreg[li] = ld16(kp, kb + (int64_t)key * ksn + c8 * 8);
-        if (with_v) vreg[li] = ld16(vp, vb + (int64_t)key * vsn + c8 * 8);
+      if (j0 + row < n) {
+        kreg[li] = ld16(kp, kt + (int64_t)row * ksn + c8 * 8);
+        if (with_v) vreg[li] = ld16(vp, vt + (int64_t)row * vsn + c8 * 8);
       }
     }
   };
@@ -536,8 +565,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     for (int kc = 0; kc < C::KC; ++kc) {
       u32x4 rk = u32x4{0u, 0u, 0u, 0u}, rv = rk;
       if (kok[kb]) {
-        rk = ld16(s.k, s.kbase + (int64_t)key[kb] * s.ksn + kc * 32 + gq * 8);
-        if (!mla) rv = ld16(s.v, s.vbase + (int64_t)key[kb] * s.vsn + kc * 32 + gq * 8);
+        rk = ld16(s.k, key_elem(s, s.kbase, s.ksn, key[kb]) + kc * 32 + gq * 8);
+        if (!mla) rv = ld16(s.v, key_elem(s, s.vbase, s.vsn, key[kb]) + kc * 32 + gq * 8);
       }
       kf[kb][kc] = __builtin_bit_cast(v8, rk);
       vf[kb][kc] = mla ? kf[kb][kc] : __builtin_bit_cast(v8, rv);
@@ -696,7 +725,23 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         k4[r] = (T)dkt[kb][db][r];
-        v4[r] = C::MLA_ONLY ? (T)0.f : (T)dvt[kb][db][r];
+        if constexpr (C::MLA_ONLY) {
+          v4[r] = (T)0.f;
+        } else {
+          v4[r] = (T)dvt[kb][db][r];
+        }
+      }
+      if (s.pages) {  // float32 gradients, added atomically
+        float* dkf = (float*)s.dk + key_elem(s, s.dkbase, s.dksn, key[kb]) + db * 16 + gq * 4;
+        float* dvf = (float*)s.dv + key_elem(s, s.dvbase, s.dvsn, key[kb]) + db * 16 + gq * 4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) atomicAdd(dkf + r, dkt[kb][db][r]);
+        if constexpr (!C::MLA_ONLY) {
+          if (!mla)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) atomicAdd(dvf + r, dvt[kb][db][r]);
+        }
+        continue;
       }
       *(u32x2*)(s.dk + (s.dkbase + (int64_t)key[kb] * s.dksn + db * 16 + gq * 4) * 2) = *(const u32x2*)k4;
       if (!mla)
@@ -771,7 +816,8 @@ static int check_bwd(const fmlm_attn_params& p, const fmlm_attn_grads& g, BwdFns
   if (p.D == 512 && !mla) return FMLM_E_HEAD_DIM;  // the 512-wide head dim is the MLA latent
   const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
   if (causal && (!p.cu_seqlens_q || p.kv_layout != FMLM_LAYOUT_PACKED)) return FMLM_E_ARG;
-  if (p.ctx_block_table) return FMLM_E_ARG;  // paged contexts: forward only
+  if (p.ctx_block_table && (p.ctx_pages_per_batch < 0 || p.ctx_rows < 1 || p.ctx_page_stride < 0))
+    return FMLM_E_ARG;
   // keys shared by all heads must be shared by K and V alike
   if (!mla && ((p.k_sh == 0) != (p.v_sh == 0))) return FMLM_E_ARG;
   if (!row_ok(p.q, p.q_sb, p.q_sh, p.q_sn) || !row_ok(p.o, p.o_sb, p.o_sh, p.o_sn) ||
@@ -835,7 +881,12 @@ extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* 
   if (e != hipSuccess) return (int)e;
   // 2. dK / dV, context keys then main keys in one launch
   const int64_t munits = causal ? ((int64_t)p.total_q + f.dkv_keys - 1) / f.dkv_keys : (int64_t)p.total_q / f.dkv_keys + p.B;
-  const int64_t crows = !ctx_grads ? 0 : (p.cu_seqlens_kv ? p.ctx_rows : (int64_t)n_ctx * p.ctx_len);
+  // context rows over all batches: a packed context's rows per head, a paged one's pages
+  // per batch (ctx_rows counts pool pages there), or the uniform length per batch
+  const int64_t crows = !ctx_grads                ? 0
+                        : p.ctx_block_table       ? (int64_t)n_ctx * p.ctx_pages_per_batch * FMLM_PAGE_ROWS
+                        : p.cu_seqlens_kv         ? (int64_t)p.ctx_rows
+                                                  : (int64_t)n_ctx * p.ctx_len;
   const int64_t cunits = ctx_grads ? crows / f.dkv_keys + n_ctx : 0;
   if (munits + cunits > 0x7fffffff) return FMLM_E_ARG;
   const unsigned kheads = (p.k_sh == 0 && (n_ctx == 0 || p.c_sh == 0)) ? 1u : (unsigned)p.H;

@@ -117,8 +117,6 @@ def _backward_unsupported(q: torch.Tensor, d: int, entry, is_mla: bool) -> str |
         return "the attention backward needs bf16 or fp16 inputs"
     if d not in _BWD_HEAD_DIMS and not (is_mla and d == 512):
         return "the attention backward supports head_dim 32, 64, 128 or 256 (and a 512-wide MLA latent)"
-    if entry is not None and entry.block_table is not None:
-        return "paged KV contexts have no attention backward"
     return None
 
 
@@ -171,6 +169,9 @@ def _attention_backward(plan: AttnLaunch, out: torch.Tensor, dout: torch.Tensor,
         mla = bool(plan.params.flags & _lib.FLAG_MLA)
         dk = _unpack_kv_grad(plan.lib, dk, plan, mla)
         dv = None if mla else _unpack_kv_grad(plan.lib, dv, plan, mla)
+    if plan.params.ctx_block_table:  # float32 accumulation -> the pool's dtype
+        dkc = None if dkc is None else dkc.to(out.dtype)
+        dvc = None if dvc is None else dvc.to(out.dtype)
     return dq, dk, dv, dkc, dvc
 
 
@@ -203,10 +204,13 @@ def _backward_args(plan: AttnLaunch, out: torch.Tensor, dout: torch.Tensor, want
         g.dv = dv.data_ptr()
     dkc = dvc = None
     if want_ctx and not prefill and k_ctx is not None and k_ctx.numel():
-        dkc = torch.zeros_like(k_ctx)
+        # a paged context's gradient is accumulated in float32 (a page can serve several
+        # context batches); _attention_backward rounds it to the cache dtype
+        acc = torch.float32 if p.ctx_block_table else k_ctx.dtype
+        dkc = torch.zeros(k_ctx.shape, dtype=acc, device=k_ctx.device)
         g.dk_ctx = dkc.data_ptr()
         if not mla:
-            dvc = torch.zeros_like(v_ctx)
+            dvc = torch.zeros(v_ctx.shape, dtype=acc, device=v_ctx.device)
             g.dv_ctx = dvc.data_ptr()
     nbytes = int(lib.fmlm_attn_bwd_workspace_bytes(p))
     _lib.check(nbytes if nbytes < 0 else 0, "fmlm_attn_bwd_workspace_bytes")

@@ -237,9 +237,12 @@ FMLM_API int fmlm_attn_fwd(const fmlm_attn_params* p, void* stream);
  *           of K and of V (V is K) and dv is unused.  Keys with head stride 0 (the MLA
  *           latent) are shared by all heads, and so is their gradient row (dk_sh = 0).
  *   dk_ctx, dv_ctx  the context's gradient, laid out like k_ctx / v_ctx (c_sb, c_sh,
- *           c_sn), or NULL to skip it: rows [c0, c1) of every context batch.
+ *           c_sn), or NULL to skip it: rows [c0, c1) of every context batch.  With a
+ *           paged context (ctx_block_table) they are float32 buffers laid out like the
+ *           pool, zeroed by the caller, that the kernel adds into atomically: a page used
+ *           by several context batches receives the sum of their gradients.
  * Rows not listed are not written.  dout is laid out like o (o_layout).
- * bf16 / f16, D in {32, 64, 128, 256}, or 512 with FMLM_FLAG_MLA; contiguous (non-paged) contexts; with
+ * bf16 / f16, D in {32, 64, 128, 256}, or 512 with FMLM_FLAG_MLA; with
  * FMLM_FLAG_CAUSAL_SEQ the main keys must be packed (kv_layout PACKED).
  * workspace: fmlm_attn_bwd_workspace_bytes(p) bytes (per-row softmax statistics and the
  *           tile tables of the two kernels).

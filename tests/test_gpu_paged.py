@@ -135,16 +135,67 @@ def test_paged_context_longer_than_64_pages(mla, device):
     assert torch.equal(out, out_flat)
 
 
-def test_paged_context_has_no_backward(device):
-    cache = _paged([70, 10], H=2, D=64, mla=False, dtype=torch.bfloat16, device=device)[0]
-    lengths = [5, 9]
-    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), 9, block_n=64)
-    q = torch.randn((2, 2, 9, 64), device=device).to(torch.bfloat16).requires_grad_()
-    with pytest.warns(UserWarning, match="paged KV contexts have no attention backward"):
-        out = flash_attn_mlm_compressed(q, q.detach(), q.detach(), 2, meta, 0.1, cache, 0, block_n=64)
-    assert out.grad_fn is None
-    with torch.no_grad():  # the forward alone is fine
-        flash_attn_mlm_compressed(q, q, q, 2, meta, 0.1, cache, 0, block_n=64)
+def _scatter_to_pages(grad_ctx, block_table, lens, H_kv, P, D):
+    """Inverse of gather_pages for gradients: contiguous context rows [H_kv*T, D] added
+    into a pool [H_kv, P, PAGE, D] (rows of a page used by several batches sum)."""
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    pool = np.zeros((H_kv, P, PAGE, D))
+    for c, n in enumerate(lens):
+        for j in range(n):
+            pool[:, int(block_table[c][j // PAGE]), j % PAGE] += grad_ctx[np.arange(H_kv) * T + cu[c] + j]
+    return pool
+
+
+@pytest.mark.parametrize("mla", [False, True])
+@pytest.mark.parametrize("shared_page", [False, True])
+def test_paged_context_backward(mla, shared_page, device):
+    """Backward over a paged context (float32 accumulation of the pool gradient): q/k/v
+    gradients equal those of the same rows stored contiguously, and the pool gradient is
+    the oracle's context gradient added back into the pages, pages used by two context
+    batches (a shared prefix) receiving both batches' gradients."""
+    g = torch.Generator().manual_seed(6400 + 2 * mla + shared_page)
+    H, D, dtype = 2, 128 if not mla else 64, torch.bfloat16
+    h_kv = 1 if mla else H
+    lens = [130, 70, 64]
+    P = 9
+    bt = torch.tensor([[3, 5, 0], [3, 7, -1], [8, -1, -1]] if shared_page else [[3, 5, 0], [1, 7, -1], [8, -1, -1]],
+                      dtype=torch.int32)
+    kp = (torch.randn((h_kv, P, PAGE, D), generator=g) * 0.5).to(dtype).to(device).requires_grad_()
+    vp = None if mla else (torch.randn((h_kv, P, PAGE, D), generator=g) * 0.5).to(dtype).to(device).requires_grad_()
+    cache = InferenceCache()
+    cache.prefill_paged_kv_cache(0, k_pages=kp, v_pages=vp, block_table=bt.to(device),
+                                 context_lens=torch.tensor(lens, dtype=torch.int32), is_mla=mla, num_heads=H,
+                                 head_dim=D)
+    lengths = [50, 33, 64]
+    B, N = len(lengths), 64
+    q, k, v = ((torch.randn((B, H, N, D), generator=g) * 0.5).to(dtype).to(device).requires_grad_() for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, k if mla else v, H, meta, 0.125, cache, 0, is_mla=mla, block_n=64)
+    dout = torch.randn(out.shape, generator=g).to(dtype).to(device)
+    out.backward(dout)
+
+    kc, cu = pack_ref.gather_pages(_np(kp).transpose(1, 0, 2, 3), bt.numpy(), lens)
+    vc = None if mla else pack_ref.gather_pages(_np(vp).transpose(1, 0, 2, 3), bt.numpy(), lens)[0]
+    ref = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(k if mla else v), _np(unpack_from_kernel(dout, meta, H)), lengths, 0.125, is_mla=mla,
+        k_cache=kc, v_cache=vc, cu_seqlens_kv=cu, total_context_len=int(cu[-1]), context_batch_size=B)
+
+    def close(got, want, what):
+        scale = float(np.abs(want).max())
+        assert scale > 0, what
+        err = float(np.abs(_np(got) - want).max())
+        assert err <= 2e-2 * scale, f"{what}: max err {err:.3e} (ref max {scale:.3e})"
+
+    close(q.grad, ref[0], "dq")
+    close(k.grad, ref[1], "dk")
+    if not mla:
+        close(v.grad, ref[2], "dv")
+    close(kp.grad, _scatter_to_pages(ref[3], bt.numpy(), lens, h_kv, P, D), "d k_pages")
+    if not mla:
+        close(vp.grad, _scatter_to_pages(ref[4], bt.numpy(), lens, h_kv, P, D), "d v_pages")
+    unused = sorted(set(range(P)) - {int(x) for row in bt.tolist() for x in row if x >= 0})
+    assert torch.count_nonzero(kp.grad[:, unused]) == 0  # pages no batch uses get nothing
 
 
 def test_paged_context_errors(device):
