@@ -1447,12 +1447,13 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
 // ---------------------------------------------------------------------------
 template <int D>
 struct SimtCfg {
-  static constexpr int TPR = D > 64 ? D / 64 : 1;  // threads per query row
-  static constexpr int DPT = D / TPR;              // dims per thread
-  static constexpr int RPW = 64;                   // query rows per workgroup
-  static constexpr int NT = RPW * TPR;
-  static constexpr int BKS = (4096 / D) < 8 ? 8 : ((4096 / D) > 64 ? 64 : (4096 / D));
+  static constexpr int TPR = D / 4 < 16 ? D / 4 : 16;  // threads per query row
+  static constexpr int DPT = D / TPR;                   // dims per thread (a multiple of 4)
+  static constexpr int NT = 256;
+  static constexpr int RPW = NT / TPR;                  // query rows per workgroup
+  static constexpr int BKS = 4096 / D < 64 ? 4096 / D : 64;  // keys per LDS tile
   static constexpr int LDS_BYTES = 2 * BKS * D * 4;
+  static_assert(DPT % 4 == 0 && (TPR & (TPR - 1)) == 0, "simt tiling");
 };
 
 template <typename T>
@@ -1460,6 +1461,20 @@ FMLM_DEV float to_f(T x) {
   return (float)x;
 }
 
+// four consecutive elements as floats
+template <typename T>
+FMLM_DEV float4 load4(const T* p) {
+  return float4{to_f(p[0]), to_f(p[1]), to_f(p[2]), to_f(p[3])};
+}
+template <>
+FMLM_DEV float4 load4<float>(const float* p) {
+  return *(const float4*)p;
+}
+
+// fp32 (and head dims without an MFMA instantiation): TPR threads per query row, each
+// holding DPT dims of q and o; a row's partial dot products meet through xor shuffles
+// inside its TPR lanes.  K/V tiles of BKS keys are staged as fp32 in LDS and read as
+// float4 (a row's lanes cover one contiguous key row).
 template <typename T, int D>
 __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
     const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
@@ -1482,9 +1497,13 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
   const bool ok = row < w.qcount;
   const T* qp = (const T*)p.q + w.q_row0 + (int64_t)row * w.q_sn + d0;
 #pragma unroll
-  for (int d = 0; d < C::DPT; ++d) {
-    q[d] = ok ? to_f(qp[d]) : 0.f;
-    o[d] = 0.f;
+  for (int d = 0; d < C::DPT; d += 4) {
+    const float4 v4 = ok ? load4(qp + d) : float4{0.f, 0.f, 0.f, 0.f};
+    q[d] = v4.x;
+    q[d + 1] = v4.y;
+    q[d + 2] = v4.z;
+    q[d + 3] = v4.w;
+    o[d] = o[d + 1] = o[d + 2] = o[d + 3] = 0.f;
   }
   float m_i = -INFINITY, l_i = 0.f;
 
@@ -1493,17 +1512,15 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
     for (int j0 = 0; j0 < s.n; j0 += C::BKS) {
       const int nk = min(C::BKS, s.n - j0);
       __syncthreads();
-      for (int e = tid; e < C::BKS * D; e += C::NT) {
+      for (int e = tid * 4; e < C::BKS * D; e += C::NT * 4) {
         const int kk = e / D, d = e % D;
-        float kv = 0.f, vv = 0.f;
+        float4 kv = float4{0.f, 0.f, 0.f, 0.f}, vv = kv;
         if (kk < nk) {
-          const int64_t kr = seg_row(s, j0 + kk, false, cu, B);
-          const int64_t vr = seg_row(s, j0 + kk, true, cu, B);
-          kv = to_f(((const T*)s.k)[kr + d]);
-          vv = to_f(((const T*)s.v)[vr + d]);
+          kv = load4((const T*)s.k + seg_row(s, j0 + kk, false, cu, B) + d);
+          vv = load4((const T*)s.v + seg_row(s, j0 + kk, true, cu, B) + d);
         }
-        Kf[e] = kv;
-        Vf[e] = vv;
+        *(float4*)(Kf + e) = kv;
+        *(float4*)(Vf + e) = vv;
       }
       __syncthreads();
       float sc[C::BKS];
@@ -1512,7 +1529,10 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
       for (int kk = 0; kk < C::BKS; ++kk) {
         float acc = 0.f;
 #pragma unroll
-        for (int d = 0; d < C::DPT; ++d) acc += q[d] * Kf[kk * D + d0 + d];
+        for (int d = 0; d < C::DPT; d += 4) {
+          const float4 k4 = *(const float4*)(Kf + kk * D + d0 + d);
+          acc += q[d] * k4.x + q[d + 1] * k4.y + q[d + 2] * k4.z + q[d + 3] * k4.w;
+        }
 #pragma unroll
         for (int off = 1; off < C::TPR; off <<= 1) acc += __shfl_xor(acc, off);
         sc[kk] = kk < nk ? acc * c : -INFINITY;
@@ -1530,7 +1550,13 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
         l_i += pv;
         const float pr = to_f((T)pv);
 #pragma unroll
-        for (int d = 0; d < C::DPT; ++d) o[d] += pr * Vf[kk * D + d0 + d];
+        for (int d = 0; d < C::DPT; d += 4) {
+          const float4 v4 = *(const float4*)(Vf + kk * D + d0 + d);
+          o[d] += pr * v4.x;
+          o[d + 1] += pr * v4.y;
+          o[d + 2] += pr * v4.z;
+          o[d + 3] += pr * v4.w;
+        }
       }
     }
   }
