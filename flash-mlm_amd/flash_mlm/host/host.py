@@ -123,15 +123,18 @@ def _backward_unsupported(q: torch.Tensor, d: int, entry, is_mla: bool) -> str |
 def _run(impl, q, k, v, inference_cache, layer_id, prefill: bool, is_mla: bool):
     """Run one attention call, through autograd when an input requires grad.  A call
     without a backward (see _backward_unsupported) returns its output without a graph,
-    as the reference's kernels do, and warns that no gradient will flow."""
+    as the reference's kernels do, and warns that no gradient will flow.  ``impl(owned)``
+    runs the forward; ``owned`` asks it to keep every tensor the kernel reads in buffers
+    of its own rather than the cache's reusable packing buffers, which a later call may
+    overwrite before this call's backward runs."""
     kc, vc, entry = _cache_tensors(inference_cache, layer_id, prefill)
     if not _wants_grad(q, k, v, kc, vc):
-        return impl()[0]
+        return impl(False)[0]
     why = _backward_unsupported(q, int(q.shape[-1]), entry, is_mla)
     if why is not None:
         warnings.warn(f"flash_mlm: {why}; the output carries no gradient", stacklevel=3)
-        return impl()[0]
-    return _Attention.apply(impl, q, k, v, kc, vc)
+        return impl(False)[0]
+    return _Attention.apply(lambda: impl(True), q, k, v, kc, vc)
 
 
 class _Attention(torch.autograd.Function):
@@ -378,7 +381,7 @@ def flash_attn_mlm(
     layer's new context with context_batch_size = B.  ``context_index`` (int [B], an
     extension) maps sequence b to cached context batch ``context_index[b]``.
     """
-    def impl():
+    def impl(owned: bool):
         return _dense_impl(
             q, k, v, scale, inference_cache, layer_id, is_mla, context_batch_size, prefill,
             context_index=context_index,
@@ -549,10 +552,11 @@ def flash_attn_mlm_compressed(
     context_batch_size = B) before the attention runs.  ``context_index`` (int [B], an
     extension) maps sequence b to cached context batch ``context_index[b]`` instead.
     """
-    def impl():
+    def impl(owned: bool):
         return _compressed_impl(
             q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
             block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, context_index=context_index,
+            owned_buffers=owned,
         )
 
     return _run(impl, q, k, v, inference_cache, layer_id, prefill, is_mla)
@@ -561,6 +565,7 @@ def flash_attn_mlm_compressed(
 def _compressed_impl(
     q, k, v, num_heads, q_meta, scale, inference_cache, layer_id, is_mla, context_batch_size,
     block_m, block_n, auto_tune_tiles, prefill, causal_query_seq_attn, run=True, context_index=None,
+    owned_buffers=False,
 ):
     """Body of :func:`flash_attn_mlm_compressed`; returns (out, prepared launch or None)."""
     b, h, n, d = validate_qkv_same_shape_rank4(q, k, v, error_prefix="q/k/v")
@@ -670,7 +675,7 @@ def _compressed_impl(
             kv_heads = 1 if is_mla else num_heads
 
             def alloc(name: str) -> torch.Tensor:
-                if inference_cache is None:
+                if inference_cache is None or owned_buffers:
                     return torch.empty((kv_heads * T, d), dtype=k.dtype, device=k.device)
                 return inference_cache.packing.get_2d(name, kv_heads * T, d, dtype=k.dtype, device=k.device)
 
@@ -764,7 +769,7 @@ def flash_attn_mlm_precompressed(
     layer's context after the launch.
     """
 
-    def impl():
+    def impl(owned: bool):
         return _precompressed_impl(
             q, k, v, num_heads, total_q_len, cu_seqlens_q, batch_ids_q, q_tile_starts_q, scale, inference_cache,
             layer_id, is_mla, context_batch_size, prefill, causal_query_seq_attn, context_index,

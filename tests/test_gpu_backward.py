@@ -408,3 +408,28 @@ def test_backward_long_sequences_against_torch(causal, device):
     for got, ref, name in ((q.grad, qf.grad, "dq"), (k.grad, kf.grad, "dk"), (v.grad, vf.grad, "dv"),
                            (kc.grad, kcf.grad, "dkc"), (vc.grad, vcf.grad, "dvc")):
         _close(got, ref.detach().cpu().numpy().astype(np.float64), name)
+
+
+def test_backward_two_causal_calls_sharing_a_cache(device):
+    """Two layers' causal calls through one InferenceCache, then one backward: the second
+    forward must not overwrite the packed K/V the first call's backward reads (the
+    cache's reusable packing buffers are not used for calls under autograd)."""
+    gen = torch.Generator().manual_seed(8100)
+    lengths = [40, 25, 64]
+    B, H, N, D, dtype = len(lengths), 2, 64, 64, torch.bfloat16
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    cache = InferenceCache()
+    calls = []
+    for layer in range(2):
+        q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+        out = flash_attn_mlm_compressed(q, k, v, H, meta, 0.2, cache, layer, block_n=64, causal_query_seq_attn=True)
+        dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+        calls.append((q, k, v, out, dout))
+    sum((out.float() * dout.float()).sum() for _, _, _, out, dout in calls).backward()
+    from flash_mlm import unpack_from_kernel
+    for layer, (q, k, v, _, dout) in enumerate(calls):
+        g = ar.mlm_attention_packed_backward(_np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)),
+                                             lengths, 0.2, causal_query_seq_attn=True)
+        _close(q.grad, g[0], f"layer {layer} dq")
+        _close(k.grad, g[1], f"layer {layer} dk")
+        _close(v.grad, g[2], f"layer {layer} dv")
