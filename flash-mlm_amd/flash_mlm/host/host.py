@@ -146,7 +146,8 @@ class _Attention(torch.autograd.Function):
     def forward(ctx, impl, q, k, v, k_cache, v_cache):
         out, plan = impl()
         ctx.plan = plan
-        ctx.save_for_backward(out, q, k, v)
+        # saved so that autograd rejects a backward after any of them changed in place
+        ctx.save_for_backward(out, q, k, v, k_cache, v_cache)
         return out
 
     @staticmethod

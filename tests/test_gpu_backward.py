@@ -433,3 +433,20 @@ def test_backward_two_causal_calls_sharing_a_cache(device):
         _close(q.grad, g[0], f"layer {layer} dq")
         _close(k.grad, g[1], f"layer {layer} dk")
         _close(v.grad, g[2], f"layer {layer} dv")
+
+
+def test_backward_rejects_inputs_changed_in_place(device):
+    """The backward reads the tensors of the forward call: changing q or the cached
+    context in place between forward and backward is an autograd error."""
+    gen = torch.Generator().manual_seed(8200)
+    lengths = [20, 9]
+    B, H, N, D, dtype = 2, 2, 20, 64, torch.bfloat16
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    for target in ("q", "cache"):
+        q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+        cache, kc, vc, _, _ = _packed_cache([10, 5], H=H, D=D, mla=False, dtype=dtype, device=device, gen=gen)
+        out = flash_attn_mlm_compressed(q, k, v, H, meta, 0.2, cache, 0, block_n=64)
+        with torch.no_grad():
+            (q if target == "q" else kc).mul_(2.0)
+        with pytest.raises(RuntimeError, match="modified by an inplace operation"):
+            out.sum().backward()
