@@ -236,6 +236,93 @@ __global__ __launch_bounds__(kScanThreads) void bwd_units_kernel(const fmlm_attn
 }
 
 // ---------------------------------------------------------------------------
+// Key units of the dK / dV kernels: unit blockIdx.x of head blockIdx.y is a tile of
+// `keys` keys, context tiles first (unit table c), then main-key tiles (per sequence from
+// unit table k, or with CAUSAL tiles of the causal token range).
+// ---------------------------------------------------------------------------
+struct KeyUnit {
+  BSeg s;
+  int slot, j0;       // sequence / context batch, first key of the tile
+  int b_lo, b_hi;     // sequences whose queries may attend to these keys
+  bool is_ctx;
+  bool causal_main;   // main keys of the causal token range (key j seen by b iff j < cu[b+1])
+  bool shared;        // key rows shared by all heads (head stride 0)
+};
+
+template <bool CAUSAL>
+FMLM_DEV bool resolve_key_unit(const fmlm_attn_params& p, const fmlm_attn_grads& g, int n_ctx, int keys,
+                               KeyUnit& k) {
+  const int32_t* cu = p.cu_seqlens_q;
+  const int kh = blockIdx.y;
+  const UnitTables ut = unit_tables(p, g);
+  const int n_main = CAUSAL ? (min(cu[p.B], p.total_q) + keys - 1) / keys : ut.k[p.B];
+  const int n_cunits = n_ctx > 0 ? ut.c[n_ctx] : 0;
+  const int u = blockIdx.x;
+  k.is_ctx = u < n_cunits;
+  if (k.is_ctx) {
+    k.slot = find_seq(ut.c, n_ctx, u);
+    k.j0 = (u - ut.c[k.slot]) * keys;
+  } else {
+    const int um = u - n_cunits;
+    if (um >= n_main) return false;
+    if (CAUSAL) {
+      k.slot = 0;
+      k.j0 = um * keys;
+    } else {
+      k.slot = find_seq(ut.k, p.B, um);
+      k.j0 = (um - ut.k[k.slot]) * keys;
+    }
+  }
+  k.causal_main = CAUSAL && !k.is_ctx;
+  if (k.is_ctx) {
+    k.s = ctx_seg(p, g, k.slot, kh);
+    k.b_lo = 0;
+    k.b_hi = p.B;
+    k.shared = p.c_sh == 0;
+  } else if (CAUSAL) {
+    k.s = main_seg(p, g, -1, kh);
+    k.b_lo = k.j0 < k.s.n ? find_seq(cu, p.B, k.j0) : p.B;
+    k.b_hi = p.B;
+    k.shared = p.k_sh == 0;
+  } else {
+    k.s = main_seg(p, g, k.slot, kh);
+    k.b_lo = k.slot;
+    k.b_hi = k.slot + 1;
+    k.shared = p.k_sh == 0;
+  }
+  return k.j0 < k.s.n && !(k.shared && kh > 0);  // the grid covers the larger segment kind
+}
+
+// Query steps of a key unit: (head hq, sequence b, rows [p0, p0 + qs)) over every
+// sequence whose queries attend to the unit's keys, heads outermost; hq == hq_hi ends.
+struct QStep {
+  int hq, b, p0;
+};
+struct QuerySteps {
+  const fmlm_attn_params* p;
+  const KeyUnit* k;
+  int hq_hi, qs;
+  FMLM_DEV bool seq_ok(int b) const {
+    if (k->is_ctx && ctx_batch_of(*p, b) != k->slot) return false;
+    const SeqInfo si = seq_info(*p, b);
+    return si.len > 0 && (!k->causal_main || si.mainlen > k->j0);  // causal: tokens < cu[b+1]
+  }
+  FMLM_DEV QStep first_from(int hq, int b) const {
+    while (hq < hq_hi) {
+      for (; b < k->b_hi; ++b)
+        if (seq_ok(b)) return QStep{hq, b, 0};
+      ++hq;
+      b = k->b_lo;
+    }
+    return QStep{hq_hi, k->b_lo, 0};
+  }
+  FMLM_DEV QStep next(const QStep& st) const {
+    if (st.p0 + qs < seq_info(*p, st.b).len) return QStep{st.hq, st.b, st.p0 + qs};
+    return first_from(st.hq, st.b + 1);
+  }
+};
+
+// ---------------------------------------------------------------------------
 // dq kernel: grid (query-tile units, H), kBwdNW waves, QB blocks of 16 rows per wave.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
@@ -502,49 +589,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   float* const dl_s = lse_s + C::QS;
 
   const bool mla = C::MLA_ONLY || (p.flags & FMLM_FLAG_MLA);
-  const int32_t* cu = p.cu_seqlens_q;
   const int kh = blockIdx.y;
-  const UnitTables ut = unit_tables(p, g);
-  const int n_main = CAUSAL ? (min(cu[p.B], p.total_q) + C::DKV_KEYS - 1) / C::DKV_KEYS : ut.k[p.B];
-  const int n_cunits = n_ctx > 0 ? ut.c[n_ctx] : 0;
-  const int u = blockIdx.x;
-  const bool is_ctx = u < n_cunits;
-  int slot, j0;
-  if (is_ctx) {
-    slot = find_seq(ut.c, n_ctx, u);
-    j0 = (u - ut.c[slot]) * C::DKV_KEYS;
-  } else {
-    const int um = u - n_cunits;
-    if (um >= n_main) return;
-    if (CAUSAL) {
-      slot = 0;
-      j0 = um * C::DKV_KEYS;
-    } else {
-      slot = find_seq(ut.k, p.B, um);
-      j0 = (um - ut.k[slot]) * C::DKV_KEYS;
-    }
-  }
-  const bool causal_main = CAUSAL && !is_ctx;
-  BSeg s;
-  int b_lo, b_hi;  // sequences whose queries may attend to these keys
-  bool shared;     // key rows shared by all heads (head stride 0)
-  if (is_ctx) {
-    s = ctx_seg(p, g, slot, kh);
-    b_lo = 0;
-    b_hi = p.B;
-    shared = p.c_sh == 0;
-  } else if (CAUSAL) {
-    s = main_seg(p, g, -1, kh);
-    b_lo = j0 < s.n ? find_seq(cu, p.B, j0) : p.B;
-    b_hi = p.B;
-    shared = p.k_sh == 0;
-  } else {
-    s = main_seg(p, g, slot, kh);
-    b_lo = slot;
-    b_hi = slot + 1;
-    shared = p.k_sh == 0;
-  }
-  if (j0 >= s.n || (shared && kh > 0)) return;  // the grid covers the larger segment kind
+  KeyUnit ku;
+  if (!resolve_key_unit<CAUSAL>(p, g, n_ctx, C::DKV_KEYS, ku)) return;
+  const BSeg& s = ku.s;
+  const int j0 = ku.j0;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
   const float c = p.scale * kLog2e;
@@ -584,33 +633,13 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   // Query steps: (head hq, sequence b, rows [p0, p0 + QS)) over every sequence whose
   // queries attend to these keys, heads outermost.  A step's rows are loaded into
   // registers (one step ahead with DKV_PF) and written to LDS between two barriers.
-  const int hq_lo = shared ? 0 : kh, hq_hi = shared ? p.H : kh + 1;
-  struct Step {
-    int hq, b, p0;
-  };
-  auto seq_ok = [&](int b) {
-    if (is_ctx && ctx_batch_of(p, b) != slot) return false;
-    const SeqInfo si = seq_info(p, b);
-    return si.len > 0 && (!causal_main || si.mainlen > j0);  // causal: tokens < cu[b+1]
-  };
-  auto first_from = [&](int hq, int b) {
-    while (hq < hq_hi) {
-      for (; b < b_hi; ++b)
-        if (seq_ok(b)) return Step{hq, b, 0};
-      ++hq;
-      b = b_lo;
-    }
-    return Step{hq_hi, b_lo, 0};
-  };
-  auto next_step = [&](const Step& st) {
-    if (st.p0 + C::QS < seq_info(p, st.b).len) return Step{st.hq, st.b, st.p0 + C::QS};
-    return first_from(st.hq, st.b + 1);
-  };
+  const int hq_lo = ku.shared ? 0 : kh, hq_hi = ku.shared ? p.H : kh + 1;
+  const QuerySteps steps{&p, &ku, hq_hi, C::QS};
   constexpr int QCH = C::QS * C::C8;             // 16-byte chunks per step and tensor
   constexpr int QPT = (QCH + C::NT - 1) / C::NT;  // ... per thread
   u32x4 qreg[QPT], dreg[QPT];
   float lreg = INFINITY, dlreg = 0.f;
-  auto fetch = [&](const Step& st) {
+  auto fetch = [&](const QStep& st) {
     const SeqInfo si = seq_info(p, st.b);
 #pragma unroll
     for (int li = 0; li < QPT; ++li) {
@@ -648,11 +677,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     }
   };
 
-  Step cur = first_from(hq_lo, b_lo);
+  QStep cur = steps.first_from(hq_lo, ku.b_lo);
   if (C::DKV_PF && cur.hq < hq_hi) fetch(cur);
   while (cur.hq < hq_hi) {
-    const Step nxt = next_step(cur);
-    const int lim = causal_main ? seq_info(p, cur.b).mainlen : 0x7fffffff;
+    const QStep nxt = steps.next(cur);
+    const int lim = ku.causal_main ? seq_info(p, cur.b).mainlen : 0x7fffffff;
     __syncthreads();  // the previous step's LDS reads are done
     if (!C::DKV_PF) fetch(cur);
     stage();
@@ -751,6 +780,262 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
 }
 
 // ---------------------------------------------------------------------------
+// SIMT backward (fp32 inputs, and head dims without an MFMA kernel): the same two-kernel
+// split as above.  TPR threads per query row (dq) or per key row (dK / dV), each holding
+// DPT dims; a row's partial dot products meet through xor shuffles inside its TPR lanes,
+// and the staged tiles are fp32 in LDS, read as float4.
+// ---------------------------------------------------------------------------
+template <int D>
+struct SimtBwdCfg {
+  static constexpr int TPR = D / 4 < 16 ? D / 4 : 16;
+  static constexpr int DPT = D / TPR;
+  static constexpr int NT = 256;
+  static constexpr int R = NT / TPR;                       // query rows / keys per workgroup
+  static constexpr int BKS = 4096 / D < 64 ? 4096 / D : 64;  // query rows per dkv step
+  static constexpr int DQK = BKS < 32 ? BKS : 32;            // keys per dq tile (scores in registers)
+  static constexpr int DQ_LDS = 2 * DQK * D * 4;
+  static constexpr int DKV_LDS = 2 * BKS * D * 4 + 2 * BKS * 4;
+  static_assert(DPT % 4 == 0 && (TPR & (TPR - 1)) == 0, "simt tiling");
+};
+
+template <typename T>
+FMLM_DEV float4 ld4f(const T* p) {
+  return float4{(float)p[0], (float)p[1], (float)p[2], (float)p[3]};
+}
+template <>
+FMLM_DEV float4 ld4f<float>(const float* p) {
+  return *(const float4*)p;
+}
+
+// sum over the TPR lanes of a row
+template <int TPR>
+FMLM_DEV float row_sum(float x) {
+#pragma unroll
+  for (int off = 1; off < TPR; off <<= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_params p, const fmlm_attn_grads g) {
+  typedef SimtBwdCfg<D> C;
+  extern __shared__ __align__(16) char smem_raw[];
+  float* const Kf = (float*)smem_raw;
+  float* const Vf = Kf + C::DQK * D;
+
+  const UnitTables ut = unit_tables(p, g);
+  const int u = blockIdx.x, h = blockIdx.y;
+  if (u >= ut.q[p.B]) return;
+  const int b = find_seq(ut.q, p.B, u);
+  const SeqInfo si = seq_info(p, b);
+  const int qpos0 = (u - ut.q[b]) * C::R;
+  if (qpos0 >= si.len) return;
+  const int tid = threadIdx.x, row = tid / C::TPR, d0 = (tid % C::TPR) * C::DPT;
+  const int pos = qpos0 + row;
+  const bool ok = pos < si.len;
+  const float c = p.scale * kLog2e;
+  const bool kv_same = p.flags & FMLM_FLAG_MLA;
+
+  float q[C::DPT], dof[C::DPT], acc[C::DPT];
+  float dsum = 0.f;
+  {
+    const T* qp = (const T*)p.q + row_at(p.q_layout, b, h, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + d0;
+    const T* dp = (const T*)g.dout + row_at(p.o_layout, b, h, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + d0;
+    const T* op = (const T*)p.o + row_at(p.o_layout, b, h, si.q0, pos, p.o_sb, p.o_sh, p.o_sn) + d0;
+#pragma unroll
+    for (int d = 0; d < C::DPT; d += 4) {
+      const float4 z4 = float4{0.f, 0.f, 0.f, 0.f};
+      const float4 a = ok ? ld4f(qp + d) : z4, e = ok ? ld4f(dp + d) : z4, o = ok ? ld4f(op + d) : z4;
+      q[d] = a.x, q[d + 1] = a.y, q[d + 2] = a.z, q[d + 3] = a.w;
+      dof[d] = e.x, dof[d + 1] = e.y, dof[d + 2] = e.z, dof[d + 3] = e.w;
+      dsum += e.x * o.x + e.y * o.y + e.z * o.z + e.w * o.w;
+      acc[d] = acc[d + 1] = acc[d + 2] = acc[d + 3] = 0.f;
+    }
+  }
+  const float delta = row_sum<C::TPR>(dsum);
+
+  const BSeg sc = ctx_seg(p, g, ctx_batch_of(p, b), h);
+  const BSeg sm = main_seg(p, g, b, h);
+  const int nt0 = (sc.n + C::DQK - 1) / C::DQK;
+  const int nt = nt0 + (sm.n + C::DQK - 1) / C::DQK;
+  float m_i = -INFINITY, l_i = 0.f;
+  for (int t = 0; t < nt; ++t) {
+    const bool m = t >= nt0;
+    const int j0 = (m ? t - nt0 : t) * C::DQK, n = m ? sm.n : sc.n;
+    const int nk = min(C::DQK, n - j0);
+    __syncthreads();
+    for (int e = tid * 4; e < C::DQK * D; e += C::NT * 4) {
+      const int kk = e / D, d = e % D, key = j0 + kk;
+      float4 kv = float4{0.f, 0.f, 0.f, 0.f}, vv = kv;
+      if (kk < nk) {
+        kv = m ? ld4f((const T*)sm.k + sm.kbase + (int64_t)key * sm.ksn + d)
+               : ld4f((const T*)sc.k + key_elem(sc, sc.kbase, sc.ksn, key) + d);
+        vv = kv_same ? kv
+             : m     ? ld4f((const T*)sm.v + sm.vbase + (int64_t)key * sm.vsn + d)
+                     : ld4f((const T*)sc.v + key_elem(sc, sc.vbase, sc.vsn, key) + d);
+      }
+      *(float4*)(Kf + e) = kv;
+      *(float4*)(Vf + e) = vv;
+    }
+    __syncthreads();
+    float z[C::DQK], dpv[C::DQK];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kk = 0; kk < C::DQK; ++kk) {
+      float sdot = 0.f, pdot = 0.f;
+#pragma unroll
+      for (int d = 0; d < C::DPT; d += 4) {
+        const float4 k4 = *(const float4*)(Kf + kk * D + d0 + d);
+        const float4 v4 = *(const float4*)(Vf + kk * D + d0 + d);
+        sdot += q[d] * k4.x + q[d + 1] * k4.y + q[d + 2] * k4.z + q[d + 3] * k4.w;
+        pdot += dof[d] * v4.x + dof[d + 1] * v4.y + dof[d + 2] * v4.z + dof[d + 3] * v4.w;
+      }
+      sdot = row_sum<C::TPR>(sdot);
+      dpv[kk] = row_sum<C::TPR>(pdot);
+      z[kk] = kk < nk ? sdot * c : -INFINITY;
+      mx = fmaxf(mx, z[kk]);
+    }
+    const float m_new = fmaxf(m_i, mx);
+    const float alpha = m_i == -INFINITY ? 0.f : fast_exp2(m_i - m_new);
+    const float mref = m_new == -INFINITY ? 0.f : m_new;
+    l_i *= alpha;
+#pragma unroll
+    for (int d = 0; d < C::DPT; ++d) acc[d] *= alpha;
+    m_i = m_new;
+#pragma unroll
+    for (int kk = 0; kk < C::DQK; ++kk) {
+      const float pv = fast_exp2(z[kk] - mref);
+      l_i += pv;
+      const float gq = pv * (dpv[kk] - delta);
+#pragma unroll
+      for (int d = 0; d < C::DPT; d += 4) {
+        const float4 k4 = *(const float4*)(Kf + kk * D + d0 + d);
+        acc[d] += gq * k4.x;
+        acc[d + 1] += gq * k4.y;
+        acc[d + 2] += gq * k4.z;
+        acc[d + 3] += gq * k4.w;
+      }
+    }
+  }
+  if (!ok) return;
+  if (d0 == 0) {
+    float* const st_lse = (float*)g.workspace;
+    const int64_t at = (int64_t)h * p.total_q + si.q0 + pos;
+    st_lse[at] = l_i > 0.f ? m_i + __log2f(l_i) : INFINITY;
+    st_lse[(int64_t)p.H * p.total_q + at] = delta;
+  }
+  const float mul = l_i > 0.f ? p.scale / l_i : 0.f;
+  T* dqp = (T*)g.dq + row_at(p.q_layout, b, h, si.q0, pos, g.dq_sb, g.dq_sh, g.dq_sn) + d0;
+#pragma unroll
+  for (int d = 0; d < C::DPT; ++d) dqp[d] = (T)(acc[d] * mul);
+}
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_simt_kernel(const fmlm_attn_params p, const fmlm_attn_grads g,
+                                                                int n_ctx) {
+  typedef SimtBwdCfg<D> C;
+  constexpr int QS = C::BKS;
+  extern __shared__ __align__(16) char smem_raw[];
+  float* const Qf = (float*)smem_raw;
+  float* const Of = Qf + QS * D;
+  float* const lse_s = Of + QS * D;
+  float* const dl_s = lse_s + QS;
+
+  const bool mla = p.flags & FMLM_FLAG_MLA;
+  const int kh = blockIdx.y;
+  KeyUnit ku;
+  if (!resolve_key_unit<CAUSAL>(p, g, n_ctx, C::R, ku)) return;
+  const BSeg& s = ku.s;
+  const int tid = threadIdx.x, d0 = (tid % C::TPR) * C::DPT;
+  const int key = ku.j0 + tid / C::TPR;
+  const bool kok = key < s.n;
+  const float c = p.scale * kLog2e;
+  const float* const st_lse = (const float*)g.workspace;
+  const float* const st_delta = st_lse + (int64_t)p.H * p.total_q;
+
+  float kf[C::DPT], vf[C::DPT], dk[C::DPT], dv[C::DPT];
+#pragma unroll
+  for (int d = 0; d < C::DPT; d += 4) {
+    const float4 z4 = float4{0.f, 0.f, 0.f, 0.f};
+    const float4 a = kok ? ld4f((const T*)s.k + key_elem(s, s.kbase, s.ksn, key) + d0 + d) : z4;
+    const float4 e = kok && !mla ? ld4f((const T*)s.v + key_elem(s, s.vbase, s.vsn, key) + d0 + d) : a;
+    kf[d] = a.x, kf[d + 1] = a.y, kf[d + 2] = a.z, kf[d + 3] = a.w;
+    vf[d] = e.x, vf[d + 1] = e.y, vf[d + 2] = e.z, vf[d + 3] = e.w;
+    dk[d] = dk[d + 1] = dk[d + 2] = dk[d + 3] = 0.f;
+    dv[d] = dv[d + 1] = dv[d + 2] = dv[d + 3] = 0.f;
+  }
+
+  const int hq_lo = ku.shared ? 0 : kh, hq_hi = ku.shared ? p.H : kh + 1;
+  const QuerySteps steps{&p, &ku, hq_hi, QS};
+  for (QStep cur = steps.first_from(hq_lo, ku.b_lo); cur.hq < hq_hi; cur = steps.next(cur)) {
+    const SeqInfo si = seq_info(p, cur.b);
+    __syncthreads();  // the previous step's LDS reads are done
+    for (int e = tid * 4; e < QS * D; e += C::NT * 4) {
+      const int r = e / D, d = e % D, pos = cur.p0 + r;
+      float4 a = float4{0.f, 0.f, 0.f, 0.f}, o = a;
+      if (pos < si.len) {
+        a = ld4f((const T*)p.q + row_at(p.q_layout, cur.b, cur.hq, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + d);
+        o = ld4f((const T*)g.dout + row_at(p.o_layout, cur.b, cur.hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + d);
+      }
+      *(float4*)(Qf + e) = a;
+      *(float4*)(Of + e) = o;
+    }
+    for (int r = tid; r < QS; r += C::NT) {
+      const int pos = cur.p0 + r;
+      const bool ok = pos < si.len;
+      const int64_t at = (int64_t)cur.hq * p.total_q + si.q0 + pos;
+      lse_s[r] = ok ? st_lse[at] : INFINITY;  // padding rows: P = 0
+      dl_s[r] = ok ? st_delta[at] : 0.f;
+    }
+    __syncthreads();
+    const bool kvalid = kok && (!ku.causal_main || key < si.mainlen);
+#pragma unroll 4
+    for (int r = 0; r < QS; ++r) {
+      float sdot = 0.f, pdot = 0.f;
+#pragma unroll
+      for (int d = 0; d < C::DPT; d += 4) {
+        const float4 q4 = *(const float4*)(Qf + r * D + d0 + d);
+        const float4 o4 = *(const float4*)(Of + r * D + d0 + d);
+        sdot += q4.x * kf[d] + q4.y * kf[d + 1] + q4.z * kf[d + 2] + q4.w * kf[d + 3];
+        pdot += o4.x * vf[d] + o4.y * vf[d + 1] + o4.z * vf[d + 2] + o4.w * vf[d + 3];
+      }
+      sdot = row_sum<C::TPR>(sdot);
+      pdot = row_sum<C::TPR>(pdot);
+      const float pv = kvalid ? fast_exp2(fmaf(sdot, c, -lse_s[r])) : 0.f;
+      const float ds = pv * (pdot - dl_s[r]) * p.scale;
+#pragma unroll
+      for (int d = 0; d < C::DPT; d += 4) {
+        const float4 q4 = *(const float4*)(Qf + r * D + d0 + d);
+        const float4 o4 = *(const float4*)(Of + r * D + d0 + d);
+        dk[d] += ds * q4.x, dk[d + 1] += ds * q4.y, dk[d + 2] += ds * q4.z, dk[d + 3] += ds * q4.w;
+        dv[d] += pv * o4.x, dv[d + 1] += pv * o4.y, dv[d + 2] += pv * o4.z, dv[d + 3] += pv * o4.w;
+      }
+    }
+  }
+  if (!kok) return;
+  if (mla) {  // V is K
+#pragma unroll
+    for (int d = 0; d < C::DPT; ++d) dk[d] += dv[d];
+  }
+  if (s.pages) {  // float32 gradients, added atomically
+    float* dkf = (float*)s.dk + key_elem(s, s.dkbase, s.dksn, key) + d0;
+    float* dvf = (float*)s.dv + key_elem(s, s.dvbase, s.dvsn, key) + d0;
+#pragma unroll
+    for (int d = 0; d < C::DPT; ++d) {
+      atomicAdd(dkf + d, dk[d]);
+      if (!mla) atomicAdd(dvf + d, dv[d]);
+    }
+    return;
+  }
+  T* dkp = (T*)s.dk + s.dkbase + (int64_t)key * s.dksn + d0;
+  T* dvp = (T*)s.dv + s.dvbase + (int64_t)key * s.dvsn + d0;
+#pragma unroll
+  for (int d = 0; d < C::DPT; ++d) {
+    dkp[d] = (T)dk[d];
+    if (!mla) dvp[d] = (T)dv[d];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 struct BwdFns {
@@ -768,6 +1053,31 @@ static BwdFns bwd_fns() {
                 C::DKV_LDS,
                 C::BQ,
                 C::DKV_KEYS};
+}
+
+template <typename T, int D>
+static BwdFns bwd_simt_fns() {
+  typedef SimtBwdCfg<D> C;
+  return BwdFns{(const void*)attn_bwd_dq_simt_kernel<T, D>,
+                {(const void*)attn_bwd_dkv_simt_kernel<T, D, false>, (const void*)attn_bwd_dkv_simt_kernel<T, D, true>},
+                C::DQ_LDS,
+                C::DKV_LDS,
+                C::R,
+                C::R};
+}
+
+// SIMT kernels: fp32, and head dims or modes without an MFMA backward
+template <typename T>
+static bool pick_bwd_simt(int D, BwdFns& f) {
+  switch (D) {
+    case 16: f = bwd_simt_fns<T, 16>(); return true;
+    case 32: f = bwd_simt_fns<T, 32>(); return true;
+    case 64: f = bwd_simt_fns<T, 64>(); return true;
+    case 128: f = bwd_simt_fns<T, 128>(); return true;
+    case 256: f = bwd_simt_fns<T, 256>(); return true;
+    case 512: f = bwd_simt_fns<T, 512>(); return true;
+    default: return false;
+  }
 }
 
 template <typename T>
@@ -806,14 +1116,19 @@ static int check_bwd(const fmlm_attn_params& p, const fmlm_attn_grads& g, BwdFns
   if (p.B < 0 || p.H < 0 || p.N < 0 || p.total_q < 0 || p.ctx_len < 0) return FMLM_E_ARG;
   const bool mla = p.flags & FMLM_FLAG_MLA;
   if (!p.q || !p.o || !p.k || (!mla && !p.v) || !g.dout || !g.dq || !g.dk || (!mla && !g.dv)) return FMLM_E_ARG;
+  // MFMA kernels for bf16 / f16 (the 512-wide one only for the MLA latent), SIMT otherwise
+  const bool mfma_ok = p.D != 16 && (p.D != 512 || mla);
+  bool picked = false;
   if (p.dtype == FMLM_DTYPE_BF16) {
-    if (!pick_bwd<bf16>(p.D, f)) return FMLM_E_HEAD_DIM;
+    picked = mfma_ok ? pick_bwd<bf16>(p.D, f) : pick_bwd_simt<bf16>(p.D, f);
   } else if (p.dtype == FMLM_DTYPE_F16) {
-    if (!pick_bwd<f16>(p.D, f)) return FMLM_E_HEAD_DIM;
+    picked = mfma_ok ? pick_bwd<f16>(p.D, f) : pick_bwd_simt<f16>(p.D, f);
+  } else if (p.dtype == FMLM_DTYPE_F32) {
+    picked = pick_bwd_simt<float>(p.D, f);
   } else {
     return FMLM_E_DTYPE;
   }
-  if (p.D == 512 && !mla) return FMLM_E_HEAD_DIM;  // the 512-wide head dim is the MLA latent
+  if (!picked) return FMLM_E_HEAD_DIM;
   const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
   if (causal && (!p.cu_seqlens_q || p.kv_layout != FMLM_LAYOUT_PACKED)) return FMLM_E_ARG;
   if (p.ctx_block_table && (p.ctx_pages_per_batch < 0 || p.ctx_rows < 1 || p.ctx_page_stride < 0))

@@ -94,7 +94,7 @@ def _launch(*, run: bool = True, **kw) -> AttnLaunch:
 # context tensors: the forward runs as before inside an autograd Function, and its
 # backward runs fmlm_attn_bwd on the forward's own parameter block.
 # ---------------------------------------------------------------------------
-_BWD_HEAD_DIMS = (32, 64, 128, 256)
+_BWD_HEAD_DIMS = (16, 32, 64, 128, 256, 512)
 
 
 def _cache_tensors(inference_cache, layer_id, prefill: bool):
@@ -112,11 +112,11 @@ def _wants_grad(*tensors) -> bool:
 
 
 def _backward_unsupported(q: torch.Tensor, d: int, entry, is_mla: bool) -> str | None:
-    """Why this call has no backward, or None."""
-    if q.dtype not in (torch.bfloat16, torch.float16):
-        return "the attention backward needs bf16 or fp16 inputs"
-    if d not in _BWD_HEAD_DIMS and not (is_mla and d == 512):
-        return "the attention backward supports head_dim 32, 64, 128 or 256 (and a 512-wide MLA latent)"
+    """Why this call has no backward, or None (every head dim the forward runs has one)."""
+    if q.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        return "the attention backward needs bf16, fp16 or fp32 inputs"
+    if d not in _BWD_HEAD_DIMS:
+        return "the attention backward supports head_dim 16, 32, 64, 128, 256 or 512"
     return None
 
 

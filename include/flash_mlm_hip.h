@@ -242,7 +242,7 @@ FMLM_API int fmlm_attn_fwd(const fmlm_attn_params* p, void* stream);
  *           pool, zeroed by the caller, that the kernel adds into atomically: a page used
  *           by several context batches receives the sum of their gradients.
  * Rows not listed are not written.  dout is laid out like o (o_layout).
- * bf16 / f16, D in {32, 64, 128, 256}, or 512 with FMLM_FLAG_MLA; with
+ * bf16 / f16 (MFMA) and f32 (SIMT), D in {16, 32, 64, 128, 256, 512}; with
  * FMLM_FLAG_CAUSAL_SEQ the main keys must be packed (kv_layout PACKED).
  * workspace: fmlm_attn_bwd_workspace_bytes(p) bytes (per-row softmax statistics and the
  *           tile tables of the two kernels).

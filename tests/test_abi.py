@@ -69,8 +69,10 @@ def test_argument_rejection_without_launch():
     g.dout = g.dq = g.dk = g.dv = 256
     assert lib.fmlm_attn_bwd(p, g, None) == -3  # head dim without a backward kernel
     p.D = 64
-    p.dtype = _lib.DTYPE_F32
+    p.dtype = 7
     assert lib.fmlm_attn_bwd(p, g, None) == -2
+    p.dtype = _lib.DTYPE_F32  # SIMT kernels: accepted, then the missing workspace is reported
+    assert lib.fmlm_attn_bwd(p, g, None) == -5
     p.dtype = _lib.DTYPE_BF16
     assert lib.fmlm_attn_bwd(p, g, None) == -5  # no workspace
     assert lib.fmlm_attn_bwd_workspace_bytes(p) == 256  # 2 floats per (head, row) + tile tables, rounded up

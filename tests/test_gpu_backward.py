@@ -265,21 +265,55 @@ def test_backward_against_torch_fp32_autograd(device):
         _close(got, ref.detach().cpu().numpy().astype(np.float64), name)
 
 
-def test_backward_unsupported_warns_and_returns_plain_output(device):
-    """fp32 and head dims without a backward kernel: the forward runs as in the reference
-    (no graph on the output) and a warning says no gradient will flow."""
-    B, H, N, D = 1, 1, 8, 64
-    meta = build_pack_metadata(torch.tensor([8], device=device, dtype=torch.int32), N, block_n=64)
-    q = torch.randn((B, H, N, D), device=device, requires_grad=True)  # fp32
-    with pytest.warns(UserWarning, match="bf16 or fp16"):
-        out = flash_attn_mlm_compressed(q, q.detach(), q.detach(), H, meta, 0.1, block_n=64)
-    assert out.grad_fn is None and not out.requires_grad
-    q16 = torch.randn((B, H, N, 16), device=device).to(torch.bfloat16).requires_grad_()
-    with pytest.warns(UserWarning, match="head_dim"):
-        out = flash_attn_mlm_compressed(q16, q16.detach(), q16.detach(), H, meta, 0.1, block_n=64)
-    assert out.grad_fn is None
-    with torch.no_grad():  # no gradient wanted: no warning either
-        flash_attn_mlm_compressed(q16, q16, q16, H, meta, 0.1, block_n=64)
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.float32, 128), (torch.float32, 16),
+                                     (torch.bfloat16, 16), (torch.float16, 16)])
+@pytest.mark.parametrize("mode", ["ctx", "causal_mla_ctx"])
+def test_backward_simt_kernels(dtype, D, mode, device):
+    """fp32 inputs and head dim 16 take the SIMT backward kernels; fp32 gradients are held
+    to 1e-4 of the largest reference entry, bf16/fp16 to the tolerance above."""
+    gen = torch.Generator().manual_seed(8300 + D + (mode == "ctx"))
+    mla, causal = "mla" in mode, "causal" in mode
+    lengths = [70, 1, 0, 45]
+    B, H, N = len(lengths), 3, 72
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    cache, kc, vc, cu_kv, total = _packed_cache([65, 0, 130, 7], H=H, D=D, mla=mla, dtype=dtype, device=device,
+                                                gen=gen)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, k if mla else v, H, meta, scale, cache, 0, is_mla=mla, block_n=64,
+                                    causal_query_seq_attn=causal)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    from flash_mlm import unpack_from_kernel
+    g = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(k if mla else v), _np(unpack_from_kernel(dout, meta, H)), lengths, scale, is_mla=mla,
+        causal_query_seq_attn=causal, k_cache=_np(kc), v_cache=None if mla else _np(vc), cu_seqlens_kv=cu_kv,
+        total_context_len=total, context_batch_size=B)
+    pairs = [(q.grad, g[0], "dq"), (k.grad, g[1], "dk"), (kc.grad, g[3], "dkc")]
+    if not mla:
+        pairs += [(v.grad, g[2], "dv"), (vc.grad, g[4], "dvc")]
+    for got, ref, name in pairs:
+        if dtype == torch.float32:
+            err = float(np.abs(_np(got) - ref).max()) / float(np.abs(ref).max())
+            assert err <= 1e-4, f"{name}: {err:.2e}"
+        else:
+            _close(got, ref, name)
+
+
+def test_backward_dense_fp32_config1_shape(device):
+    """The dense fp32 workload of the reference's CPU-runnable configuration, through the
+    SIMT backward."""
+    gen = torch.Generator().manual_seed(8400)
+    B, H, N, D = 2, 8, 128, 64
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_leaf((B, H, N, D), torch.float32, device, gen, mult=1.0) for _ in range(3))
+    out = flash_attn_mlm(q, k, v, scale)
+    dout = torch.randn(out.shape, generator=gen).to(device)
+    out.backward(dout)
+    g = ar.mlm_attention_dense_backward(_np(q), _np(k), _np(v), _np(dout), scale)
+    for got, ref, name in ((q.grad, g[0], "dq"), (k.grad, g[1], "dk"), (v.grad, g[2], "dv")):
+        err = float(np.abs(_np(got) - ref).max()) / float(np.abs(ref).max())
+        assert err <= 1e-4, f"{name}: {err:.2e}"
 
 
 def test_backward_mla_shared_tensor_and_strided_views(device):

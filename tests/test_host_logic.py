@@ -276,3 +276,14 @@ def test_layer_entry_returns_the_stored_tensors():
     entry = cache.layer_entry("x")
     assert entry.k_cache is k and entry.v_cache is v  # gradients reach the caller's tensors
     assert cache.layer_entry("y") is None
+
+
+def test_backward_available_for_every_forward_head_dim_and_dtype():
+    from flash_mlm.host import host as hh
+
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        q = torch.zeros(1, dtype=dt)
+        for d in (16, 32, 64, 128, 256, 512):
+            assert hh._backward_unsupported(q, d, None, is_mla=False) is None
+    assert "bf16, fp16 or fp32" in hh._backward_unsupported(torch.zeros(1, dtype=torch.float64), 64, None, False)
+    assert "head_dim" in hh._backward_unsupported(torch.zeros(1, dtype=torch.float32), 48, None, False)
