@@ -147,15 +147,15 @@ def _scatter_to_pages(grad_ctx, block_table, lens, H_kv, P, D):
     return pool
 
 
-@pytest.mark.parametrize("mla", [False, True])
+@pytest.mark.parametrize("mla,D", [(False, 128), (True, 64), (False, 16)])
 @pytest.mark.parametrize("shared_page", [False, True])
-def test_paged_context_backward(mla, shared_page, device):
+def test_paged_context_backward(mla, D, shared_page, device):
     """Backward over a paged context (float32 accumulation of the pool gradient): q/k/v
     gradients equal those of the same rows stored contiguously, and the pool gradient is
     the oracle's context gradient added back into the pages, pages used by two context
     batches (a shared prefix) receiving both batches' gradients."""
-    g = torch.Generator().manual_seed(6400 + 2 * mla + shared_page)
-    H, D, dtype = 2, 128 if not mla else 64, torch.bfloat16
+    g = torch.Generator().manual_seed(6400 + 2 * mla + shared_page + D)
+    H, dtype = 2, torch.bfloat16  # D = 16 takes the SIMT backward kernels
     h_kv = 1 if mla else H
     lens = [130, 70, 64]
     P = 9
