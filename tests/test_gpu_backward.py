@@ -265,9 +265,10 @@ def test_backward_against_torch_fp32_autograd(device):
         _close(got, ref.detach().cpu().numpy().astype(np.float64), name)
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.float32, 128), (torch.float32, 16),
-                                     (torch.bfloat16, 16), (torch.float16, 16)])
-@pytest.mark.parametrize("mode", ["ctx", "causal_mla_ctx"])
+@pytest.mark.parametrize("dtype,D,mode", [
+    (dt, d, m) for dt, d in [(torch.float32, 64), (torch.float32, 128), (torch.float32, 16),
+                             (torch.bfloat16, 16), (torch.float16, 16)] for m in ("ctx", "causal_mla_ctx")
+] + [(torch.float32, 512, "causal_mla_ctx")])
 def test_backward_simt_kernels(dtype, D, mode, device):
     """fp32 inputs and head dim 16 take the SIMT backward kernels; fp32 gradients are held
     to 1e-4 of the largest reference entry, bf16/fp16 to the tolerance above."""
