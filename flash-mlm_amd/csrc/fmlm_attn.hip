@@ -633,13 +633,6 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(con
 // wait for every outstanding load before the first V read; ordering is enforced here
 // by the explicit wait + barrier of step 4 instead.
 // ---------------------------------------------------------------------------
-template <int D>
-FMLM_DEV int kv_swz(int r) {
-  if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  else if constexpr (D == 64) return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
-  else if constexpr (D == 32) return (r >> 2) & 3;
-  else return (r >> 3) & 1;
-}
 
 // NaN-propagating max (v_maximum3_f32): no operand canonicalisation, unlike fmaxf
 FMLM_DEV float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
@@ -659,27 +652,6 @@ FMLM_DEV float lane_max_xor16_32(float x) {
 // and arithmetic consuming it stays after, in the order of the surrounding side effects.
 template <typename X>
 FMLM_DEV void pin(X& x) { asm volatile("" : "+v"(x)); }
-
-FMLM_DEV uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const FMLM_LDS char*)p;
-}
-
-FMLM_DEV const char* uniform_ptr(const char* p) {
-  const uint64_t v = (uint64_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const char*)(((uint64_t)hi << 32) | lo);
-}
-
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// 64 lanes x 16 bytes from base + off (per lane) to LDS [lds, lds + 1024), lane l at
-// lds + 16 l.  base and lds are wave-uniform.
-FMLM_DEV void dma16_sbase(const char* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(off), "s"(base), "s"(lds) : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 
 template <typename T>

@@ -42,10 +42,17 @@ struct BwdCfg {
   static constexpr int RS = D + 16;               // LDS row stride (elements)
   static constexpr int C8 = D / 8;                // 16-byte chunks per row
   static constexpr int QB = D >= 256 ? 1 : 2;     // 16-row query blocks per wave (dq kernel)
-  // dq kernel: load the next key tile into registers during the current one's math
-  // (off where those registers would not fit beside QB = 2)
-  static constexpr bool PF = D <= 64;
   static constexpr int BQ = kBwdNW * QB * 16;     // query rows per dq workgroup
+  // dq kernel key tiles: unpadded rows whose 16-byte chunks are swizzled by kv_swz,
+  // filled by direct global->LDS loads of RPI rows per wave-wide load.  The 512-wide
+  // latent (PAD) instead stages its tile through registers into rows padded to D + 16
+  // elements: its accumulators leave no room for the direct-load pipeline (it spilled).
+  static constexpr int CPR = D / 8;               // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;            // rows per wave-wide load
+  static constexpr bool PAD = D >= 512;
+  static constexpr int ROWB = (PAD ? D + 16 : D) * 2;  // LDS row pitch (bytes)
+  static constexpr int TILEB = kBwdBK * ROWB;
+  static constexpr int NPW = kBwdBK / RPI / kBwdNW;  // wave-wide loads per tile and tensor
   static constexpr int NKB = kBwdBK / 16;
   static constexpr int NKS = kBwdBK / 32;
   // dkv kernel: 16-key blocks per wave, and whether the next query step is loaded ahead
@@ -55,12 +62,16 @@ struct BwdCfg {
   static constexpr bool DKV_PF = D <= 128;
   static constexpr int DKV_KEYS = kBwdNW * 16 * KB;  // keys per dkv workgroup
   static constexpr int QS = D >= 256 ? 32 : 64;   // query rows per dkv step (32-row groups)
-  static constexpr int DQ_LDS = 2 * kBwdBK * RS * 2;                  // K and V tiles
   static constexpr int DKV_LDS = 2 * QS * RS * 2 + 2 * QS * 4;  // Q, dO, lse, delta
   // waves per SIMD the kernels are built for: the 512-wide latent needs more than 256
   // registers per wave, which gfx950 gives a wave (VGPRs + AGPRs) only at one wave per SIMD
   static constexpr int WPS = D >= 512 ? 1 : 2;
   static constexpr bool MLA_ONLY = D >= 512;  // the 512-wide head dim exists for the MLA latent only
+  // dq kernel: two buffers per tensor (the next tile loads during the current one's
+  // math) where they fit beside the other workgroups of a CU, one at D >= 256; the
+  // latent needs no V tile (V = K)
+  static constexpr int DQ_NBUF = D <= 128 ? 2 : 1;
+  static constexpr int DQ_LDS = DQ_NBUF * (MLA_ONLY ? 1 : 2) * TILEB;
   static_assert(D % 32 == 0 && D >= 32 && D <= 512, "head dim");
 };
 
@@ -332,8 +343,6 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   typedef typename Mfma<T>::v8 v8;
   constexpr int QB = C::QB;
   extern __shared__ __align__(16) char smem_raw[];
-  T* const Ks = (T*)smem_raw;
-  T* const Vs = Ks + kBwdBK * C::RS;
 
   const UnitTables ut = unit_tables(p, g);
   const int u = blockIdx.x, h = blockIdx.y;
@@ -345,9 +354,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
   const float c = p.scale * kLog2e;  // scores in log2 units
-  // MLA: V is K, so the K tile serves both products and no V tile is staged
+  // MLA: V is K, so the K tile serves both products and no V tile is loaded
   const bool kv_same = C::MLA_ONLY || (p.flags & FMLM_FLAG_MLA);
-  const T* const Vt = kv_same ? Ks : Vs;
 
   const BSeg sc = ctx_seg(p, g, ctx_batch_of(p, b), h);  // context, then main keys
   const BSeg sm = main_seg(p, g, b, h);
@@ -386,46 +394,103 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     delta[qb] = dsum;
   }
 
-  // key tile t of [context || main] (64 keys; rows past a segment end are 0): fetch()
-  // loads it into registers, stage() writes the registers to LDS.  With PF the next
-  // tile's loads are issued before the current tile's math.
-  constexpr int LPT = kBwdBK * C::C8 / C::NT;  // 16-byte chunks per thread per tensor
-  u32x4 kreg[LPT], vreg[LPT];
+  // ---- key tiles t of [context || main], 64 keys each, K in buffer (NBUF = 2: t % 2)
+  // at kbuf, V at vbuf.  issue() starts the direct loads of tile t: wave-wide load
+  // i = wave + j*NW brings rows [i*RPI, (i+1)*RPI), lane l fetching logical chunk
+  // (l % CPR) ^ kv_swz(row) of row i*RPI + l/CPR into physical chunk l % CPR.  Rows past
+  // the segment end repeat its last row (their scores are masked to -inf, so P = 0).
   auto keys_in = [&](int t) {
     return t < nt0 ? min(kBwdBK, sc.n - t * kBwdBK) : min(kBwdBK, sm.n - (t - nt0) * kBwdBK);
   };
-  auto fetch = [&](int t, bool with_v) {
-    const bool m = t >= nt0;
-    const int j0 = (m ? t - nt0 : t) * kBwdBK, n = m ? sm.n : sc.n;
-    const char* kp = m ? sm.k : sc.k;
-    const char* vp = m ? sm.v : sc.v;
-    const int64_t ksn = m ? sm.ksn : sc.ksn, vsn = m ? sm.vsn : sc.vsn;
-    // row 0 of the tile (a paged context tile is one page)
-    const int64_t kt = m ? sm.kbase + (int64_t)j0 * ksn : key_elem(sc, sc.kbase, ksn, j0);
-    const int64_t vt = m ? sm.vbase + (int64_t)j0 * vsn : key_elem(sc, sc.vbase, vsn, j0);
+  auto kbuf = [&](int buf) { return smem_raw + buf * C::TILEB; };
+  auto vbuf = [&](int buf) { return smem_raw + (C::DQ_NBUF + buf) * C::TILEB; };
+  auto issue = [&](int t, int buf) {
+    if constexpr (C::PAD) {  // register-staged; single buffer, so nothing reads it meanwhile
+      constexpr int LPT = kBwdBK * C::CPR / C::NT;  // 16-byte chunks per thread and tensor
+      const bool m = t >= nt0;
+      const int j0 = (m ? t - nt0 : t) * kBwdBK, n = m ? sm.n : sc.n;
+      const char* const kp = m ? sm.k : sc.k;
+      const char* const vp = m ? sm.v : sc.v;
+      const int64_t ksn = m ? sm.ksn : sc.ksn, vsn = m ? sm.vsn : sc.vsn;
+      const int64_t kt = m ? sm.kbase + (int64_t)j0 * ksn : key_elem(sc, sc.kbase, ksn, j0);
+      const int64_t vt = m ? sm.vbase + (int64_t)j0 * vsn : key_elem(sc, sc.vbase, vsn, j0);
+      u32x4 kreg[LPT], vreg[LPT];
 #pragma unroll
-    for (int li = 0; li < LPT; ++li) {
-      const int it = tid + li * C::NT;
-      const int row = it / C::C8, c8 = it % C::C8;
-      kreg[li] = u32x4{0u, 0u, 0u, 0u};
-      vreg[li] = kreg[li];
-      if (j0 + row < n) {
-        kreg[li] = ld16(kp, kt + (int64_t)row * ksn + c8 * 8);
-        if (with_v) vreg[li] = ld16(vp, vt + (int64_t)row * vsn + c8 * 8);
+      for (int li = 0; li < LPT; ++li) {  // rows past the segment end are 0
+        const int it = tid + li * C::NT;
+        const int row = it / C::CPR, c8 = it % C::CPR;
+        kreg[li] = u32x4{0u, 0u, 0u, 0u};
+        vreg[li] = kreg[li];
+        if (j0 + row < n) {
+          kreg[li] = ld16(kp, kt + (int64_t)row * ksn + c8 * 8);
+          if (!kv_same) vreg[li] = ld16(vp, vt + (int64_t)row * vsn + c8 * 8);
+        }
       }
-    }
-  };
-  auto stage = [&](bool with_v) {
 #pragma unroll
-    for (int li = 0; li < LPT; ++li) {
-      const int it = tid + li * C::NT;
-      const int row = it / C::C8, c8 = it % C::C8;
-      *(u32x4*)(Ks + row * C::RS + c8 * 8) = kreg[li];
-      if (with_v) *(u32x4*)(Vs + row * C::RS + c8 * 8) = vreg[li];
+      for (int li = 0; li < LPT; ++li) {
+        const int it = tid + li * C::NT;
+        const int at = (it / C::CPR) * C::ROWB + (it % C::CPR) * 16;
+        *(u32x4*)(kbuf(buf) + at) = kreg[li];
+        if (!kv_same) *(u32x4*)(vbuf(buf) + at) = vreg[li];
+      }
+      return;
+    }
+    // the lane's load offsets are recomputed per tile (cheap integer work) rather than
+    // hoisted out of the key loop, where they would hold NPW registers through the math
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int drow0 = wave * C::RPI + ln / C::CPR;  // + j*NW*RPI for load j
+    // (fields picked one by one: a reference to either segment would put both in memory)
+    const bool m = t >= nt0;
+    const int j0 = (m ? t - nt0 : t) * kBwdBK;
+    const int last = min(kBwdBK, (m ? sm.n : sc.n) - j0) - 1;
+    // row 0 of the tile (a paged context tile is one page): both page lookups before
+    // any load is issued, so their waits wait for nothing else
+    const int64_t kt = m ? sm.kbase + (int64_t)j0 * sm.ksn : key_elem(sc, sc.kbase, sc.ksn, j0);
+    const int64_t vt = kv_same ? 0 : m ? sm.vbase + (int64_t)j0 * sm.vsn : key_elem(sc, sc.vbase, sc.vsn, j0);
+    const char* const kp = uniform_ptr((m ? sm.k : sc.k) + kt * 2);
+    const char* const vp = uniform_ptr((m ? sm.v : sc.v) + vt * 2);
+    const uint32_t krowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.ksn : sc.ksn) * 2u);
+    const uint32_t vrowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.vsn : sc.vsn) * 2u);
+    const uint32_t k0 = lds_addr(kbuf(buf)), v0 = lds_addr(vbuf(buf));
+#pragma unroll
+    for (int j = 0; j < C::NPW; ++j) {
+      const int row = drow0 + j * kBwdNW * C::RPI;
+      const int i = wave + j * kBwdNW;
+      const uint32_t r = (uint32_t)min(row, last);
+      const uint32_t sw = 16u * (uint32_t)((ln % C::CPR) ^ kv_swz<D>(row));
+      dma16_sbase(kp, r * krowb + sw, __builtin_amdgcn_readfirstlane(k0 + i * 1024));
+      if (!kv_same) dma16_sbase(vp, r * vrowb + sw, __builtin_amdgcn_readfirstlane(v0 + i * 1024));
     }
   };
-  // S^T = K Q^T of the staged tile: lane (q + 16g) reg r = S[query q][key 16kb + 4g + r]
-  auto scores = [&](f32x4 (&s)[C::NKB][QB]) {
+  // per-lane LDS byte offsets in a tile: the row fragment (rows 16kb + l16, columns
+  // 32kc + 8g .. +8) is at kb*16*ROWB + 256*(kc/4) + koff[kc%4]; the tr16 fragment of
+  // rows 32ks + 16h + 4g + (l16 >> 2), columns 16db + 4*(l16 & 3) .. +4 at
+  // (32ks + 16h)*ROWB + 256*(db/8) + voff[db%8].  Padded rows (PAD): one base each.
+  int koff[4], voff[8];
+  if constexpr (!C::PAD) {
+    const int ksw = kv_swz<D>(l16);
+#pragma unroll
+    for (int b4 = 0; b4 < 4; ++b4) koff[b4] = l16 * C::ROWB + 16 * ((4 * b4 + gq) ^ ksw);
+    const int vr = 4 * gq + (l16 >> 2);
+    const int vsw = kv_swz<D>(vr);
+    const int x = (l16 & 3) >> 1;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) voff[db] = vr * C::ROWB + 16 * ((2 * db + x) ^ vsw) + 8 * (l16 & 1);
+  }
+  auto row_frag = [&](const char* tile, int kb, int kc) {
+    if constexpr (C::PAD) return *(const v8*)((const T*)tile + (kb * 16 + l16) * (C::ROWB / 2) + kc * 32 + gq * 8);
+    return *(const v8*)(tile + kb * 16 * C::ROWB + 256 * (kc / 4) + koff[kc % 4]);
+  };
+  auto col_frag = [&](const char* tile, int ks, int db) {
+    if constexpr (C::PAD) return tr_frag<T>((const T*)tile, C::ROWB / 2, ks * 32, db, l16, gq);
+    const char* a = tile + ks * 32 * C::ROWB + 256 * (db / 8) + voff[db % 8];
+    const s16x4 lo = lds_read_tr16(a);
+    const s16x4 hi = lds_read_tr16(a + 16 * C::ROWB);
+    return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  // S^T = K Q^T of a tile: lane (q + 16g) reg r = S[query q][key 16kb + 4g + r]
+  auto scores = [&](const char* kt, f32x4 (&s)[C::NKB][QB]) {
 #pragma unroll
     for (int kb = 0; kb < C::NKB; ++kb)
 #pragma unroll
@@ -434,7 +499,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     for (int kc = 0; kc < C::KC; ++kc)
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb) {
-        const v8 a = *(const v8*)(Ks + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
+        const v8 a = row_frag(kt, kb, kc);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) s[kb][qb] = Mfma<T>::run(a, qf[qb][kc], s[kb][qb]);
       }
@@ -456,16 +521,23 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     m_i[qb] = -INFINITY;
     l_i[qb] = 0.f;
   }
-  if (C::PF && nt > 0) fetch(0, !kv_same);
+  // NBUF = 2: tile t+1 loads while tile t is used; its buffer was last read by tile t-1,
+  // which every wave has finished at the barrier before the issue
+  if (C::DQ_NBUF == 2 && nt > 0) issue(0, 0);
   for (int t = 0; t < nt; ++t) {
     const int nk = keys_in(t);
-    __syncthreads();  // the previous tile's LDS reads are done
-    if (!C::PF) fetch(t, !kv_same);
-    stage(!kv_same);
-    __syncthreads();
-    if (C::PF && t + 1 < nt) fetch(t + 1, !kv_same);
+    const int buf = C::DQ_NBUF == 2 ? (t & 1) : 0;
+    if (C::DQ_NBUF == 1) {
+      __syncthreads();  // the previous tile's LDS reads are done
+      issue(t, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t have landed
+    __syncthreads();                // ... and every other wave's
+    if (C::DQ_NBUF == 2 && t + 1 < nt) issue(t + 1, buf ^ 1);
+    const char* const kt = kbuf(buf);
+    const char* const vt = kv_same ? kt : vbuf(buf);
     f32x4 s[C::NKB][QB], dp[C::NKB][QB];
-    scores(s);
+    scores(kt, s);
     // dP^T = V dO^T, same layout as S^T
 #pragma unroll
     for (int kb = 0; kb < C::NKB; ++kb)
@@ -475,7 +547,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     for (int kc = 0; kc < C::KC; ++kc)
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb) {
-        const v8 a = *(const v8*)(Vt + (kb * 16 + l16) * C::RS + kc * 32 + gq * 8);
+        const v8 a = row_frag(vt, kb, kc);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = Mfma<T>::run(a, df[qb][kc], dp[kb][qb]);
       }
@@ -530,7 +602,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     for (int ks = 0; ks < C::NKS; ++ks)
 #pragma unroll
       for (int db = 0; db < C::NDB; ++db) {
-        const v8 a = tr_frag<T>(Ks, C::RS, ks * 32, db, l16, gq);
+        const v8 a = col_frag(kt, ks, db);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) dq[db][qb] = Mfma<T>::run(a, dsf[ks][qb], dq[db][qb]);
       }

@@ -139,4 +139,37 @@ FMLM_DEV s16x4 lds_read_tr16_at(uint32_t a) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLM_LDS s16x4*)(uintptr_t)a);
 }
 
+// 16-byte chunk swizzle of a row-major LDS tile of head dim D: logical chunk c of row r
+// sits in physical chunk c ^ kv_swz(r).  It depends on r % 16 only and makes both the
+// b128 row-fragment reads (16 rows, one chunk each) and the tr16 reads (4 rows x 4
+// lanes per 16-lane group) bank-conflict free.
+template <int D>
+FMLM_DEV int kv_swz(int r) {
+  if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else if constexpr (D == 64) return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+  else if constexpr (D == 32) return (r >> 2) & 3;
+  else return (r >> 3) & 1;
+}
+
+FMLM_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const FMLM_LDS char*)p;
+}
+
+FMLM_DEV const char* uniform_ptr(const char* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const char*)(((uint64_t)hi << 32) | lo);
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 64 lanes x 16 bytes from base + off (per lane) to LDS [lds, lds + 1024), lane l at
+// lds + 16 l.  base and lds are wave-uniform.
+FMLM_DEV void dma16_sbase(const char* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 }  // namespace fmlm
