@@ -39,7 +39,6 @@ struct BwdCfg {
   static constexpr int NT = kBwdNW * 64;
   static constexpr int KC = D / 32;               // 32-wide contraction steps over D
   static constexpr int NDB = D / 16;              // 16-wide column blocks
-  static constexpr int RS = D + 16;               // LDS row stride (elements)
   static constexpr int C8 = D / 8;                // 16-byte chunks per row
   static constexpr int QB = D >= 256 ? 1 : 2;     // 16-row query blocks per wave (dq kernel)
   static constexpr int BQ = kBwdNW * QB * 16;     // query rows per dq workgroup
@@ -55,14 +54,18 @@ struct BwdCfg {
   static constexpr int NPW = kBwdBK / RPI / kBwdNW;  // wave-wide loads per tile and tensor
   static constexpr int NKB = kBwdBK / 16;
   static constexpr int NKS = kBwdBK / 32;
-  // dkv kernel: 16-key blocks per wave, and whether the next query step is loaded ahead
-  // (the register budget allows both only up to D = 64; at D = 128 two blocks spill,
-  // which measured slower than one block with the load ahead)
+  // dkv kernel: 16-key blocks per wave (at D = 128 two blocks spill, which measured
+  // slower than one)
   static constexpr int KB = (D <= 64 || D >= 512) ? 2 : 1;
-  static constexpr bool DKV_PF = D <= 128;
   static constexpr int DKV_KEYS = kBwdNW * 16 * KB;  // keys per dkv workgroup
   static constexpr int QS = D >= 256 ? 32 : 64;   // query rows per dkv step (32-row groups)
-  static constexpr int DKV_LDS = 2 * QS * RS * 2 + 2 * QS * 4;  // Q, dO, lse, delta
+  // dK/dV kernel: a query step's Q and dO rows (tiles like the dq kernel's) and its lse
+  // and delta, in two buffers (the next step loads during the current one's math), one
+  // register-staged buffer for the latent
+  static constexpr int DKV_NBUF = PAD ? 1 : 2;
+  static constexpr int STEPB = QS * ROWB;
+  static constexpr int DKV_SB = 2 * STEPB + 2 * QS * 4;  // bytes per step buffer
+  static constexpr int DKV_LDS = DKV_NBUF * DKV_SB;
   // waves per SIMD the kernels are built for: the 512-wide latent needs more than 256
   // registers per wave, which gfx950 gives a wave (VGPRs + AGPRs) only at one wave per SIMD
   static constexpr int WPS = D >= 512 ? 1 : 2;
@@ -183,6 +186,75 @@ FMLM_DEV typename Mfma<T>::v8 tr_frag(const T* tile, int rs, int row0, int db, i
   const s16x4 lo = lds_read_tr16(base);
   const s16x4 hi = lds_read_tr16(base + 16 * rs);
   return __builtin_bit_cast(typename Mfma<T>::v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Fragment reads from a row-major LDS tile of head dim D (row pitch ROWB bytes): rows of
+// D elements whose 16-byte chunks are swizzled by kv_swz (logical chunk c of row r in
+// physical chunk c ^ kv_swz(r)), or, with PAD, rows padded to D + 16 elements.
+//   row(tile, kb, kc): A operand of rows 16kb + l16, columns 32kc + 8g .. +8;
+//   col(tile, ks, db): tr_frag's fragment of X^T from rows 32ks .. +32, columns 16db .. +16.
+template <typename T, int D>
+struct TileReader {
+  typedef BwdCfg<D> C;
+  typedef typename Mfma<T>::v8 v8;
+  int koff[4], voff[8], l16, g;
+  FMLM_DEV TileReader(int l16_, int g_) : l16(l16_), g(g_) {
+    if constexpr (!C::PAD) {
+      // row fragment at kb*16*ROWB + 256*(kc/4) + koff[kc%4]; tr16 fragment of rows
+      // 32ks + 16h + 4g + (l16 >> 2), columns 16db + 4*(l16 & 3) .. +4 at
+      // (32ks + 16h)*ROWB + 256*(db/8) + voff[db%8]
+      const int ksw = kv_swz<D>(l16);
+#pragma unroll
+      for (int b4 = 0; b4 < 4; ++b4) koff[b4] = l16 * C::ROWB + 16 * ((4 * b4 + g) ^ ksw);
+      const int vr = 4 * g + (l16 >> 2);
+      const int vsw = kv_swz<D>(vr);
+      const int x = (l16 & 3) >> 1;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) voff[db] = vr * C::ROWB + 16 * ((2 * db + x) ^ vsw) + 8 * (l16 & 1);
+    }
+  }
+  FMLM_DEV v8 row(const char* tile, int kb, int kc) const {
+    if constexpr (C::PAD) {
+      return *(const v8*)((const T*)tile + (kb * 16 + l16) * (C::ROWB / 2) + kc * 32 + g * 8);
+    } else {
+      return *(const v8*)(tile + kb * 16 * C::ROWB + 256 * (kc / 4) + koff[kc % 4]);
+    }
+  }
+  FMLM_DEV v8 col(const char* tile, int ks, int db) const {
+    if constexpr (C::PAD) {
+      return tr_frag<T>((const T*)tile, C::ROWB / 2, ks * 32, db, l16, g);
+    } else {
+      const char* a = tile + ks * 32 * C::ROWB + 256 * (db / 8) + voff[db % 8];
+      const s16x4 lo = lds_read_tr16(a);
+      const s16x4 hi = lds_read_tr16(a + 16 * C::ROWB);
+      return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  }
+};
+
+// Direct global->LDS loads of an NR-row swizzled tile: rows from the wave-uniform row-0
+// address src at pitch rowb bytes (rows past `last` repeat row `last`) into the tile at
+// LDS byte address lds.  Wave-wide load i = wave + j*NW brings rows [i*RPI, (i+1)*RPI),
+// lane l fetching logical chunk (l % CPR) ^ kv_swz(row) of row i*RPI + l/CPR into
+// physical chunk l % CPR.  Nothing waits here: the caller waits (vmcnt) and meets a
+// barrier before the tile is read.
+template <int D, int NR>
+FMLM_DEV void dma_rows(const char* src, uint32_t rowb, int last, uint32_t lds, int wave, int lane) {
+  typedef BwdCfg<D> C;
+  static_assert(!C::PAD && NR % (C::RPI * kBwdNW) == 0, "whole wave-wide loads per wave");
+  // the lane's offsets are recomputed per call (cheap integer work) rather than hoisted
+  // out of the caller's loop, where they would hold registers through the math
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  const int row0 = wave * C::RPI + ln / C::CPR;
+#pragma unroll
+  for (int j = 0; j < NR / (C::RPI * kBwdNW); ++j) {
+    const int row = row0 + j * kBwdNW * C::RPI;
+    const int i = wave + j * kBwdNW;
+    const uint32_t r = (uint32_t)min(row, last);
+    dma16_sbase(src, r * rowb + 16u * (uint32_t)((ln % C::CPR) ^ kv_swz<D>(row)),
+                __builtin_amdgcn_readfirstlane(lds + i * 1024));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -395,9 +467,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   }
 
   // ---- key tiles t of [context || main], 64 keys each, K in buffer (NBUF = 2: t % 2)
-  // at kbuf, V at vbuf.  issue() starts the direct loads of tile t: wave-wide load
-  // i = wave + j*NW brings rows [i*RPI, (i+1)*RPI), lane l fetching logical chunk
-  // (l % CPR) ^ kv_swz(row) of row i*RPI + l/CPR into physical chunk l % CPR.  Rows past
+  // at kbuf, V at vbuf.  issue() starts the direct loads of tile t (dma_rows); rows past
   // the segment end repeat its last row (their scores are masked to -inf, so P = 0).
   auto keys_in = [&](int t) {
     return t < nt0 ? min(kBwdBK, sc.n - t * kBwdBK) : min(kBwdBK, sm.n - (t - nt0) * kBwdBK);
@@ -405,10 +475,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   auto kbuf = [&](int buf) { return smem_raw + buf * C::TILEB; };
   auto vbuf = [&](int buf) { return smem_raw + (C::DQ_NBUF + buf) * C::TILEB; };
   auto issue = [&](int t, int buf) {
+    const bool m = t >= nt0;
+    const int j0 = (m ? t - nt0 : t) * kBwdBK;
     if constexpr (C::PAD) {  // register-staged; single buffer, so nothing reads it meanwhile
       constexpr int LPT = kBwdBK * C::CPR / C::NT;  // 16-byte chunks per thread and tensor
-      const bool m = t >= nt0;
-      const int j0 = (m ? t - nt0 : t) * kBwdBK, n = m ? sm.n : sc.n;
+      const int n = m ? sm.n : sc.n;
       const char* const kp = m ? sm.k : sc.k;
       const char* const vp = m ? sm.v : sc.v;
       const int64_t ksn = m ? sm.ksn : sc.ksn, vsn = m ? sm.vsn : sc.vsn;
@@ -433,62 +504,24 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
         *(u32x4*)(kbuf(buf) + at) = kreg[li];
         if (!kv_same) *(u32x4*)(vbuf(buf) + at) = vreg[li];
       }
-      return;
-    }
-    // the lane's load offsets are recomputed per tile (cheap integer work) rather than
-    // hoisted out of the key loop, where they would hold NPW registers through the math
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    const int drow0 = wave * C::RPI + ln / C::CPR;  // + j*NW*RPI for load j
-    // (fields picked one by one: a reference to either segment would put both in memory)
-    const bool m = t >= nt0;
-    const int j0 = (m ? t - nt0 : t) * kBwdBK;
-    const int last = min(kBwdBK, (m ? sm.n : sc.n) - j0) - 1;
-    // row 0 of the tile (a paged context tile is one page): both page lookups before
-    // any load is issued, so their waits wait for nothing else
-    const int64_t kt = m ? sm.kbase + (int64_t)j0 * sm.ksn : key_elem(sc, sc.kbase, sc.ksn, j0);
-    const int64_t vt = kv_same ? 0 : m ? sm.vbase + (int64_t)j0 * sm.vsn : key_elem(sc, sc.vbase, sc.vsn, j0);
-    const char* const kp = uniform_ptr((m ? sm.k : sc.k) + kt * 2);
-    const char* const vp = uniform_ptr((m ? sm.v : sc.v) + vt * 2);
-    const uint32_t krowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.ksn : sc.ksn) * 2u);
-    const uint32_t vrowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.vsn : sc.vsn) * 2u);
-    const uint32_t k0 = lds_addr(kbuf(buf)), v0 = lds_addr(vbuf(buf));
-#pragma unroll
-    for (int j = 0; j < C::NPW; ++j) {
-      const int row = drow0 + j * kBwdNW * C::RPI;
-      const int i = wave + j * kBwdNW;
-      const uint32_t r = (uint32_t)min(row, last);
-      const uint32_t sw = 16u * (uint32_t)((ln % C::CPR) ^ kv_swz<D>(row));
-      dma16_sbase(kp, r * krowb + sw, __builtin_amdgcn_readfirstlane(k0 + i * 1024));
-      if (!kv_same) dma16_sbase(vp, r * vrowb + sw, __builtin_amdgcn_readfirstlane(v0 + i * 1024));
+    } else {
+      // (segment fields picked one by one: a reference to either would put both in memory)
+      const int last = min(kBwdBK, (m ? sm.n : sc.n) - j0) - 1;
+      // row 0 of the tile (a paged context tile is one page): both page lookups before
+      // any load is issued, so their waits wait for nothing else
+      const int64_t kt = m ? sm.kbase + (int64_t)j0 * sm.ksn : key_elem(sc, sc.kbase, sc.ksn, j0);
+      const int64_t vt = kv_same ? 0 : m ? sm.vbase + (int64_t)j0 * sm.vsn : key_elem(sc, sc.vbase, sc.vsn, j0);
+      const char* const kp = uniform_ptr((m ? sm.k : sc.k) + kt * 2);
+      const char* const vp = uniform_ptr((m ? sm.v : sc.v) + vt * 2);
+      const uint32_t krowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.ksn : sc.ksn) * 2u);
+      const uint32_t vrowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.vsn : sc.vsn) * 2u);
+      dma_rows<D, kBwdBK>(kp, krowb, last, lds_addr(kbuf(buf)), wave, lane);
+      if (!kv_same) dma_rows<D, kBwdBK>(vp, vrowb, last, lds_addr(vbuf(buf)), wave, lane);
     }
   };
-  // per-lane LDS byte offsets in a tile: the row fragment (rows 16kb + l16, columns
-  // 32kc + 8g .. +8) is at kb*16*ROWB + 256*(kc/4) + koff[kc%4]; the tr16 fragment of
-  // rows 32ks + 16h + 4g + (l16 >> 2), columns 16db + 4*(l16 & 3) .. +4 at
-  // (32ks + 16h)*ROWB + 256*(db/8) + voff[db%8].  Padded rows (PAD): one base each.
-  int koff[4], voff[8];
-  if constexpr (!C::PAD) {
-    const int ksw = kv_swz<D>(l16);
-#pragma unroll
-    for (int b4 = 0; b4 < 4; ++b4) koff[b4] = l16 * C::ROWB + 16 * ((4 * b4 + gq) ^ ksw);
-    const int vr = 4 * gq + (l16 >> 2);
-    const int vsw = kv_swz<D>(vr);
-    const int x = (l16 & 3) >> 1;
-#pragma unroll
-    for (int db = 0; db < 8; ++db) voff[db] = vr * C::ROWB + 16 * ((2 * db + x) ^ vsw) + 8 * (l16 & 1);
-  }
-  auto row_frag = [&](const char* tile, int kb, int kc) {
-    if constexpr (C::PAD) return *(const v8*)((const T*)tile + (kb * 16 + l16) * (C::ROWB / 2) + kc * 32 + gq * 8);
-    return *(const v8*)(tile + kb * 16 * C::ROWB + 256 * (kc / 4) + koff[kc % 4]);
-  };
-  auto col_frag = [&](const char* tile, int ks, int db) {
-    if constexpr (C::PAD) return tr_frag<T>((const T*)tile, C::ROWB / 2, ks * 32, db, l16, gq);
-    const char* a = tile + ks * 32 * C::ROWB + 256 * (db / 8) + voff[db % 8];
-    const s16x4 lo = lds_read_tr16(a);
-    const s16x4 hi = lds_read_tr16(a + 16 * C::ROWB);
-    return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-  };
+  const TileReader<T, D> tr(l16, gq);
+  auto row_frag = [&](const char* tile, int kb, int kc) { return tr.row(tile, kb, kc); };
+  auto col_frag = [&](const char* tile, int ks, int db) { return tr.col(tile, ks, db); };
   // S^T = K Q^T of a tile: lane (q + 16g) reg r = S[query q][key 16kb + 4g + r]
   auto scores = [&](const char* kt, f32x4 (&s)[C::NKB][QB]) {
 #pragma unroll
@@ -655,10 +688,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   typedef BwdCfg<D> C;
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
-  T* const Qs = (T*)smem_raw;
-  T* const Os = Qs + C::QS * C::RS;  // dO rows
-  float* const lse_s = (float*)(Os + C::QS * C::RS);
-  float* const dl_s = lse_s + C::QS;
+  // step buffer i: QS rows of Q, QS rows of dO (pitch ROWB), then QS lse and QS delta
+  auto qbuf = [&](int i) { return smem_raw + i * C::DKV_SB; };
+  auto obuf = [&](int i) { return smem_raw + i * C::DKV_SB + C::STEPB; };
+  auto lse_s = [&](int i) { return (float*)(smem_raw + i * C::DKV_SB + 2 * C::STEPB); };
+  auto dl_s = [&](int i) { return lse_s(i) + C::QS; };
 
   const bool mla = C::MLA_ONLY || (p.flags & FMLM_FLAG_MLA);
   const int kh = blockIdx.y;
@@ -703,29 +737,16 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     }
 
   // Query steps: (head hq, sequence b, rows [p0, p0 + QS)) over every sequence whose
-  // queries attend to these keys, heads outermost.  A step's rows are loaded into
-  // registers (one step ahead with DKV_PF) and written to LDS between two barriers.
+  // queries attend to these keys, heads outermost.  prep() starts the loads of a step:
+  // its rows by direct loads into step buffer buf (rows past the sequence end repeat its
+  // last row; their lse is +inf, so P = dS = 0) and its lse / delta into registers, which
+  // go to LDS at the top of the step's iteration.  The latent (PAD) stages everything
+  // through registers into its single buffer after the previous step's reads.
   const int hq_lo = ku.shared ? 0 : kh, hq_hi = ku.shared ? p.H : kh + 1;
   const QuerySteps steps{&p, &ku, hq_hi, C::QS};
-  constexpr int QCH = C::QS * C::C8;             // 16-byte chunks per step and tensor
-  constexpr int QPT = (QCH + C::NT - 1) / C::NT;  // ... per thread
-  u32x4 qreg[QPT], dreg[QPT];
   float lreg = INFINITY, dlreg = 0.f;
-  auto fetch = [&](const QStep& st) {
+  auto prep = [&](const QStep& st, int buf) {
     const SeqInfo si = seq_info(p, st.b);
-#pragma unroll
-    for (int li = 0; li < QPT; ++li) {
-      const int it = tid + li * C::NT;
-      const int r = it / C::C8, c8 = it % C::C8;
-      const int pos = st.p0 + r;
-      qreg[li] = u32x4{0u, 0u, 0u, 0u};
-      dreg[li] = qreg[li];
-      if ((QCH % C::NT == 0 || it < QCH) && pos < si.len) {
-        qreg[li] = ld16((const char*)p.q, row_at(p.q_layout, st.b, st.hq, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + c8 * 8);
-        dreg[li] = ld16((const char*)g.dout,
-                        row_at(p.o_layout, st.b, st.hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + c8 * 8);
-      }
-    }
     if (tid < C::QS) {
       const int pos = st.p0 + tid;
       const bool ok = pos < si.len;
@@ -733,32 +754,70 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       lreg = ok ? st_lse[at] : INFINITY;  // padding rows: P = 0
       dlreg = ok ? st_delta[at] : 0.f;
     }
-  };
-  auto stage = [&]() {
+    if constexpr (C::PAD) {
+      constexpr int QCH = C::QS * C::C8;             // 16-byte chunks per step and tensor
+      constexpr int QPT = (QCH + C::NT - 1) / C::NT;  // ... per thread
+      u32x4 qreg[QPT], dreg[QPT];
 #pragma unroll
-    for (int li = 0; li < QPT; ++li) {
-      const int it = tid + li * C::NT;
-      if (QCH % C::NT != 0 && it >= QCH) continue;
-      const int r = it / C::C8, c8 = it % C::C8;
-      *(u32x4*)(Qs + r * C::RS + c8 * 8) = qreg[li];
-      *(u32x4*)(Os + r * C::RS + c8 * 8) = dreg[li];
-    }
-    if (tid < C::QS) {
-      lse_s[tid] = lreg;
-      dl_s[tid] = dlreg;
+      for (int li = 0; li < QPT; ++li) {
+        const int it = tid + li * C::NT;
+        const int r = it / C::C8, c8 = it % C::C8;
+        const int pos = st.p0 + r;
+        qreg[li] = u32x4{0u, 0u, 0u, 0u};
+        dreg[li] = qreg[li];
+        if ((QCH % C::NT == 0 || it < QCH) && pos < si.len) {
+          qreg[li] = ld16((const char*)p.q, row_at(p.q_layout, st.b, st.hq, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + c8 * 8);
+          dreg[li] = ld16((const char*)g.dout,
+                          row_at(p.o_layout, st.b, st.hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + c8 * 8);
+        }
+      }
+#pragma unroll
+      for (int li = 0; li < QPT; ++li) {
+        const int it = tid + li * C::NT;
+        if (QCH % C::NT != 0 && it >= QCH) continue;
+        const int at = (it / C::C8) * C::ROWB + (it % C::C8) * 16;
+        *(u32x4*)(qbuf(buf) + at) = qreg[li];
+        *(u32x4*)(obuf(buf) + at) = dreg[li];
+      }
+      if (tid < C::QS) {
+        lse_s(buf)[tid] = lreg;
+        dl_s(buf)[tid] = dlreg;
+      }
+    } else {
+      const int last = min(C::QS, si.len - st.p0) - 1;
+      const int64_t qe = row_at(p.q_layout, st.b, st.hq, si.q0, st.p0, p.q_sb, p.q_sh, p.q_sn);
+      const int64_t de = row_at(p.o_layout, st.b, st.hq, si.q0, st.p0, g.do_sb, g.do_sh, g.do_sn);
+      dma_rows<D, C::QS>(uniform_ptr((const char*)p.q + qe * 2), __builtin_amdgcn_readfirstlane((uint32_t)p.q_sn * 2u),
+                         last, lds_addr(qbuf(buf)), wave, lane);
+      dma_rows<D, C::QS>(uniform_ptr((const char*)g.dout + de * 2),
+                         __builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), last, lds_addr(obuf(buf)), wave, lane);
     }
   };
+  const TileReader<T, D> tr(l16, gq);
 
   QStep cur = steps.first_from(hq_lo, ku.b_lo);
-  if (C::DKV_PF && cur.hq < hq_hi) fetch(cur);
+  int buf = 0;
+  if constexpr (!C::PAD)
+    if (cur.hq < hq_hi) prep(cur, 0);
   while (cur.hq < hq_hi) {
     const QStep nxt = steps.next(cur);
     const int lim = ku.causal_main ? seq_info(p, cur.b).mainlen : 0x7fffffff;
-    __syncthreads();  // the previous step's LDS reads are done
-    if (!C::DKV_PF) fetch(cur);
-    stage();
-    __syncthreads();
-    if (C::DKV_PF && nxt.hq < hq_hi) fetch(nxt);
+    if constexpr (C::PAD) {
+      __syncthreads();  // the previous step's LDS reads are done
+      prep(cur, 0);
+    } else if (tid < C::QS) {  // this buffer's statistics were last read two steps ago
+      lse_s(buf)[tid] = lreg;
+      dl_s(buf)[tid] = dlreg;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the step have landed
+    __syncthreads();                // ... and every other wave's
+    // the other buffer was last read by the previous step, which every wave has finished
+    if constexpr (!C::PAD)
+      if (nxt.hq < hq_hi) prep(nxt, buf ^ 1);
+    const char* const qt = qbuf(buf);
+    const char* const ot = obuf(buf);
+    const float* const ls = lse_s(buf);
+    const float* const dls = dl_s(buf);
 
     // per 32-row group: S and dP for its two 16-row halves (lane (key + 16g) reg r = row
     // 32grp + 16h + 4g + r), P and dS packed as B operands (element 4h + r), then the
@@ -776,16 +835,16 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       }
 #pragma unroll
       for (int kc = 0; kc < C::KC; ++kc) {
-        const v8 aq = *(const v8*)(Qs + (grp * 32 + hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
-        const v8 ao = *(const v8*)(Os + (grp * 32 + hh * 16 + l16) * C::RS + kc * 32 + gq * 8);
+        const v8 aq = tr.row(qt, grp * 2 + hh, kc);
+        const v8 ao = tr.row(ot, grp * 2 + hh, kc);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           sc[kb] = Mfma<T>::run(aq, kf[kb][kc], sc[kb]);
           dp[kb] = Mfma<T>::run(ao, vf[kb][kc], dp[kb]);
         }
       }
-      const f32x4 L4 = *(const f32x4*)(lse_s + grp * 32 + hh * 16 + gq * 4);
-      const f32x4 D4 = *(const f32x4*)(dl_s + grp * 32 + hh * 16 + gq * 4);
+      const f32x4 L4 = *(const f32x4*)(ls + grp * 32 + hh * 16 + gq * 4);
+      const f32x4 D4 = *(const f32x4*)(dls + grp * 32 + hh * 16 + gq * 4);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const bool kvalid = kok[kb] && key[kb] < lim;
@@ -800,8 +859,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     // dV^T += dO^T P and dK^T += Q^T dS (MLA: both into dK)
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db) {
-      const v8 ao = tr_frag<T>(Os, C::RS, grp * 32, db, l16, gq);
-      const v8 aq = tr_frag<T>(Qs, C::RS, grp * 32, db, l16, gq);
+      const v8 ao = tr.col(ot, grp, db);
+      const v8 aq = tr.col(qt, grp, db);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         if (mla) {
@@ -813,6 +872,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       }
     }
     }
+    if constexpr (!C::PAD) buf ^= 1;
     cur = nxt;
   }
 
