@@ -417,8 +417,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   extern __shared__ __align__(16) char smem_raw[];
 
   const UnitTables ut = unit_tables(p, g);
-  const int u = blockIdx.x, h = blockIdx.y;
-  if (u >= ut.q[p.B]) return;
+  // causal_query_seq_attn: later sequences see more keys, so their tiles go first (the
+  // grid is dispatched in blockIdx.x order; the last workgroups then are short ones)
+  const int u = (p.flags & FMLM_FLAG_CAUSAL_SEQ) ? ut.q[p.B] - 1 - (int)blockIdx.x : (int)blockIdx.x;
+  const int h = blockIdx.y;
+  if (u < 0 || u >= ut.q[p.B]) return;
   const int b = find_seq(ut.q, p.B, u);
   const SeqInfo si = seq_info(p, b);
   const int qpos0 = (u - ut.q[b]) * C::BQ;
@@ -955,8 +958,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_p
   float* const Vf = Kf + C::DQK * D;
 
   const UnitTables ut = unit_tables(p, g);
-  const int u = blockIdx.x, h = blockIdx.y;
-  if (u >= ut.q[p.B]) return;
+  // causal_query_seq_attn: later sequences see more keys, so their tiles go first (the
+  // grid is dispatched in blockIdx.x order; the last workgroups then are short ones)
+  const int u = (p.flags & FMLM_FLAG_CAUSAL_SEQ) ? ut.q[p.B] - 1 - (int)blockIdx.x : (int)blockIdx.x;
+  const int h = blockIdx.y;
+  if (u < 0 || u >= ut.q[p.B]) return;
   const int b = find_seq(ut.q, p.B, u);
   const SeqInfo si = seq_info(p, b);
   const int qpos0 = (u - ut.q[b]) * C::R;
