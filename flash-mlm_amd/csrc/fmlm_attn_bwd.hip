@@ -258,21 +258,24 @@ FMLM_DEV void dma_rows(const char* src, uint32_t rowb, int last, uint32_t lds, i
 }
 
 // ---------------------------------------------------------------------------
-// Unit tables.  The workspace holds, after the row statistics (2*H*total_q floats), three
-// exclusive prefix sums of tile counts: query tiles of BQ rows per sequence (B + 1),
-// key tiles of DKV_KEYS rows per sequence (B + 1) and per context batch (n_ctx + 1).  A
+// Unit tables.  The workspace holds, after the row statistics (2*H*total_q floats), an
+// order of the sequences (B ints, see bwd_units_kernel) and three exclusive prefix sums
+// of tile counts: query tiles of BQ rows per sequence in that order (B + 1), key tiles
+// of DKV_KEYS rows per sequence (B + 1) and per context batch (n_ctx + 1).  A
 // workgroup maps its linear unit id to (sequence or batch, tile) by binary search, so
 // the grids hold only real tiles plus a bound of one per sequence / batch.
 // ---------------------------------------------------------------------------
 struct UnitTables {
-  int32_t* q;  // [B + 1]
-  int32_t* k;  // [B + 1]
-  int32_t* c;  // [n_ctx + 1]
+  int32_t* perm;  // [B]: the sequence of query-table entry r
+  int32_t* q;     // [B + 1], over the sequences in perm order
+  int32_t* k;     // [B + 1]
+  int32_t* c;     // [n_ctx + 1]
 };
 
 FMLM_DEV UnitTables unit_tables(const fmlm_attn_params& p, const fmlm_attn_grads& g) {
   UnitTables t;
-  t.q = (int32_t*)((char*)g.workspace + 2 * (int64_t)p.H * p.total_q * 4);
+  t.perm = (int32_t*)((char*)g.workspace + 2 * (int64_t)p.H * p.total_q * 4);
+  t.q = t.perm + p.B;
   t.k = t.q + p.B + 1;
   t.c = t.k + p.B + 1;
   return t;
@@ -305,11 +308,40 @@ FMLM_DEV void scan_tiles(int n, int tile, LenFn len, int32_t* out, int32_t* part
   __syncthreads();
 }
 
+// keys a query row of sequence b attends to (context, then its own or causal main keys)
+FMLM_DEV int dq_keys(const fmlm_attn_params& p, int b) {
+  int c0 = 0, c1 = 0;
+  if (!(p.flags & FMLM_FLAG_PREFILL) && p.k_ctx) ctx_range(p, ctx_batch_of(p, b), c0, c1);
+  const SeqInfo si = seq_info(p, b);
+  const bool causal = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q;
+  return max(c1 - c0, 0) + (causal ? si.mainlen : si.len);
+}
+
+// Sequences ranked by key count, largest first (ties by index), up to this many; the
+// dq kernel's query table follows that order, so the workgroups dispatched last (the
+// grid runs in blockIdx.x order) are the short ones.  More sequences keep their order.
+constexpr int kRankMax = 1024;
+
 __global__ __launch_bounds__(kScanThreads) void bwd_units_kernel(const fmlm_attn_params p, const fmlm_attn_grads g,
                                                                  int bq, int bk, int n_ctx) {
   __shared__ int32_t part[kScanThreads];
+  __shared__ int32_t s_keys[kRankMax], s_perm[kRankMax];
   const UnitTables t = unit_tables(p, g);
-  scan_tiles(p.B, bq, [&](int b) { return seq_info(p, b).len; }, t.q, part);
+  const int tid = threadIdx.x;
+  const bool ranked = p.B <= kRankMax;
+  if (ranked) {
+    for (int b = tid; b < p.B; b += kScanThreads) s_keys[b] = dq_keys(p, b);
+    __syncthreads();
+    for (int b = tid; b < p.B; b += kScanThreads) {
+      const int kb = s_keys[b];
+      int r = 0;
+      for (int j = 0; j < p.B; ++j) r += (s_keys[j] > kb) || (s_keys[j] == kb && j < b);
+      s_perm[r] = b;  // ranks are a permutation of [0, B)
+    }
+    __syncthreads();
+  }
+  for (int r = tid; r < p.B; r += kScanThreads) t.perm[r] = ranked ? s_perm[r] : r;
+  scan_tiles(p.B, bq, [&](int r) { return seq_info(p, ranked ? s_perm[r] : r).len; }, t.q, part);
   scan_tiles(p.B, bk, [&](int b) { return seq_info(p, b).len; }, t.k, part);
   scan_tiles(n_ctx, bk, [&](int cb) {
     int c0, c1;
@@ -417,14 +449,12 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   extern __shared__ __align__(16) char smem_raw[];
 
   const UnitTables ut = unit_tables(p, g);
-  // causal_query_seq_attn: later sequences see more keys, so their tiles go first (the
-  // grid is dispatched in blockIdx.x order; the last workgroups then are short ones)
-  const int u = (p.flags & FMLM_FLAG_CAUSAL_SEQ) ? ut.q[p.B] - 1 - (int)blockIdx.x : (int)blockIdx.x;
-  const int h = blockIdx.y;
-  if (u < 0 || u >= ut.q[p.B]) return;
-  const int b = find_seq(ut.q, p.B, u);
+  const int u = blockIdx.x, h = blockIdx.y;
+  if (u >= ut.q[p.B]) return;
+  const int rk = find_seq(ut.q, p.B, u);  // table entry: sequences by key count, largest first
+  const int b = ut.perm[rk];
   const SeqInfo si = seq_info(p, b);
-  const int qpos0 = (u - ut.q[b]) * C::BQ;
+  const int qpos0 = (u - ut.q[rk]) * C::BQ;
   if (qpos0 >= si.len) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
@@ -958,14 +988,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_p
   float* const Vf = Kf + C::DQK * D;
 
   const UnitTables ut = unit_tables(p, g);
-  // causal_query_seq_attn: later sequences see more keys, so their tiles go first (the
-  // grid is dispatched in blockIdx.x order; the last workgroups then are short ones)
-  const int u = (p.flags & FMLM_FLAG_CAUSAL_SEQ) ? ut.q[p.B] - 1 - (int)blockIdx.x : (int)blockIdx.x;
-  const int h = blockIdx.y;
-  if (u < 0 || u >= ut.q[p.B]) return;
-  const int b = find_seq(ut.q, p.B, u);
+  const int u = blockIdx.x, h = blockIdx.y;
+  if (u >= ut.q[p.B]) return;
+  const int rk = find_seq(ut.q, p.B, u);  // table entry: sequences by key count, largest first
+  const int b = ut.perm[rk];
   const SeqInfo si = seq_info(p, b);
-  const int qpos0 = (u - ut.q[b]) * C::R;
+  const int qpos0 = (u - ut.q[rk]) * C::R;
   if (qpos0 >= si.len) return;
   const int tid = threadIdx.x, row = tid / C::TPR, d0 = (tid % C::TPR) * C::DPT;
   const int pos = qpos0 + row;
@@ -1299,8 +1327,10 @@ extern "C" int fmlm_attn_grads_size(void) { return (int)sizeof(fmlm_attn_grads);
 
 extern "C" int64_t fmlm_attn_bwd_workspace_bytes(const fmlm_attn_params* p) {
   if (!p || p->H < 0 || p->total_q < 0 || p->B < 0 || p->ctx_batch < 0) return FMLM_E_ARG;
-  // row statistics, then the unit tables (B + 1, B + 1, context batches + 1 ints)
-  const int64_t bytes = 2 * (int64_t)p->H * p->total_q * 4 + 4 * (2 * ((int64_t)p->B + 1) + (p->ctx_batch > 1 ? p->ctx_batch : 1) + 1);
+  // row statistics, then the sequence order (B ints) and the unit tables (B + 1, B + 1,
+  // context batches + 1 ints)
+  const int64_t bytes = 2 * (int64_t)p->H * p->total_q * 4 +
+                        4 * ((int64_t)p->B + 2 * ((int64_t)p->B + 1) + (p->ctx_batch > 1 ? p->ctx_batch : 1) + 1);
   return (bytes + 255) / 256 * 256;
 }
 

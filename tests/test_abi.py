@@ -77,7 +77,7 @@ def test_argument_rejection_without_launch():
     assert lib.fmlm_attn_bwd(p, g, None) == -5  # no workspace
     assert lib.fmlm_attn_bwd_workspace_bytes(p) == 256  # 2 floats per (head, row) + tile tables, rounded up
     p.H, p.total_q = 8, 4096
-    assert lib.fmlm_attn_bwd_workspace_bytes(p) == (2 * 8 * 4096 * 4 + 4 * (2 * 2 + 1 + 1) + 255) // 256 * 256
+    assert lib.fmlm_attn_bwd_workspace_bytes(p) == (2 * 8 * 4096 * 4 + 4 * (1 + 2 * 2 + 1 + 1) + 255) // 256 * 256
     p.q = 264  # not 16-byte aligned
     assert lib.fmlm_attn_bwd(p, g, None) == -4
     with pytest.raises(RuntimeError, match="invalid argument"):
