@@ -485,3 +485,24 @@ def test_backward_rejects_inputs_changed_in_place(device):
             (q if target == "q" else kc).mul_(2.0)
         with pytest.raises(RuntimeError, match="modified by an inplace operation"):
             out.sum().backward()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_more_sequences_than_the_rank_limit(causal, device):
+    # the dq kernel visits sequences by key count for up to 1024 of them and in index
+    # order beyond: 1030 short sequences (some empty) take the second path
+    gen = torch.Generator().manual_seed(7300 + causal)
+    lengths = torch.randint(0, 4, (1030,), generator=gen).tolist()
+    B, H, N, D = len(lengths), 1, 4, 32
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_leaf((B, H, N, D), torch.bfloat16, device, gen) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, None, None, block_n=64, causal_query_seq_attn=causal)
+    dout = torch.randn(out.shape, generator=gen).to(torch.bfloat16).to(device)
+    out.backward(dout)
+    from flash_mlm import unpack_from_kernel
+    g = ar.mlm_attention_packed_backward(_np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)), lengths,
+                                         scale, causal_query_seq_attn=causal)
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk")
+    _close(v.grad, g[2], "dv")
