@@ -243,7 +243,8 @@ __global__ __launch_bounds__(256) void unpack_kernel(const char* __restrict__ pa
 // elements) go to rows [dst_start[c], dst_start[c] + len) of dst (head stride dst_sh).
 // Lengths and starts are clamped to the row counts of src and dst, so inconsistent offsets
 // cannot address outside either tensor.  The row blocks stride over the segment, so the
-// grid does not depend on segment lengths the host has not read.
+// grid does not depend on segment lengths the host has not read.  A null src writes zero
+// rows (src_rows then only bounds the segment offsets).
 // ---------------------------------------------------------------------------
 template <int VB>
 __global__ __launch_bounds__(256) void segment_copy_kernel(const char* __restrict__ src, int64_t src_sh,
@@ -257,9 +258,14 @@ __global__ __launch_bounds__(256) void segment_copy_kernel(const char* __restric
   const int s0 = min(max(src_cu[c], 0), src_rows);
   const int d0 = min(max(dst_start[c], 0), dst_rows);
   const int len = min(min(src_cu[c + 1] - s0, src_rows - s0), dst_rows - d0);
-  const char* const sbase = src + ((int64_t)h * src_sh + (int64_t)s0 * D) * esz;
   char* const dbase = dst + ((int64_t)h * dst_sh + (int64_t)d0 * D) * esz;
   const int64_t row_bytes = (int64_t)D * esz;
+  if (!src) {
+    for (int r = blockIdx.x * blockDim.y + threadIdx.y; r < len; r += gridDim.x * blockDim.y)
+      for (int k = threadIdx.x; k < cpr; k += blockDim.x) *(V*)(dbase + (int64_t)r * row_bytes + (int64_t)k * VB) = V{};
+    return;
+  }
+  const char* const sbase = src + ((int64_t)h * src_sh + (int64_t)s0 * D) * esz;
   for (int r = blockIdx.x * blockDim.y + threadIdx.y; r < len; r += gridDim.x * blockDim.y)
     for (int k = threadIdx.x; k < cpr; k += blockDim.x)
       *(V*)(dbase + (int64_t)r * row_bytes + (int64_t)k * VB) = *(const V*)(sbase + (int64_t)r * row_bytes + (int64_t)k * VB);
@@ -413,7 +419,7 @@ extern "C" int fmlm_copy_segments(int32_t elem_bytes, const void* src, int64_t s
   if (!valid_elem_bytes(esz)) return FMLM_E_DTYPE;
   if (C < 0 || H < 0 || D < 1 || src_rows < 0 || dst_rows < 0 || src_sh < 0 || dst_sh < 0) return FMLM_E_ARG;
   if ((int64_t)C * H == 0 || src_rows == 0 || dst_rows == 0) return 0;
-  if (!src || !dst || !src_cu || !dst_start) return FMLM_E_ARG;
+  if (!dst || !src_cu || !dst_start) return FMLM_E_ARG;
   if (H > 65535 || C > 65535) return FMLM_E_ARG;
   const int vb = pick_vec((int64_t)D * esz, {(uint64_t)src, (uint64_t)dst, (uint64_t)(src_sh * esz),
                                              (uint64_t)(dst_sh * esz)});

@@ -357,9 +357,11 @@ class InferenceCache:
         for MLA (``v_cache`` must be None), else [H * T_new, D].  Batch c's new rows are
         ``cu_seqlens_kv[c] .. cu_seqlens_kv[c+1]``.  The entry becomes [old rows of c ||
         new rows of c] for every batch c: new buffers of T_old + T_new rows per head, and
-        cu_seqlens_kv = old + new offsets.  Rows per head past the last batch are left
-        unwritten (nothing attends to them).  The copy is a HIP segment copy per tensor and
-        source, stream-ordered; nothing is read back to the host.
+        cu_seqlens_kv = old + new offsets.  Rows per head past the last batch are zero, as
+        the zero padding rows of a prefilled packed entry are: a later call that asks for a
+        shared context (``context_batch_size=1``) attends to every row of the entry.  The
+        copy is a HIP segment copy per tensor and source, stream-ordered; nothing is read
+        back to the host.
         """
         key = self._layer_key(layer_id)
         entry = self._layer_kv.get(key)
@@ -399,6 +401,9 @@ class InferenceCache:
         start_old = cu_out[:-1].contiguous()            # batch c's old rows open its segment
         start_new = (cu_old[1:] + cu_new[:-1]).contiguous()  # its new rows follow them
         rows = t_old + t_new
+        # rows [cu_out[-1], rows) of each head: one zero segment, sized on the device
+        tail_cu = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev), rows - cu_out[-1:]])
+        tail_start = cu_out[-1:].contiguous()
 
         def merged(old: torch.Tensor, new: torch.Tensor) -> torch.Tensor:
             out = torch.empty((h_kv * rows, d), dtype=entry.dtype, device=dev)
@@ -407,6 +412,8 @@ class InferenceCache:
                 new = new.contiguous()
                 copy_segments(old, t_old, cu_old, out, rows, start_old, n_batch, h_kv, d)
                 copy_segments(new, t_new, cu_new, out, rows, start_new, n_batch, h_kv, d)
+            if rows > 0:
+                copy_segments(None, rows, tail_cu, out, rows, tail_start, 1, h_kv, d)
             return out
 
         k_out = merged(entry.k_cache, k_cache)

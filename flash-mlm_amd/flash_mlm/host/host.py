@@ -308,9 +308,11 @@ def _prepare(
     stream = _lib.stream_of(q.device)
     with _device_scope(q.device):
         if ws_bytes > 0 and schedule_cache is not None:
-            # what the unit list depends on (the kernel and its tile size, the heads);
-            # context lengths only steer where key ranges are split
-            key = (p.dtype, D, B, H, total_q, p.flags, p.kv_layout)
+            # what the unit list depends on: the kernel (dtype, head dim, flags, K/V
+            # layout, paged context or not), whose tile size and occupancy fix the slots,
+            # the split records and the grid, and the shape (B, H, N, total_q); context
+            # lengths only steer where key ranges are split
+            key = (p.dtype, D, B, H, N, total_q, p.flags, p.kv_layout, block_table is not None)
             sched = schedule_cache.get(key)
             if sched is None:
                 sched = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
@@ -875,12 +877,14 @@ def _precompressed_impl(
         )
 
     if prefill and inference_cache is not None:
+        # the contiguous tensors the kernel read, as the reference stores its
+        # make_contiguous copies (host.py:663-683, 777-786)
         inference_cache.prefill_kv_cache(
             layer_id,
-            k_cache=k,
-            v_cache=None if is_mla else v,
+            k_cache=k_,
+            v_cache=None if is_mla else v_,
             total_context_len=int(total_q_len),
-            cu_seqlens_kv=cu_seqlens_q,
+            cu_seqlens_kv=cu_seqlens_q.contiguous(),
             context_batch_size=b,
             is_mla=is_mla,
             num_heads=num_heads,

@@ -665,17 +665,18 @@ def unpack_from_kernel(packed: torch.Tensor, meta: PackMetadata, H: int):
     return out
 
 
-def copy_segments(src: torch.Tensor, src_rows: int, src_cu: torch.Tensor, dst: torch.Tensor, dst_rows: int,
+def copy_segments(src: torch.Tensor | None, src_rows: int, src_cu: torch.Tensor, dst: torch.Tensor, dst_rows: int,
                   dst_start: torch.Tensor, C: int, H: int, D: int) -> None:
     """Head-major segment copy on the GPU (one HIP launch): for head h and segment c,
     rows src_cu[c]..src_cu[c+1] of head h of ``src`` ([H * src_rows, D]) go to rows
-    dst_start[c].. of head h of ``dst`` ([H * dst_rows, D]).  The kernel of
-    :meth:`InferenceCache.append_kv_cache`; no counterpart in the reference."""
+    dst_start[c].. of head h of ``dst`` ([H * dst_rows, D]); ``src=None`` writes zero rows
+    there instead.  The kernel of :meth:`InferenceCache.append_kv_cache`; no counterpart in
+    the reference."""
     _require_device(src, dst, src_cu, dst_start, what="copy_segments")
     lib = _lib.load()
     with _device_scope(dst.device):
         rc = lib.fmlm_copy_segments(
-            src.element_size(), src.data_ptr(), src_rows * D, src_rows, src_cu.data_ptr(),
+            dst.element_size(), None if src is None else src.data_ptr(), src_rows * D, src_rows, src_cu.data_ptr(),
             dst.data_ptr(), dst_rows * D, dst_rows, dst_start.data_ptr(), C, H, D, _lib.stream_of(dst.device),
         )
     _lib.check(rc, "fmlm_copy_segments")

@@ -140,6 +140,8 @@ FMLM_API int fmlm_unpack(int32_t elem_bytes, const void* packed, int64_t p_sh, v
  * head h < H and segment c < C, rows [src_cu[c], src_cu[c+1]) of src (row h*src_sh/D +
  * i) go to rows [dst_start[c], dst_start[c] + len) of dst (row h*dst_sh/D + i); rows are
  * D elements of elem_bytes.  Offsets are clamped to src_rows / dst_rows rows per head.
+ * src == NULL writes zero rows instead (the same segments of dst; src_rows still bounds
+ * the offsets src_cu).
  * No counterpart in the reference, which replaces a layer's context on prefill and lists
  * appends with paged KV on its roadmap (README.md:34-41).
  * ------------------------------------------------------------------------- */

@@ -115,8 +115,8 @@ def append_segments(old: np.ndarray, cu_old, new: np.ndarray, cu_new, heads: int
     lists appends with paged KV, README.md:34-41): head-major caches old [heads*T_old, D]
     and new [heads*T_new, D] with per-batch offsets cu_old / cu_new -> (merged
     [heads*(T_old+T_new), D], cu_out) where batch c of every head holds its old rows then
-    its new rows, cu_out = cu_old + cu_new.  Rows past cu_out[-1] are zero here (the
-    GPU leaves them unwritten)."""
+    its new rows, cu_out = cu_old + cu_new.  Rows past cu_out[-1] of every head are zero,
+    like the zero padding rows of a prefilled packed entry."""
     cu_old = np.asarray(cu_old, dtype=np.int64)
     cu_new = np.asarray(cu_new, dtype=np.int64)
     D = old.shape[1]

@@ -65,9 +65,51 @@ def test_append_matches_oracle_bit_exact(dtype, mla, device):
     np.testing.assert_array_equal(_np(e.cu_seqlens_kv), ref_cu)
     rows = e.total_context_len
     np.testing.assert_array_equal(_owned(_np(e.k_cache.float()), ref_cu, rows, h_kv), _owned(ref_k, ref_cu, rows, h_kv))
+    # the whole buffer, rows past the last batch (zero) included
+    np.testing.assert_array_equal(_np(e.k_cache.float()), ref_k)
     if not mla:
         ref_v, _ = pack_ref.append_segments(_np(v0.float()), _np(cu0), _np(v1.float()), _np(cu1), h_kv)
         np.testing.assert_array_equal(_owned(_np(e.v_cache.float()), ref_cu, rows, h_kv), _owned(ref_v, ref_cu, rows, h_kv))
+        np.testing.assert_array_equal(_np(e.v_cache.float()), ref_v)
+
+
+@pytest.mark.parametrize("mla", [False, True])
+def test_append_then_shared_context(mla, device):
+    """An appended multi-batch entry read as a shared context (context_batch_size=1): every
+    sequence attends to all rows of every head, cu_seqlens_kv = [0, total]
+    (host_utils.py:232-237), so the rows past the last batch must be the zeros a prefilled
+    packed entry holds there.  Checked against the oracle over the oracle's merge."""
+    torch.manual_seed(5300 + mla)
+    dtype, H, N = torch.bfloat16, 2, 80
+    D = 512 if mla else 64
+    lengths = [80, 33, 5]
+    B = len(lengths)
+    h_kv = 1 if mla else H
+    cache = InferenceCache()
+    # 4 padding rows per head past the last batch, filled with non-zero values: the append
+    # must not carry them over as they are
+    k0, v0, cu0 = _entry(cache, H=H, D=D, mla=mla, dtype=dtype, device=device, lengths=[20, 0, 45], extra_rows=4)
+    new_len = [3, 17, 0]
+    cu1 = _cu(new_len)
+    t1 = int(cu1[-1])
+    k1 = torch.randn((h_kv * t1, D), device=device).to(dtype)
+    v1 = None if mla else torch.randn((h_kv * t1, D), device=device).to(dtype)
+    # make the old padding rows zero in the oracle's input: the merged entry's tail is zero
+    rows0 = k0.shape[0] // h_kv
+    mk, mcu = pack_ref.append_segments(_np(k0.float()), _np(cu0), _np(k1.float()), _np(cu1), h_kv)
+    mv = None if mla else pack_ref.append_segments(_np(v0.float()), _np(cu0), _np(v1.float()), _np(cu1), h_kv)[0]
+    cache.append_kv_cache(0, k_cache=k1, v_cache=v1, cu_seqlens_kv=cu1.to(device))
+    Tc = rows0 + t1
+    assert cache._layer_kv["0"].total_context_len == Tc
+    q, kq, vq = (torch.randn((B, H, N, D), device=device).to(dtype) * (0.5 if mla else 1.0) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    scale = 1.0 / math.sqrt(D)
+    out = flash_attn_mlm_compressed(q, kq, vq, H, meta, scale, cache, 0, is_mla=mla, block_n=64,
+                                    context_batch_size=1)
+    ref = ar.mlm_attention_packed(_np(q.float()), _np(kq.float()), _np(vq.float()), lengths, scale, is_mla=mla,
+                                  k_cache=mk, v_cache=mv, cu_seqlens_kv=[0, Tc], total_context_len=Tc,
+                                  context_batch_size=1)
+    np.testing.assert_allclose(_np(unpack_from_kernel(out, meta, H).float()), ref, atol=1e-2, rtol=1e-2)
 
 
 @pytest.mark.parametrize("mla", [False, True])

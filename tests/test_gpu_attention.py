@@ -274,6 +274,49 @@ def test_precompressed_prefill_stores_cache_entry(is_mla, device):
     _close(unpack_from_kernel(out, meta, H), _packed_oracle(q, k, v, [20, 7], 0.55, is_mla=is_mla, prefill=True))
 
 
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_precompressed_prefill_non_contiguous_kv(is_mla, device):
+    # packed k / v given as strided views (row stride 2*D): the prefill stores the
+    # contiguous copies the kernel read, as the reference stores its make_contiguous
+    # outputs (host.py:663-683, 777-786), and a later call attends to them as context
+    torch.manual_seed(53)
+    B, H, N, D = 3, 2, 40, 64
+    lens = [40, 9, 23]
+    lengths = torch.tensor(lens, device=device, dtype=torch.int32)
+    q, k = _randn((B, H, N, D), device), _randn((B, H, N, D), device)
+    v = k if is_mla else _randn((B, H, N, D), device)
+    meta = build_pack_metadata(lengths, N, block_n=32)
+    q_p, k_p, v_p = _prepack(q, k, v, meta, is_mla)
+
+    def strided(x):
+        wide = torch.zeros((x.shape[0], 2 * D), dtype=x.dtype, device=x.device)
+        wide[:, :D] = x
+        return wide[:, :D]
+
+    k_s = strided(k_p)
+    v_s = k_s if is_mla else strided(v_p)
+    assert not k_s.is_contiguous()
+    cache = InferenceCache()
+    T = q_p.shape[0] // H
+    kw = dict(num_heads=H, total_q_len=T, cu_seqlens_q=meta.cu_seqlens, batch_ids_q=meta.batch_ids_q,
+              q_tile_starts_q=meta.q_tile_starts_q, scale=0.5, inference_cache=cache, layer_id=3, is_mla=is_mla,
+              block_m=32, block_n=32)
+    out = flash_attn_mlm_precompressed(q_p, k_s, v_s, prefill=True, **kw)
+    _close(unpack_from_kernel(out, meta, H), _packed_oracle(q, k, v, lens, 0.5, is_mla=is_mla, prefill=True))
+    stored = cache.get_kv_cache(3, is_mla=is_mla, num_heads=H, head_dim=D, dtype=q.dtype, device=q.device)
+    assert stored.k_cache.is_contiguous() and torch.equal(stored.k_cache, k_p)
+    if not is_mla:
+        assert stored.v_cache.is_contiguous() and torch.equal(stored.v_cache, v_p)
+    # second call: fresh queries attend to [stored context of b || main keys of b]
+    q2, k2 = _randn((B, H, N, D), device), _randn((B, H, N, D), device)
+    v2 = k2 if is_mla else _randn((B, H, N, D), device)
+    q2_p, k2_p, v2_p = _prepack(q2, k2, v2, meta, is_mla)
+    out2 = flash_attn_mlm_precompressed(q2_p, k2_p, v2_p, **kw)
+    ref = _packed_oracle(q2, k2, v2, lens, 0.5, is_mla=is_mla, k_cache=k_p, v_cache=v_p,
+                         cu_kv=meta.cu_seqlens.cpu(), cbs=B, Tc=T)
+    _close(unpack_from_kernel(out2, meta, H), ref)
+
+
 # ---------------------------------------------------------------------------
 # wider coverage
 # ---------------------------------------------------------------------------
