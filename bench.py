@@ -8,15 +8,15 @@ HBM: for the default workload (packed varlen fp16 with a
 full-batch cached context) that is flash_attn_mlm_compressed + unpack_from_kernel
 (pack metadata is built once and memoised, as in the reference's own benchmark).
 Prints one JSON line: effective attention TFLOP/s (padding excluded, formula
-4*H*D*sum_b Lq_b*(Lctx_b + Lmain_b)), ms per step, the attention kernel's roofline
-fraction against the MI355X dense fp16/bf16 MFMA peak (kernel time: median of HIP-event
-timings on its launch stream, L2/MALL flushed before each launch), the kernel's HBM bytes
-per launch from two
+4*H*D*sum_b Lq_b*(Lctx_b + Lmain_b)), ms per step, the host time of one API call, the
+attention kernel's roofline fraction against the MI355X dense fp16/bf16 MFMA peak
+(kernel time: mean of HIP-event timings on its launch stream over back-to-back launches;
+also with L2/MALL flushed before each launch), the kernel's HBM bytes per launch from two
 rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE) run as child processes before this
 process touches the GPU, each scaled by the counter's reading for a 256 MiB copy, the
-HBM rate of the pack and unpack kernels on the same tensors ("hbm_kernels"), and the
-reference's per-sequence PyTorch SDPA path timed on this host's CPU cores as a reported
-baseline.
+HBM rate and counter-measured bytes of the pack, unpack and KV-append kernels on the same
+tensors ("hbm_kernels"), and the reference's per-sequence PyTorch SDPA path and eager
+per-(sequence, head) path timed on this host's CPU cores as a reported baseline.
 
 The configs (BASELINE.json "configs") are built by `make_case`, which the GPU tests
 reuse for parity checks.
@@ -261,25 +261,57 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
     raise ValueError(f"unknown config {cfg}")
 
 
-def _time_steps(case: "Case", steps: int, warmup: int) -> tuple[float, float]:
-    """(ms per step, mean attention-call ms): K steps back to back between two device
-    synchronisations, with HIP events on the launch stream around the attention call of
-    every timed step (the kernel, plus the split merge where there is one)."""
+def _median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
+
+
+def _time_steps(case: "Case", steps: int, warmup: int) -> tuple[float, float, float]:
+    """(ms per step, median host us of the attention API call, median host us of a whole
+    step): K steps back to back between two device synchronisations.  The host times are
+    what the Python API costs the caller per call (validation, parameter block, launch);
+    the launches are asynchronous, so they overlap the GPU's work."""
     for _ in range(warmup):
         case.step()
-    stream = torch.cuda.current_stream()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
+    call_us, step_us = [], []
     t0 = time.perf_counter()
-    for e0, e1 in events:
-        e0.record(stream)
+    for _ in range(steps):
+        a = time.perf_counter()
         out = case.call()
-        e1.record(stream)
+        b = time.perf_counter()
         if case.post is not None:
             case.post(out)
+        call_us.append((b - a) * 1e6)
+        step_us.append((time.perf_counter() - a) * 1e6)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    return ms, sum(e0.elapsed_time(e1) for e0, e1 in events) / steps
+    return ms, _median(call_us), _median(step_us)
+
+
+def _launch_stream(attention):
+    return torch.cuda.ExternalStream(attention.stream) if attention.stream else torch.cuda.current_stream()
+
+
+def _kernel_device_ms(attention, reps: int) -> tuple[float, float]:
+    """Device time of the prepared attention launch (the kernel, plus the split merge where
+    there is one): `reps` launches back to back on the kernel's launch stream with HIP
+    events recorded on that stream around each.  The host enqueues a launch in well under
+    a kernel's duration, so the queue stays full and no host time falls inside an event
+    pair.  Returns (mean, median) in ms."""
+    stream = _launch_stream(attention)
+    for _ in range(5):
+        attention()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for e0, e1 in events:
+            e0.record(stream)
+            attention()
+            e1.record(stream)
+    torch.cuda.synchronize()
+    times = [e0.elapsed_time(e1) for e0, e1 in events]
+    return sum(times) / len(times), _median(times)
 
 
 FLUSH_BYTES = 512 << 20  # > the 256 MB MALL (and the 4 MB L2s)
@@ -289,7 +321,7 @@ def _kernel_ms(attention, reps: int) -> tuple[float, float]:
     """Attention-kernel duration from HIP events recorded on the kernel's launch stream
     around each of `reps` prepared launches, with L2/MALL flushed before every launch by
     writing a 512 MiB buffer.  Returns (median, mean) in ms."""
-    stream = torch.cuda.ExternalStream(attention.stream) if attention.stream else torch.cuda.current_stream()
+    stream = _launch_stream(attention)
     flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
     for _ in range(3):
         attention()
@@ -308,10 +340,26 @@ def _kernel_ms(attention, reps: int) -> tuple[float, float]:
 COPY_KIB = (256 << 20) / 1024  # the --profile driver's calibration copy
 
 
+def _kernel_class(name: str) -> str | None:
+    """Which measured kernel a rocprofv3 dispatch belongs to (by demangled name)."""
+    if "copyBuffer" in name:
+        return "copy"
+    if "fmlm::unpack_kernel" in name:
+        return "unpack"
+    if "fmlm::pack_kernel" in name:
+        return "pack"
+    if "fmlm::segment_copy_kernel" in name:
+        return "kv_append"
+    if "attn_" in name and "schedule" not in name:
+        return "attn"
+    return None
+
+
 def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s: float) -> dict:
     """One `rocprofv3 --pmc <counter>` run of this script's --profile driver in a child
     process.  Returns {"attn": mean KiB per attention dispatch, "copy": KiB of the
-    256 MiB calibration copy}."""
+    256 MiB calibration copy, and for each copy kernel of the path ("pack", "unpack",
+    "kv_append") the KiB of its one profiled call, summed over its dispatches}."""
     import csv
     import shutil
     import subprocess
@@ -334,21 +382,24 @@ def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s
         files = list(out.rglob("*counter_collection.csv"))
         if not files:
             raise RuntimeError(f"rocprofv3 --pmc {counter} wrote no counter file")
-        attn, copies = [], []
+        vals: dict[str, list[float]] = {}
         for f in files:
             with open(f, newline="") as fh:
                 for row in csv.DictReader(fh):
                     if row["Counter_Name"] != counter:
                         continue
-                    name, v = row["Kernel_Name"], float(row["Counter_Value"])
-                    if "attn_" in name and "schedule" not in name:
-                        attn.append(v)
-                    elif "copyBuffer" in name:
-                        copies.append(v)
+                    kind = _kernel_class(row["Kernel_Name"])
+                    if kind is not None:
+                        vals.setdefault(kind, []).append(float(row["Counter_Value"]))
+        attn, copies = vals.get("attn", []), vals.get("copy", [])
         if len(attn) < launches or not copies:
             raise RuntimeError(f"rocprofv3 --pmc {counter}: {len(attn)} attention dispatches, "
                                f"{len(copies)} copies")
-        return {"attn": sum(attn[-launches:]) / launches, "copy": max(copies)}
+        res = {"attn": sum(attn[-launches:]) / launches, "copy": max(copies)}
+        for kind in ("pack", "unpack", "kv_append"):
+            if kind in vals:
+                res[kind] = sum(vals[kind])
+        return res
     finally:
         shutil.rmtree(out, ignore_errors=True)
 
@@ -360,11 +411,16 @@ def hbm_traffic(cfg: int, variant: str, launches: int = 3, timeout_s: float = 12
     f = _counter_pass("FETCH_SIZE", cfg, variant, launches, timeout_s)
     w = _counter_pass("WRITE_SIZE", cfg, variant, launches, timeout_s)
     ff, fw = COPY_KIB / f["copy"], COPY_KIB / w["copy"]
-    return {
+    res = {
         "bytes": 1024.0 * (f["attn"] * ff + w["attn"] * fw),
         "fetch_kib": f["attn"], "write_kib": w["attn"],
         "fetch_scale": round(ff, 4), "write_scale": round(fw, 4),
     }
+    for kind in ("pack", "unpack", "kv_append"):
+        if kind in f and kind in w:
+            res[kind] = {"bytes": 1024.0 * (f[kind] * ff + w[kind] * fw), "fetch_kib": f[kind],
+                         "write_kib": w[kind]}
+    return res
 
 
 def _event_ms(fn, reps: int) -> float:
@@ -385,12 +441,13 @@ def _event_ms(fn, reps: int) -> float:
     return times[len(times) // 2]
 
 
-def hbm_kernels(case: Case, reps: int = 30) -> dict:
-    """HBM rate of the path's copy kernels on this workload's tensors: unpack_from_kernel
-    (read H*T*D, write B*H*N*D), pack_and_pad_main_tensors_for_mlm_compressed (per
-    tensor: read heads*T*D, write heads*T_pad*D; MLA packs q and one latent head) and the
-    KV append of this step's rows to the cached context (read + write every owned row).
-    Algorithmic bytes / median time, against the 8 TB/s HBM peak."""
+def copy_kernel_calls(case: Case) -> dict:
+    """The path's copy kernels on this workload's tensors, as {name: (call, algorithmic
+    bytes, note)}: unpack_from_kernel (read H*T*D, write B*H*N*D),
+    pack_and_pad_main_tensors_for_mlm_compressed (per tensor: read heads*T*D, write
+    heads*T_pad*D; MLA packs q and one latent head) and the KV append of this step's rows
+    to the cached context (InferenceCache.append_kv_cache: reads and writes every row of
+    the merged entry once).  Each call is independent of the others' results."""
     import flash_mlm as fm
     from flash_mlm.host import host_utils as hu
 
@@ -401,28 +458,20 @@ def hbm_kernels(case: Case, reps: int = 30) -> dict:
     esz = torch.finfo(case.dtype).bits // 8
     B, H, N, D = (int(x) for x in t["q"].shape)
     T = int(meta.total_tokens)
-    out = {}
+    calls = {}
 
     packed = torch.randn((H * T, D), device="cuda").to(case.dtype)
-    ms = _event_ms(lambda: fm.unpack_from_kernel(packed, meta, H), reps)
-    nbytes = esz * D * (H * T + B * H * N)
-    out["unpack"] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
-                     "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    calls["unpack"] = (lambda: fm.unpack_from_kernel(packed, meta, H), esz * D * (H * T + B * H * N), "")
 
     pc = fm.PackingCache()
+    bn = int(case.config.get("block_n", 64))
     pack = lambda: hu.pack_and_pad_main_tensors_for_mlm_compressed(  # noqa: E731
-        t["q"], t["k"], t["v"], q_meta=meta, num_heads=H, is_mla=case.is_mla, block_m=64,
-        block_n=int(case.config.get("block_n", 64)), packing_cache=pc)
-    T_pad = pack()[3]
-    ms = _event_ms(pack, reps)
+        t["q"], t["k"], t["v"], q_meta=meta, num_heads=H, is_mla=case.is_mla, block_m=64, block_n=bn,
+        packing_cache=pc)
+    T_pad = hu._compute_total_q_len_padded(T, meta.host_cu_seqlens(), 64, bn)
     heads = H + (1 if case.is_mla else 2 * H)
-    nbytes = esz * D * heads * (T + T_pad)
-    out["pack"] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
-                   "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-                   "tensors": "q + latent head" if case.is_mla else "q, k, v"}
+    calls["pack"] = (pack, esz * D * heads * (T + T_pad), "q + latent head" if case.is_mla else "q, k, v")
 
-    # KV append (InferenceCache.append_kv_cache): this step's K/V rows appended to every
-    # context batch of the layer's packed entry; reads and writes every owned row once
     ent = t["cache"].get_kv_cache(0, is_mla=case.is_mla, num_heads=H, head_dim=D, dtype=case.dtype,
                                   device=t["q"].device) if "cache" in t else None
     if ent is not None and ent.cu_seqlens_kv is not None and ent.block_table is None:
@@ -432,21 +481,34 @@ def hbm_kernels(case: Case, reps: int = 30) -> dict:
         new_k = torch.randn((h_kv * T, D), device="cuda").to(case.dtype)
         new_v = None if case.is_mla else torch.randn((h_kv * T, D), device="cuda").to(case.dtype)
 
-        def fresh():  # a cache holding (views of) the layer's entry; append replaces it
+        def append():  # a cache holding (views of) the layer's entry; append replaces it
             c = fm.InferenceCache()
             c.prefill_kv_cache(0, k_cache=ent.k_cache, v_cache=ent.v_cache, total_context_len=ent.total_context_len,
                                cu_seqlens_kv=ent.cu_seqlens_kv, context_batch_size=ent.context_batch_size,
                                is_mla=case.is_mla, num_heads=H, head_dim=D)
-            return c
+            c.append_kv_cache(0, k_cache=new_k, v_cache=new_v, cu_seqlens_kv=cu_new)
 
-        pool = [fresh() for _ in range(reps + 2)]
-        ms = _event_ms(lambda: pool.pop().append_kv_cache(0, k_cache=new_k, v_cache=new_v, cu_seqlens_kv=cu_new),
-                       reps)
-        rows = int(ent.cu_seqlens_kv[-1]) + T
+        rows = int(ent.total_context_len) + T
         nbytes = esz * D * h_kv * (1 if case.is_mla else 2) * 2 * rows
-        out["kv_append"] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
-                            "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-                            "tensors": "latent" if case.is_mla else "k, v"}
+        calls["kv_append"] = (append, nbytes, "latent" if case.is_mla else "k, v")
+    return calls
+
+
+def hbm_kernels(case: Case, reps: int = 30, traffic: dict | None = None) -> dict:
+    """HBM rate of the path's copy kernels (copy_kernel_calls): algorithmic bytes / median
+    HIP-event time with L2/MALL flushed before each call, against the 8 TB/s HBM peak; with
+    `traffic` (hbm_traffic's counter readings) also the measured HBM bytes per call."""
+    out = {}
+    for name, (fn, nbytes, note) in copy_kernel_calls(case).items():
+        ms = _event_ms(fn, reps)
+        out[name] = {"ms": round(ms, 5), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                     "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        if note:
+            out[name]["tensors"] = note
+        if traffic and name in traffic:
+            tb = traffic[name]["bytes"]
+            out[name]["traffic"] = round(tb)
+            out[name]["traffic_over_algorithmic"] = round(tb / nbytes, 3)
     return out
 
 
@@ -475,13 +537,14 @@ def backward_kernels(case: Case, reps: int = 20) -> dict | None:
             "grads": ("q, latent k" if case.is_mla else "q, k, v") + (", context" if g.dk_ctx else "")}
 
 
-def cpu_baseline(case: Case, budget_s: float = 20.0) -> dict:
-    """The reference's per-sequence PyTorch SDPA path (oracle/cpu_baseline.py) on this
-    host's CPU cores, fp32, over a bounded prefix of the workload's sequences."""
+def cpu_baseline(case: Case, budget_s: float = 20.0, path: str = "sdpa") -> dict:
+    """The reference's per-sequence PyTorch SDPA path, or its eager per-(sequence, head)
+    path (oracle/cpu_baseline.py), on this host's CPU cores, fp32, over a bounded prefix
+    of the workload's sequences."""
     sys.path.insert(0, str(REPO))
     from oracle import cpu_baseline as cb
 
-    return cb.time_case(case, budget_s=budget_s)
+    return cb.time_case(case, budget_s=budget_s, path=path)
 
 
 def main() -> None:
@@ -493,7 +556,7 @@ def main() -> None:
     ap.add_argument("--config", type=int, default=DEFAULT_CONFIG)
     ap.add_argument("--variant", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes that measure HBM traffic")
     ap.add_argument(
@@ -539,12 +602,19 @@ def main() -> None:
         for _ in range(args.steps):
             case.attention()
         torch.cuda.synchronize()
-        print(f"[bench] profiled {args.steps} attention launches", file=sys.stderr, flush=True)
+        # then one call of each copy kernel of the path
+        for name, (fn, _, _) in copy_kernel_calls(case).items():
+            fn()
+            torch.cuda.synchronize()
+        print(f"[bench] profiled {args.steps} attention launches and the copy kernels", file=sys.stderr, flush=True)
         return
 
-    ms, kms = _time_steps(case, args.steps, args.warmup)
-    print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step, attention call {kms:.4f} ms (mean)",
-          file=sys.stderr, flush=True)
+    ms, call_us, step_us = _time_steps(case, args.steps, args.warmup)
+    print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step; host {call_us:.1f} us per attention API call, "
+          f"{step_us:.1f} us per step (medians)", file=sys.stderr, flush=True)
+    kms, kmed = _kernel_device_ms(case.attention, args.kernel_reps)
+    print(f"[bench] attention launch on the device: mean {kms:.4f} ms, median {kmed:.4f} ms over "
+          f"{args.kernel_reps} back-to-back launches", file=sys.stderr, flush=True)
     fms, fmean = _kernel_ms(case.attention, args.kernel_reps)
     print(f"[bench] attention kernel with cold caches: median {fms:.4f} ms, mean {fmean:.4f} ms over "
           f"{args.kernel_reps} flushed launches", file=sys.stderr, flush=True)
@@ -561,8 +631,10 @@ def main() -> None:
         "frac": round(k_tflops / peak, 5),
         "traffic": None if traffic is None else round(traffic["bytes"]),
         "kernel_ms": round(kms, 5),
-        "kernel_timing": f"HIP events on the launch stream around the attention call of each of the "
-                         f"{args.steps} timed steps (mean)",
+        "kernel_ms_median": round(kmed, 5),
+        "kernel_timing": f"HIP events on the launch stream around each of {args.kernel_reps} back-to-back "
+                         "launches of the prepared attention call (the kernel, plus the split merge when key "
+                         "ranges are split), queue kept full; mean",
         "kernel_ms_cold": round(fms, 5),
         "kernel_ms_cold_mean": round(fmean, 5),
         "kernel_cold_timing": f"the same kernel launched alone {args.kernel_reps} times, L2/MALL flushed "
@@ -576,7 +648,7 @@ def main() -> None:
         roofline["hbm_gbs"] = round(traffic["bytes"] / (kms * 1e-3) / 1e9, 1)
     elif traffic_note:
         roofline["traffic_note"] = traffic_note
-    hbm = hbm_kernels(case)
+    hbm = hbm_kernels(case, traffic=traffic)
     if hbm:
         print(f"[bench] copy kernels: {hbm}", file=sys.stderr, flush=True)
     bwd = backward_kernels(case)
@@ -586,6 +658,8 @@ def main() -> None:
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(case)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+        cpu["eager"] = cpu_baseline(case, path="eager", budget_s=10.0)
+        print(f"[bench] cpu eager path: {cpu['eager']}", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,
@@ -595,6 +669,8 @@ def main() -> None:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "host_us_per_call": round(call_us, 2),
+        "host_us_per_step": round(step_us, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -617,8 +617,47 @@ def _check_sampled(case, out_unpacked, pairs, rows=None):
         _close(out_unpacked[b, h, torch.tensor(sel, device=out_unpacked.device)], ref)
 
 
+def _torch_attention_rows(case, b):
+    """fp32 torch attention of every head of sequence b of a BASELINE case on the GPU:
+    (query rows [H, L_b, D], the expected output rows [H, L_b, D]).  The key set is the
+    one _check_sampled builds row by row: [context of b || main keys of b], main keys the
+    packed tokens [cu[b], cu[b+1]), or [0, cu[b+1]) under causal_query_seq_attn."""
+    t = case.tensors
+    q, k, v = t["q"], t["k"], t["v"]
+    L = case.lengths_q[b]
+    if case.cfg in (1, 2):
+        K, V = k[b].float(), v[b].float()
+        if case.cfg == 2:
+            K = torch.cat([t["k0"][0].float(), K], dim=1)
+            V = torch.cat([t["v0"][0].float(), V], dim=1)
+    else:
+        kh = 1 if case.is_mla else case.H
+        seqs = range(b + 1) if case.causal else [b]
+        K = torch.cat([k[s, :kh, : case.lengths_q[s]].float() for s in seqs], dim=1)
+        V = K if case.is_mla else torch.cat([v[s, :, : case.lengths_q[s]].float() for s in seqs], dim=1)
+        if not case.prefill:
+            cb = b if t["cbs"] > 1 else 0
+            c0, c1 = int(t["cu_kv"][cb]), int(t["cu_kv"][cb + 1])
+            Kc = t["k_cache"].view(kh, t["Tc"], -1)[:, c0:c1].float()
+            Vc = Kc if case.is_mla else t["v_cache"].view(kh, t["Tc"], -1)[:, c0:c1].float()
+            K, V = torch.cat([Kc, K], dim=1), torch.cat([Vc, V], dim=1)
+    Q = q[b, :, :L].float()
+    out = torch.empty_like(Q)
+    step = 16  # heads per product: bounds the score buffer (config 5: 16 x 2048 x 10240 fp32)
+    for h0 in range(0, case.H, step):
+        qh = Q[h0 : h0 + step]
+        kh_ = K if K.shape[0] == 1 else K[h0 : h0 + step]
+        vh_ = V if V.shape[0] == 1 else V[h0 : h0 + step]
+        s = torch.matmul(qh, kh_.transpose(1, 2).contiguous()) * t["scale"]
+        out[h0 : h0 + step] = torch.matmul(torch.softmax(s, dim=-1), vh_)
+    return Q, out
+
+
 @pytest.mark.parametrize("cfg,variant", [(1, ""), (2, ""), (3, ""), (4, ""), (5, ""), (5, "prefill")])
 def test_baseline_config_full_size(cfg, variant, device):
+    """A BASELINE config at full size: every real row of every (sequence, head) against a
+    per-sequence fp32 torch attention on the GPU (atol = rtol = 1e-2), four (sequence,
+    head) pairs against the fp64 oracle, and zeros at the padding positions."""
     import bench
 
     case = bench.make_case(cfg, device, variant=variant)
@@ -633,6 +672,18 @@ def test_baseline_config_full_size(cfg, variant, device):
         L = torch.tensor(case.lengths_q, device=device)
         pad = torch.arange(N, device=device)[None, :] >= L[:, None]
         assert bool((out.permute(0, 2, 1, 3)[pad] == 0).all())
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        worst = 0.0
+        for b in range(B):
+            _, ref = _torch_attention_rows(case, b)
+            got = out[b, :, : case.lengths_q[b]].float()
+            excess = (got - ref).abs() - (ATOL + RTOL * ref.abs())
+            worst = max(worst, float(excess.max()) if excess.numel() else -1.0)
+            assert worst <= 0, f"sequence {b}: |out - ref| exceeds atol + rtol*|ref| by {worst:.3e}"
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
     rng = np.random.default_rng(cfg)
     pairs = [(0, 0), (B - 1, H - 1)] + [(int(rng.integers(B)), int(rng.integers(H))) for _ in range(2)]
     _check_sampled(case, out, pairs, rows=None if cfg in (1, 2, 4) else 64)
