@@ -22,6 +22,7 @@
 // the same addressing.
 #include "fmlm_common.h"
 
+#include <algorithm>
 #include <mutex>
 
 namespace fmlm {
@@ -1837,8 +1838,8 @@ static int check_params(const fmlm_attn_params& p) {
   return 0;
 }
 
-static int launch_schedule(const fmlm_attn_params& p, const Launch& L, char* sched, hipStream_t s) {
-  const SplitCfg sc = split_cfg(p, L);
+static int launch_schedule(const fmlm_attn_params& p, const Launch& L, const SplitCfg& sc, char* sched,
+                           hipStream_t s) {
   const SchedLayout l = sched_layout(p, L.bq, sc, L.hpack);
   const int64_t cap = grid_units(p, L.bq, sc, L.hpack);
   // the unit's 16-bit tile field: tiles of N rows, or of H*N (H*total_q) rows head-packed
@@ -1852,6 +1853,100 @@ static int launch_schedule(const fmlm_attn_params& p, const Launch& L, char* sch
   return launch_status();
 }
 
+// The attention launch (plus the split merge) over the schedule at `sched`, which is
+// built first when `build` is set.  sc must be the split sizing the schedule was (or is)
+// built with.
+static int launch_attention(const fmlm_attn_params& p, const Launch& L, const SplitCfg& sc, char* sched,
+                            bool build, hipStream_t s) {
+  int rc = allow_lds(L);
+  if (rc) return rc;
+  int4* units = nullptr;
+  int32_t* n_units = nullptr;
+  if (p.cu_seqlens_q) {
+    n_units = (int32_t*)sched;
+    units = (int4*)(sched + 256);
+    if (build) {
+      rc = launch_schedule(p, L, sc, sched, s);
+      if (rc) return rc;
+    }
+  }
+  const int64_t gx = grid_units(p, L.bq, sc, L.hpack);
+  if (gx <= 0) return 0;
+  if (gx > 0x7fffffff) return FMLM_E_ARG;
+  fmlm_attn_params pc = p;
+  void* args[] = {(void*)&pc, (void*)&units, (void*)&n_units};
+  hipError_t e = hipLaunchKernel(L.fn, dim3((unsigned)gx), dim3(L.threads), args, (size_t)L.lds, s);
+  if (e != hipSuccess) return (int)e;
+  if (sc.rec_cap > 0) {  // split groups (if the schedule made any) are merged here
+    const dim3 mg((unsigned)(sc.rec_cap < 1024 ? sc.rec_cap : 1024));
+    if (p.dtype == FMLM_DTYPE_BF16)
+      hipLaunchKernelGGL(merge_kernel<bf16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
+    else
+      hipLaunchKernelGGL(merge_kernel<f16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
+  }
+  return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point: the schedule (header, units, split groups)
+// and the split records live in this library-owned array, one copy per GPU, instead of
+// a caller's workspace.  Host code never uses the array's name as an address: it reads
+// each device's address once with hipGetSymbolAddress (scratch_on_current_device).
+// Every call on a GPU reuses that GPU's array; calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchBytes = FMLM_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+static int scratch_on_current_device(char** out) {
+  static std::mutex mu;
+  static char* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return FMLM_E_ARG;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return FMLM_E_ARG;
+    ptrs[dev] = (char*)ptr;
+  }
+  *out = ptrs[dev];
+  return 0;
+}
+
+// The split sizing of the allocation-free path: as split_cfg, with the record count cut
+// so that the schedule and the records fit the scratch array (no split when fewer than
+// one record per workgroup slot would fit).  Returns false when even the unsplit
+// schedule does not fit.
+static bool split_cfg_within(const fmlm_attn_params& p, const Launch& L, int64_t cap, SplitCfg& sc) {
+  sc = split_cfg(p, L);
+  auto fits = [&](int rec_cap) {
+    SplitCfg t = sc;
+    t.rec_cap = rec_cap;
+    return sched_layout(p, L.bq, t, L.hpack).bytes <= cap;
+  };
+  if (fits(sc.rec_cap)) return true;
+  // the layout grows with the record count: the largest count in [slots, rec_cap) that fits
+  int lo = sc.slots, hi = sc.rec_cap - 1;
+  if (sc.rec_cap > 0 && lo <= hi && fits(lo)) {
+    while (lo < hi) {
+      const int mid = lo + (hi - lo + 1) / 2;
+      if (fits(mid))
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    sc.rec_cap = lo;
+    return true;
+  }
+  sc.rec_cap = 0;
+  return fits(0);
+}
+
 }  // namespace fmlm
 
 using namespace fmlm;
@@ -1863,7 +1958,7 @@ extern "C" int fmlm_attn_schedule(const fmlm_attn_params* pp, void* schedule,
   const int rc = pick_launch(*pp, L);
   if (rc) return rc;
   if (schedule_bytes < workspace_for(*pp, L)) return FMLM_E_WORKSPACE;
-  return launch_schedule(*pp, L, (char*)schedule, (hipStream_t)stream);
+  return launch_schedule(*pp, L, split_cfg(*pp, L), (char*)schedule, (hipStream_t)stream);
 }
 
 extern "C" int fmlm_attn_params_size(void) { return (int)sizeof(fmlm_attn_params); }
@@ -1887,36 +1982,26 @@ extern "C" int fmlm_attn_fwd(const fmlm_attn_params* pp, void* stream) {
   if (p.B == 0 || p.H == 0) return 0;
   const int64_t need = workspace_for(p, L);
   if (need > 0 && !p.schedule && (!p.workspace || p.workspace_bytes < need)) return FMLM_E_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
+  char* sched = (char*)(p.schedule ? p.schedule : p.workspace);
+  return launch_attention(p, L, split_cfg(p, L), sched, !p.schedule, (hipStream_t)stream);
+}
 
-  rc = allow_lds(L);
+extern "C" int fmlm_attn_fwd_noalloc(const fmlm_attn_params* pp, void* stream) {
+  if (!pp) return FMLM_E_ARG;
+  const fmlm_attn_params& p = *pp;
+  int rc = check_params(p);
   if (rc) return rc;
-
-  int4* units = nullptr;
-  int32_t* n_units = nullptr;
+  Launch L;
+  rc = pick_launch(p, L);
+  if (rc) return rc;
+  if (p.B == 0 || p.H == 0) return 0;
+  SplitCfg sc;
+  char* sched = nullptr;
   if (p.cu_seqlens_q) {
-    char* sched = (char*)(p.schedule ? p.schedule : p.workspace);
-    n_units = (int32_t*)sched;
-    units = (int4*)(sched + 256);
-    if (!p.schedule) {
-      rc = launch_schedule(p, L, sched, s);
-      if (rc) return rc;
-    }
+    if (!split_cfg_within(p, L, kNoAllocScratchBytes, sc)) return FMLM_E_WORKSPACE;
+    rc = scratch_on_current_device(&sched);
+    if (rc) return rc;
   }
-  const int64_t gx = grid_units(p, L.bq, split_cfg(p, L), L.hpack);
-  if (gx <= 0) return 0;
-  if (gx > 0x7fffffff) return FMLM_E_ARG;
-  fmlm_attn_params pc = p;
-  void* args[] = {(void*)&pc, (void*)&units, (void*)&n_units};
-  hipError_t e = hipLaunchKernel(L.fn, dim3((unsigned)gx), dim3(L.threads), args, (size_t)L.lds, s);
-  if (e != hipSuccess) return (int)e;
-  const SplitCfg sc = split_cfg(p, L);
-  if (sc.rec_cap > 0) {  // split groups (if the schedule made any) are merged here
-    const dim3 mg((unsigned)(sc.rec_cap < 1024 ? sc.rec_cap : 1024));
-    if (p.dtype == FMLM_DTYPE_BF16)
-      hipLaunchKernelGGL(merge_kernel<bf16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
-    else
-      hipLaunchKernelGGL(merge_kernel<f16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
-  }
-  return launch_status();
+  // the schedule is always rebuilt: the array holds whatever the previous call left
+  return launch_attention(p, L, sc, sched, true, (hipStream_t)stream);
 }

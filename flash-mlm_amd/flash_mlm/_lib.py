@@ -154,6 +154,7 @@ SIGNATURES = {
     "fmlm_attn_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(AttnParams)]),
     "fmlm_attn_schedule": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr, _c_i64, _c_ptr]),
     "fmlm_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr]),
+    "fmlm_attn_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr]),
     "fmlm_attn_grads_size": (ctypes.c_int, []),
     "fmlm_attn_bwd_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(AttnParams)]),
     "fmlm_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), ctypes.POINTER(AttnGrads), _c_ptr]),

@@ -230,6 +230,22 @@ FMLM_API int fmlm_attn_schedule(const fmlm_attn_params* p, void* schedule, int64
 FMLM_API int fmlm_attn_fwd(const fmlm_attn_params* p, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * fmlm_attn_fwd without a workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * No counterpart in the reference.  Same parameters and results as fmlm_attn_fwd;
+ * p->workspace and p->schedule are ignored.  The work schedule and the split-KV partial
+ * results live in a device array owned by the library, FMLM_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends; the schedule is rebuilt on every call.  When the
+ * split records would not fit, fewer key ranges are split (or none); a call whose
+ * unsplit schedule does not fit returns FMLM_E_WORKSPACE.  Every call on a GPU shares
+ * that GPU's array: calls that may overlap on one GPU (different streams, or host
+ * threads) race and must be serialised by the caller.  Allocates nothing.
+ * ------------------------------------------------------------------------- */
+#define FMLM_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+FMLM_API int fmlm_attn_fwd_noalloc(const fmlm_attn_params* p, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Attention backward.  No counterpart in the reference, whose roadmap lists
  * backpropagation (README.md:26-28); it differentiates fmlm_attn_fwd for the same
  * parameter block p (p->o holding that call's output):

@@ -54,6 +54,7 @@ def test_argument_rejection_without_launch():
     assert lib.fmlm_pack_metadata(None, 0, 1, 4, 0, None, None, None, None, None, None) == -1
     assert lib.fmlm_tile_map(None, 1, 4, 0, None, None, None, None) == -1
     assert lib.fmlm_attn_fwd(None, None) == -1
+    assert lib.fmlm_attn_fwd_noalloc(None, None) == -1
     p = _lib.AttnParams()
     p.dtype, p.B, p.H, p.D, p.N = _lib.DTYPE_BF16, 1, 1, 48, 4
     assert lib.fmlm_attn_workspace_bytes(p) == -3  # unsupported head dim
