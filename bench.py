@@ -355,7 +355,7 @@ def _kernel_class(name: str) -> str | None:
     return None
 
 
-def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s: float) -> dict:
+def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s: float, tile: int = 0) -> dict:
     """One `rocprofv3 --pmc <counter>` run of this script's --profile driver in a child
     process.  Returns {"attn": mean KiB per attention dispatch, "copy": KiB of the
     256 MiB calibration copy, and for each copy kernel of the path ("pack", "unpack",
@@ -374,6 +374,8 @@ def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s
            "--steps", str(launches)]
     if variant:
         cmd += ["--variant", variant]
+    if tile:
+        cmd += ["--tile-config", str(tile)]
     env = dict(os.environ, TMPDIR="/tmp")
     try:
         # rocprofv3 may exit non-zero after writing complete results; the CSV decides
@@ -404,12 +406,12 @@ def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s
         shutil.rmtree(out, ignore_errors=True)
 
 
-def hbm_traffic(cfg: int, variant: str, launches: int = 3, timeout_s: float = 120.0) -> dict:
+def hbm_traffic(cfg: int, variant: str, launches: int = 3, timeout_s: float = 120.0, tile: int = 0) -> dict:
     """HBM bytes per attention launch from two counter passes (FETCH_SIZE, WRITE_SIZE),
     each scaled by what the same counter reads for a copy of known size (256 MiB read +
     256 MiB written) in the same run."""
-    f = _counter_pass("FETCH_SIZE", cfg, variant, launches, timeout_s)
-    w = _counter_pass("WRITE_SIZE", cfg, variant, launches, timeout_s)
+    f = _counter_pass("FETCH_SIZE", cfg, variant, launches, timeout_s, tile)
+    w = _counter_pass("WRITE_SIZE", cfg, variant, launches, timeout_s, tile)
     ff, fw = COPY_KIB / f["copy"], COPY_KIB / w["copy"]
     res = {
         "bytes": 1024.0 * (f["attn"] * ff + w["attn"] * fw),
@@ -557,6 +559,8 @@ def main() -> None:
     ap.add_argument("--variant", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=100)
+    ap.add_argument("--tile-config", type=int, default=0,
+                    help="force the attention kernel's tile configuration k (0: the library's choice)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes that measure HBM traffic")
     ap.add_argument(
@@ -578,7 +582,7 @@ def main() -> None:
     traffic, traffic_note = None, None
     if not args.profile and not args.no_traffic:
         try:
-            traffic = hbm_traffic(args.config, args.variant)
+            traffic = hbm_traffic(args.config, args.variant, tile=args.tile_config)
             print(f"[bench] HBM traffic per launch: {traffic}", file=sys.stderr, flush=True)
         except Exception as e:  # counters unavailable: report null, say why
             traffic_note = f"counter passes failed: {e}"
@@ -590,6 +594,10 @@ def main() -> None:
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.tile_config:
+        from flash_mlm.host import host as hh
+
+        hh._TILE_CONFIG = args.tile_config
     case = make_case(args.config, device, variant=args.variant)
     print(f"[bench] {case.workload}: built inputs", file=sys.stderr, flush=True)
 

@@ -619,8 +619,9 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(con
 // Software-pipelined MFMA kernel (v3) for head dims 16..256.
 //
 // The LDS holds two K tiles and three V tiles, filled by direct global->LDS loads (no
-// staging registers) with 16-byte chunks XOR-swizzled per row by kv_swz, so both the
-// b128 K reads and the tr16 V reads are bank-conflict free.  Iteration t of a wave:
+// staging registers) with 16-byte chunks XOR-swizzled per row (K tiles by k_swz, V tiles
+// by kv_swz), so both the b128 K reads and the tr16 V reads are bank-conflict free.
+// Iteration t of a wave:
 //   1. issues the loads of K(t+2) (into K(t)'s buffer) and V(t+2) (into V(t-1)'s);
 //   2. row max of S(t) (lane-local + two permlane swaps) and the lazy-rescale decision;
 //   3. one basic block that runs S(t+1) = K(t+1) Q^T on the MFMA pipe while the VALU
@@ -763,23 +764,28 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     }
   }
 
-  // ---- per-lane LDS byte offsets (see kv_swz): the K fragment of block kb, step kc is
-  // at kb*16*ROWB + 256*(kc/4) + koff[kc%4]; the V tr16 fragment of step ks, column
-  // block db, half h is at (32 ks + 16 h)*ROWB + 256*(db/8) + voff[db%8]
-  int koff[4], voff[8];
+  // ---- per-lane LDS byte addresses (see k_swz / kv_swz): the K fragment of block kb,
+  // step kc of the K tile at byte offset o from the first K buffer is at koff[kc%4] + o +
+  // kb*16*ROWB + 256*(kc/4); the V tr16 fragment of step ks, column block db, half h of
+  // the V tile at offset o from the first V buffer at voff[db%8] + o + (32 ks + 16 h)*ROWB
+  // + 256*(db/8).  The lane's register then carries the whole address and every other
+  // term is a read's immediate offset (a constant in the unrolled steps).
+  uint32_t koff[4], voff[8];
   {
-    const int ksw = kv_swz<D>(l16);
+    const int ksw = k_swz<D>(l16);
 #pragma unroll
-    for (int b = 0; b < 4; ++b) koff[b] = l16 * C::ROWB + 16 * ((4 * b + g) ^ ksw);
+    for (int b = 0; b < 4; ++b) koff[b] = lds_addr(kbuf) + l16 * C::ROWB + 16 * ((4 * b + g) ^ ksw);
     const int vr = 4 * g + (l16 >> 2);
     const int vsw = kv_swz<D>(vr);
     const int x = (l16 & 3) >> 1;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) voff[db] = vr * C::ROWB + 16 * ((2 * db + x) ^ vsw) + 8 * (l16 & 1);
+    for (int db = 0; db < 8; ++db)
+      voff[db] = lds_addr(vbuf) + vr * C::ROWB + 16 * ((2 * db + x) ^ vsw) + 8 * (l16 & 1);
   }
   // ---- per-lane direct-load layout: wave-wide load i = wave + j*NW brings rows
-  // [i*RPI, (i+1)*RPI); lane l fetches logical chunk (l % CPR) ^ kv_swz(row) of row
-  // i*RPI + l/CPR, which lands in physical chunk l % CPR
+  // [i*RPI, (i+1)*RPI); lane l fetches logical chunk (l % CPR) ^ swz(row) of row
+  // i*RPI + l/CPR, which lands in physical chunk l % CPR (swz: k_swz for K tiles, read by
+  // b128 only; kv_swz for V tiles, read by tr16 only)
   const int drow0 = wave * C::RPI + lane / C::CPR;  // + j*NW*RPI for load j
 
   f32x4 o[C::NDB][QB];
@@ -814,11 +820,12 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   // segment from there.  Rows past a segment end repeat its last row (their scores are
   // masked to -inf, so P = 0 multiplies finite values).
   typedef KeyCursor Cursor;
-  auto lane_offsets = [&](uint32_t rowb, int last, uint32_t (&ofs)[C::NPW]) {
+  auto lane_offsets = [&](uint32_t rowb, int last, bool is_v, uint32_t (&ofs)[C::NPW]) {
 #pragma unroll
     for (int j = 0; j < C::NPW; ++j) {
       const int row = drow0 + j * NW * C::RPI;
-      ofs[j] = (uint32_t)__umul24((uint32_t)min(row, last), rowb) + 16 * ((lane % C::CPR) ^ kv_swz<D>(row));
+      const int sw = is_v ? kv_swz<D>(row) : k_swz<D>(row);
+      ofs[j] = (uint32_t)__umul24((uint32_t)min(row, last), rowb) + 16 * ((lane % C::CPR) ^ sw);
     }
   };
   // a paged context (PAGED instantiation, segment 0 only) puts each key tile in a page
@@ -848,19 +855,21 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       cr.p += (size_t)skip * BK * cr.rowb;
     }
   };
-  // lane offsets of a whole tile at the main segment's K row pitch (the common case)
+  // lane offsets of a whole tile at the main segment's K row pitch (the common case), for
+  // K tiles and V tiles (the same when the two swizzles agree)
   const uint32_t oc_rowb = __builtin_amdgcn_readfirstlane((uint32_t)w.seg[1].ksn * 2u);
-  uint32_t oc[C::NPW];
-  lane_offsets(oc_rowb, BK, oc);
+  uint32_t oc_k[C::NPW], oc_v[C::NPW];
+  lane_offsets(oc_rowb, BK, false, oc_k);
+  lane_offsets(oc_rowb, BK, true, oc_v);
   // load the cursor's tile into LDS dst and advance to the next tile
   auto fetch = [&](Cursor& cr, char* dst, bool is_v) {
     const uint32_t lds0 = lds_addr(dst);
     uint32_t ofs[C::NPW];
     if (cr.left >= BK && cr.rowb == oc_rowb) {
 #pragma unroll
-      for (int j = 0; j < C::NPW; ++j) ofs[j] = oc[j];
+      for (int j = 0; j < C::NPW; ++j) ofs[j] = is_v ? oc_v[j] : oc_k[j];
     } else {
-      lane_offsets(cr.rowb, cr.left - 1, ofs);
+      lane_offsets(cr.rowb, cr.left - 1, is_v, ofs);
     }
 #pragma unroll
     for (int j = 0; j < C::NPW; ++j) {
@@ -880,15 +889,16 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   auto tile_keys = [&](int t) {
     return t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
   };
-  // S^T = K Q^T from the K tile at kt (prologue only; the steps interleave it)
-  auto qk = [&](const char* kt, f32x4 (&s)[C::NKB][QB]) {
+  // S^T = K Q^T from the K tile at byte offset kt from the first K buffer (prologue only;
+  // the steps interleave it)
+  auto qk = [&](uint32_t kt, f32x4 (&s)[C::NKB][QB]) {
 #pragma unroll
     for (int kc = 0; kc < C::KC; ++kc) {
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb) {
         v8 a;
         if (kc * 32 + g * 8 < D)
-          a = *(const v8*)(kt + kb * 16 * C::ROWB + 256 * (kc >> 2) + koff[kc & 3]);
+          a = *(const FMLM_LDS v8*)(uintptr_t)(koff[kc & 3] + kt + kb * 16 * C::ROWB + 256 * (kc >> 2));
         else
           a = v8{};
 #pragma unroll
@@ -925,10 +935,11 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     else
       __builtin_amdgcn_s_waitcnt(0);
   };
-  // One pipeline step: sc holds S(t) and mx its row maxima; computes sn = S(t+1) from kn
-  // and its maxima, consumes V(t) at vt, refills kdst with K(t+2) and vdst with V(t+2).
+  // One pipeline step: sc holds S(t) and mx its row maxima; computes sn = S(t+1) from the
+  // K tile at byte offset kn (from the first K buffer) and its maxima, consumes V(t) at
+  // byte offset vt (from the first V buffer), refills kdst with K(t+2) and vdst with V(t+2).
   auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
-                  const char* kn, const char* vt, char* kdst, char* vdst) {
+                  uint32_t kn, uint32_t vt, char* kdst, char* vdst) {
     if (t + 2 < te) fetch(kcur, kdst, false);
     if (t + 2 < te) fetch(vcur, vdst, true);
     if (!wave_active) {  // every query row of this wave is padding: loads and barriers only
@@ -990,12 +1001,12 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       if (r < C::NKF) {
         const int kc = r / C::NKB, kb = r % C::NKB;
         fr[r % (C::LEAD + 1)] = kc * 32 + g * 8 < D
-            ? *(const v8*)(kn + kb * 16 * C::ROWB + 256 * (kc >> 2) + koff[kc & 3]) : v8{};
+            ? *(const FMLM_LDS v8*)(uintptr_t)(koff[kc & 3] + kn + kb * 16 * C::ROWB + 256 * (kc >> 2)) : v8{};
       } else {
         const int j = r - C::NKF, ks = j / C::NDB, db = j % C::NDB;
-        const char* va = vt + ks * 32 * C::ROWB + 256 * (db >> 3) + voff[db & 7];
-        const s16x4 lo = lds_read_tr16(va);
-        const s16x4 hi = lds_read_tr16(va + 16 * C::ROWB);
+        const uint32_t va = voff[db & 7] + vt + ks * 32 * C::ROWB + 256 * (db >> 3);
+        const s16x4 lo = lds_read_tr16_at(va);
+        const s16x4 hi = lds_read_tr16_at(va + 16 * C::ROWB);
         fr[r % (C::LEAD + 1)] = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     };
@@ -1076,21 +1087,29 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (wave_active) {
-      qk(kbuf, sa);
+      qk(0, sa);
       row_max(sa, mx);
     }
     __syncthreads();  // every wave is done with K(0): its buffer may be refilled
   }
-  for (int t = tb; t < te; ++t) {
-    const int cur = ((t - tb) & 1) * C::TILEB, nxt = C::TILEB - cur;
-    const int v3 = (t - tb) % 3;
+  // step i of the unit uses K buffer i % 2 and V buffer i % 3; six steps per iteration
+  // make every buffer offset a constant of its step (an LDS read address is then the
+  // lane's offset register plus an immediate), the remainder takes them at run time
+  auto step_i = [&](int t, int i) {
+    const int cur = (i & 1) * C::TILEB, nxt = C::TILEB - cur;
+    const int v3 = i % 3;
     const int vc = v3 * C::TILEB, vd = (v3 == 0 ? 2 : v3 - 1) * C::TILEB;
-    step(t, sa, sb, mx, kbuf + nxt, vbuf + vc, kbuf + cur, vbuf + vd);
+    step(t, sa, sb, mx, nxt, vc, kbuf + cur, vbuf + vd);
 #pragma unroll
     for (int kb = 0; kb < C::NKB; ++kb)
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) sa[kb][qb] = sb[kb][qb];
-  }
+  };
+  int t = tb;
+  for (; t + 6 <= te; t += 6)
+#pragma unroll
+    for (int i = 0; i < 6; ++i) step_i(t + i, i);
+  for (; t < te; ++t) step_i(t, t - tb);
 
   // ---- split part: this part's record (O / l as T, then m and l per row) for
   // merge_kernel
@@ -1223,7 +1242,9 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   // step kc is at (kk ^ 64*(kc%4)) + kb*16*ROWB + 256*(kc/4); the V tr16 fragment of step
   // ks, column block db, half h at (vv ^ 32*(db%8)) + (32 ks + 16 h)*ROWB + 256*(db/8).
   // The XOR terms select the swizzled 16-byte chunk; they touch bits 5..7 only, which the
-  // row and stage offsets leave clear.
+  // row and stage offsets leave clear.  The swizzle is the tr16 one: the b128 K reads of
+  // this tile then take two cycles per 16 lanes, which measured cheaper than reading each
+  // K fragment as two conflict-free 8-byte halves (twice the LDS instructions).
   int kk, vv;
   {
     const int ksw = kv_swz<D>(l16);
@@ -1233,7 +1254,9 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
     const int x = (l16 & 3) >> 1;
     vv = vr * C::ROWB + 32 * (vsw >> 1) + 16 * (x ^ (vsw & 1)) + 8 * (l16 & 1);
   }
-  constexpr int LEAD = 3;  // LDS fragment reads in flight ahead of their MFMA
+  // LDS fragment reads in flight ahead of their MFMA (the paged variant keeps its page
+  // window in registers, which the longer lead would spill)
+  constexpr int LEAD = PAGED ? 2 : 3;
 
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
@@ -1666,6 +1689,7 @@ static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
   const bool lookup = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q &&
                       p.kv_layout != FMLM_LAYOUT_PACKED;
   if (lookup) {
+    if (p.tile_config > 1) return false;
     switch (p.D) {
       case 16: L = mfma_launch<T, 16, 2, 4, 64>(); return true;
       case 32: L = mfma_launch<T, 32, 2, 4, 64>(); return true;
@@ -1676,14 +1700,34 @@ static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
     }
   }
   const bool paged = p.ctx_block_table != nullptr;
+  const int k = p.tile_config > 0 ? p.tile_config : 1;
   switch (p.D) {
-    case 16: L = mfma3_launch<T, 16, 2, 4, 64>(paged); return true;
-    case 32: L = mfma3_launch<T, 32, 2, 4, 64>(paged); return true;
-    case 64: L = mfma3_launch<T, 64, 2, 4, 64>(paged); return true;
-    case 128: L = mfma3_launch<T, 128, 2, 4, 64>(paged); return true;
-    case 256: L = mfma3_launch<T, 256, 1, 4, 64>(paged); return true;
+    case 16:
+      if (k == 1) L = mfma3_launch<T, 16, 2, 4, 64>(paged); else return false;
+      return true;
+    case 32:
+      if (k == 1) L = mfma3_launch<T, 32, 2, 4, 64>(paged); else return false;
+      return true;
+    case 64:
+      if (k == 1) L = mfma3_launch<T, 64, 2, 4, 64>(paged);
+      else if (k == 2) L = mfma3_launch<T, 64, 2, 8, 64>(paged);
+      else if (k == 3) L = mfma3_launch<T, 64, 1, 4, 64>(paged);
+      else return false;
+      return true;
+    case 128:
+      if (k == 1) L = mfma3_launch<T, 128, 2, 4, 64>(paged);
+      else if (k == 2) L = mfma3_launch<T, 128, 2, 8, 64>(paged);
+      else if (k == 3) L = mfma3_launch<T, 128, 1, 4, 64>(paged);
+      else if (k == 4) L = mfma3_launch<T, 128, 1, 8, 64>(paged);
+      else return false;
+      return true;
+    case 256:
+      if (k == 1) L = mfma3_launch<T, 256, 1, 4, 64>(paged);
+      else if (k == 2) L = mfma3_launch<T, 256, 1, 8, 64>(paged);
+      else return false;
+      return true;
     case 512:
-      if (!(p.flags & FMLM_FLAG_MLA)) return false;
+      if (!(p.flags & FMLM_FLAG_MLA) || k != 1) return false;
       L = mla_rows_launch<T>(p.ctx_block_table != nullptr);
       return true;
     default: return false;
@@ -1705,13 +1749,14 @@ static bool pick_simt(int D, Launch& L) {
 
 static int pick_launch(const fmlm_attn_params& p, Launch& L) {
   bool ok = false;
+  if (p.tile_config < 0) return FMLM_E_ARG;
   switch (p.dtype) {
-    case FMLM_DTYPE_BF16: ok = pick_mfma<bf16>(p, L) || pick_simt<bf16>(p.D, L); break;
-    case FMLM_DTYPE_F16: ok = pick_mfma<f16>(p, L) || pick_simt<f16>(p.D, L); break;
+    case FMLM_DTYPE_BF16: ok = pick_mfma<bf16>(p, L) || (p.tile_config <= 1 && pick_simt<bf16>(p.D, L)); break;
+    case FMLM_DTYPE_F16: ok = pick_mfma<f16>(p, L) || (p.tile_config <= 1 && pick_simt<f16>(p.D, L)); break;
     case FMLM_DTYPE_F32: ok = pick_simt<float>(p.D, L); break;
     default: return FMLM_E_DTYPE;
   }
-  if (!ok) return FMLM_E_HEAD_DIM;
+  if (!ok) return p.tile_config > 1 ? FMLM_E_ARG : FMLM_E_HEAD_DIM;
   // a paged context needs a kernel whose key tile is one page (not fp32, not per-row lookups)
   if (p.ctx_block_table && !(p.flags & FMLM_FLAG_PREFILL) && !L.paged) return FMLM_E_ARG;
   return 0;

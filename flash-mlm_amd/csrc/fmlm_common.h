@@ -139,16 +139,28 @@ FMLM_DEV s16x4 lds_read_tr16_at(uint32_t a) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLM_LDS s16x4*)(uintptr_t)a);
 }
 
-// 16-byte chunk swizzle of a row-major LDS tile of head dim D: logical chunk c of row r
-// sits in physical chunk c ^ kv_swz(r).  It depends on r % 16 only and makes both the
-// b128 row-fragment reads (16 rows, one chunk each) and the tr16 reads (4 rows x 4
-// lanes per 16-lane group) bank-conflict free.
+// 16-byte chunk swizzles of a row-major LDS tile of head dim D: logical chunk c of row r
+// sits in physical chunk c ^ swz(r), swz depending on r % 16 only.  Two read shapes use
+// the tiles: b128 row fragments (lane (l16 + 16g) reads chunk 4b + g of row l16) and tr16
+// column fragments (lane (l16 + 16g) reads 8 bytes of row 4g + l16/4).  gfx950's LDS has
+// 64 banks of 4 bytes; a tr16 (or b64) read serves 32 consecutive lanes per cycle, so it
+// is conflict free when the 8 rows of those lanes put their 32-byte column block in 8
+// different bank groups.  The b128 rule is not that simple; the swizzles below were
+// chosen by measurement (SQ_LDS_BANK_CONFLICT of each read shape alone):
+//   kv_swz: conflict free for tr16 reads, and for b128 reads at D <= 64 (at D >= 128 the
+//           b128 row reads of a tile swizzled this way cost twice the cycles);
+//   k_swz:  conflict free for b128 reads at every D (tiles read by b128 only).
 template <int D>
 FMLM_DEV int kv_swz(int r) {
   if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  else if constexpr (D == 64) return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
-  else if constexpr (D == 32) return (r >> 2) & 3;
+  else if constexpr (D == 64) return r & 7;
+  else if constexpr (D == 32) return (r >> 1) & 3;
   else return (r >> 3) & 1;
+}
+template <int D>
+FMLM_DEV int k_swz(int r) {
+  if constexpr (D >= 128) return r & 15;
+  else return kv_swz<D>(r);
 }
 
 FMLM_DEV uint32_t lds_addr(const void* p) {

@@ -96,7 +96,7 @@ class AttnParams(ctypes.Structure):
         ("ctx_block_table", _c_ptr),
         ("ctx_page_stride", _c_i64),
         ("ctx_pages_per_batch", _c_i32),
-        ("reserved0", _c_i32),
+        ("tile_config", _c_i32),
     ]
 
 

@@ -41,6 +41,31 @@ from flash_mlm.host.host_utils import (
 # padded prefill length when auto_tune_tiles=True (host.py:326)
 _AUTOTUNE_MAX_BLOCK_M = 128
 
+# fmlm_attn_params.tile_config of every launch: 0 lets the library choose the kernel's
+# tile from the head dim and the work; k >= 1 forces compiled configuration k (tests and
+# tuning sweeps; see tile_config())
+_TILE_CONFIG = 0
+
+
+class tile_config:
+    """Force the attention kernel's tile configuration ``k`` (the library's k-th compiled
+    configuration of the head dim, include/flash_mlm_hip.h) for the calls made inside the
+    ``with`` block; ``k = 0`` restores the library's own choice.  A tuning and testing aid,
+    like the reference's per-shape autotune configs (mlm_kernel.py:57-166)."""
+
+    def __init__(self, k: int):
+        self.k = int(k)
+
+    def __enter__(self):
+        global _TILE_CONFIG
+        self.prev, _TILE_CONFIG = _TILE_CONFIG, self.k
+        return self
+
+    def __exit__(self, *exc):
+        global _TILE_CONFIG
+        _TILE_CONFIG = self.prev
+        return False
+
 
 def _aligned(t: torch.Tensor) -> bool:
     """Row-addressable by the kernel: unit stride in D, 16-byte aligned rows."""
@@ -278,6 +303,7 @@ def _prepare(
     p = _lib.AttnParams()
     p.dtype = _lib.dtype_code(q.dtype)
     p.flags = flags
+    p.tile_config = _TILE_CONFIG
     p.B, p.H, p.D, p.N = B, H, D, N
     p.total_q = total_q
     p.ctx_len = ctx_len
@@ -312,7 +338,7 @@ def _prepare(
             # layout, paged context or not), whose tile size and occupancy fix the slots,
             # the split records and the grid, and the shape (B, H, N, total_q); context
             # lengths only steer where key ranges are split
-            key = (p.dtype, D, B, H, N, total_q, p.flags, p.kv_layout, block_table is not None)
+            key = (p.dtype, D, B, H, N, total_q, p.flags, p.kv_layout, block_table is not None, p.tile_config)
             sched = schedule_cache.get(key)
             if sched is None:
                 sched = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)

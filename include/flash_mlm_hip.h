@@ -212,7 +212,16 @@ typedef struct fmlm_attn_params {
   const int32_t* ctx_block_table;
   int64_t ctx_page_stride;
   int32_t ctx_pages_per_batch;
-  int32_t reserved0;
+  /* Tile configuration of the bf16/f16 attention kernel: 0 = chosen by the library from
+   * the head dim and the work (query tiles against the GPU's workgroup slots); k >= 1
+   * forces compiled configuration k of the head dim (fmlm_attn_workspace_bytes returns
+   * FMLM_E_ARG for a k that does not exist).  Configurations, as (query rows per
+   * workgroup, waves per workgroup): D = 16, 32: 1 = (128, 4); D = 64: 1 = (128, 4),
+   * 2 = (256, 8), 3 = (64, 4); D = 128: 1 = (128, 4), 2 = (256, 8), 3 = (64, 4),
+   * 4 = (128, 8); D = 256: 1 = (64, 4),
+   * 2 = (128, 8); MLA D = 512: 1 = (128, 8).  Replaces the reference's autotuned
+   * BLOCK_M / BLOCK_N / num_warps (mlm_kernel.py:57-166).  Ignored by f32 inputs.       */
+  int32_t tile_config;
 } fmlm_attn_params;
 
 /* Bytes of device workspace (and of a schedule buffer) fmlm_attn_fwd needs for these

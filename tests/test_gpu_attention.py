@@ -340,6 +340,63 @@ def test_packed_head_dim_dtype_sweep(dtype, D, mode, device):
 
 
 # ---------------------------------------------------------------------------
+# every compiled tile configuration (fmlm_attn_params.tile_config), forced
+# ---------------------------------------------------------------------------
+TILE_CONFIGS = {16: (1,), 32: (1,), 64: (1, 2, 3), 128: (1, 2, 3, 4), 256: (1, 2)}
+
+
+def test_tile_config_table_matches_library(device):
+    # configurations past the table are rejected (FMLM_E_ARG) before any launch
+    from flash_mlm import _lib
+
+    lib = _lib.load()
+    for D, ks in TILE_CONFIGS.items():
+        for dt in (_lib.DTYPE_BF16, _lib.DTYPE_F16):
+            p = _lib.AttnParams()
+            p.dtype, p.B, p.H, p.D, p.N, p.total_q = dt, 1, 1, D, 64, 64
+            for k in ks:
+                p.tile_config = k
+                assert lib.fmlm_attn_workspace_bytes(p) == 0, (D, k)
+            p.tile_config = max(ks) + 1
+            assert lib.fmlm_attn_workspace_bytes(p) == -1, (D, p.tile_config)
+    p.D, p.flags, p.tile_config = 512, _lib.FLAG_MLA, 2
+    assert lib.fmlm_attn_workspace_bytes(p) == -1
+
+
+@pytest.mark.parametrize("D,k", [(D, k) for D, ks in TILE_CONFIGS.items() for k in ks])
+@pytest.mark.parametrize("mode", ["ctx", "causal_ctx", "dense_shared", "split"])
+def test_every_tile_config(D, k, mode, device):
+    from flash_mlm.host.host import tile_config
+
+    torch.manual_seed(8000 + D + 10 * k)
+    dtype = torch.bfloat16 if (D + k) % 2 else torch.float16
+    scale = 1.0 / math.sqrt(D)
+    with tile_config(k):
+        if mode == "dense_shared":
+            B, H, N, C = 3, 4, 300, 150
+            q, kk, v = (_randn((B, H, N, D), device, dtype) for _ in range(3))
+            kc, vc = (_randn((1, H, C, D), device, dtype) for _ in range(2))
+            cache = InferenceCache()
+            cache.prefill_kv_cache(0, k_cache=kc.reshape(H * C, D), v_cache=vc.reshape(H * C, D),
+                                   context_batch_size=1, is_mla=False, num_heads=H, head_dim=D)
+            out = flash_attn_mlm(q, kk, v, scale, inference_cache=cache, layer_id=0)
+            ref = ar.mlm_attention_dense(_np(q), _np(kk), _np(v), scale, k_cache=_np(kc.reshape(H * C, D)),
+                                         v_cache=_np(vc.reshape(H * C, D)), context_len=C, context_batch_size=1)
+            _close(out, ref)
+            return
+        causal = mode == "causal_ctx"
+        lengths = [300, 1, 0, 257, 64, 130] if mode != "split" else [97, 300, 1]
+        ctx = [5, 0, 40, 700, 64, 3] if mode != "split" else [3000, 4100, 65]
+        B, H, N = len(lengths), 3, max(lengths)
+        q, kk, v = (_randn((B, H, N, D), device, dtype) for _ in range(3))
+        cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, ctx, device, dtype)
+        meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+        out = flash_attn_mlm_compressed(q, kk, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=causal)
+    ref = _packed_oracle(q, kk, v, lengths, scale, causal=causal, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=B, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+
+
+# ---------------------------------------------------------------------------
 # split-KV: few work units over long key ranges are cut into parts whose partial
 # results a second kernel merges (the schedule decides; these shapes have far fewer
 # units than workgroup slots and tens of key tiles per unit)
