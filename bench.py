@@ -315,20 +315,31 @@ def _kernel_device_ms(attention, reps: int) -> tuple[float, float]:
 
 
 FLUSH_BYTES = 512 << 20  # > the 256 MB MALL (and the 4 MB L2s)
+_flush_buf = None
+
+
+def _flush_caches() -> None:
+    """Evict L2 and MALL before a cold-cache launch by reading FLUSH_BYTES: the caches then
+    hold clean lines.  (Writing the buffer instead leaves up to 256 MB of dirty lines whose
+    write-back lands inside the next timed launch: the copy kernels measured 20-30% slower
+    after a write flush than after a read flush.)"""
+    global _flush_buf
+    if _flush_buf is None:
+        _flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+    _flush_buf.sum()
 
 
 def _kernel_ms(attention, reps: int) -> tuple[float, float]:
     """Attention-kernel duration from HIP events recorded on the kernel's launch stream
     around each of `reps` prepared launches, with L2/MALL flushed before every launch by
-    writing a 512 MiB buffer.  Returns (median, mean) in ms."""
+    reading a 512 MiB buffer.  Returns (median, mean) in ms."""
     stream = _launch_stream(attention)
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
     for _ in range(3):
         attention()
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     with torch.cuda.stream(stream):
         for e0, e1 in events:
-            flush.fill_(0)
+            _flush_caches()
             e0.record(stream)
             attention()
             e1.record(stream)
@@ -348,7 +359,7 @@ def _kernel_class(name: str) -> str | None:
         return "unpack"
     if "fmlm::pack_kernel" in name:
         return "pack"
-    if "fmlm::segment_copy_kernel" in name:
+    if "fmlm::kv_append_kernel" in name:
         return "kv_append"
     if "attn_" in name and "schedule" not in name:
         return "attn"
@@ -427,14 +438,13 @@ def hbm_traffic(cfg: int, variant: str, launches: int = 3, timeout_s: float = 12
 
 def _event_ms(fn, reps: int) -> float:
     """Median duration of fn() from HIP events on the current stream, L2/MALL flushed
-    (512 MiB write) before each call."""
+    (512 MiB read) before each call."""
     stream = torch.cuda.current_stream()
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
     for _ in range(2):
         fn()
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     for e0, e1 in events:
-        flush.fill_(0)
+        _flush_caches()
         e0.record(stream)
         fn()
         e1.record(stream)
@@ -449,7 +459,8 @@ def copy_kernel_calls(case: Case) -> dict:
     pack_and_pad_main_tensors_for_mlm_compressed (per tensor: read heads*T*D, write
     heads*T_pad*D; MLA packs q and one latent head) and the KV append of this step's rows
     to the cached context (InferenceCache.append_kv_cache: reads and writes every row of
-    the merged entry once).  Each call is independent of the others' results."""
+    the merged entry once; one fmlm_kv_append launch).  Each call is independent of the
+    others' results."""
     import flash_mlm as fm
     from flash_mlm.host import host_utils as hu
 
@@ -498,7 +509,8 @@ def copy_kernel_calls(case: Case) -> dict:
 
 def hbm_kernels(case: Case, reps: int = 30, traffic: dict | None = None) -> dict:
     """HBM rate of the path's copy kernels (copy_kernel_calls): algorithmic bytes / median
-    HIP-event time with L2/MALL flushed before each call, against the 8 TB/s HBM peak; with
+    HIP-event time with L2/MALL flushed (by a read) before each call, against the 8 TB/s
+    HBM peak; with
     `traffic` (hbm_traffic's counter readings) also the measured HBM bytes per call."""
     out = {}
     for name, (fn, nbytes, note) in copy_kernel_calls(case).items():
@@ -646,7 +658,7 @@ def main() -> None:
         "kernel_ms_cold": round(fms, 5),
         "kernel_ms_cold_mean": round(fmean, 5),
         "kernel_cold_timing": f"the same kernel launched alone {args.kernel_reps} times, L2/MALL flushed "
-                              "(512 MiB write) before each (median)",
+                              "(512 MiB read) before each (median)",
         "frac_cold": round(F / (fms * 1e-3) / 1e12 / peak, 5),
         "algorithmic_bytes": case.attention_bytes,
     }

@@ -8,6 +8,8 @@
 // every packed row once; unpack writes every padded row once (zeros included).
 #include "fmlm_common.h"
 
+#include <algorithm>
+
 namespace fmlm {
 
 // ---------------------------------------------------------------------------
@@ -166,53 +168,97 @@ struct PackArgs {
 };
 
 // ---------------------------------------------------------------------------
-// Pack: block (TX chunk lanes x TY rows) over grid (row block, tensor*heads, sequence),
-// so the sequence and head come from the block index and no thread divides or searches.
-// Sequence b's rows p < min(L_b, N) go to dst row h*T_pad + cu[b] + p (rows outside
-// [0, T) are skipped); the last grid slice (z = B) zero-fills the rows of [0, T_pad) not
-// covered by [cu[0], cu[B]) (the packed tail [T, T_pad) for consistent metadata).
-// Without cu_seqlens, sequence b covers rows [b*N, (b+1)*N).
+// Span copies.  Pack, unpack and the KV append each move, per (sequence or segment,
+// head), one contiguous run of rows to another contiguous run, with zero rows around.
+// A workgroup takes a window of kWin bytes of one such destination span: every thread
+// moves kPer vectors of VB bytes, issuing all its loads before its stores, and the
+// threads of one vector index cover kSpanThreads * VB consecutive bytes.
 // ---------------------------------------------------------------------------
+constexpr int kSpanThreads = 256;
+constexpr int kPer = 4;
+
 template <int VB>
-__global__ __launch_bounds__(256) void pack_kernel(PackArgs args, int n_tensors, int hmax, int esz,
-                                                   int B, int N, int D,
-                                                   const int32_t* __restrict__ cu, int T,
-                                                   int T_pad) {
+struct Span {
   typedef typename VecOf<VB>::type V;
+  static constexpr int64_t kWin = (int64_t)kSpanThreads * kPer * VB;
+};
+
+// Bytes [w0, w0 + kWin) of a destination span of `len` bytes: offsets below `cpy` come from
+// src at the same offset, the rest are zero.  src_row_bytes / src_pitch (bytes) read a
+// strided source: offset o is row o / src_row_bytes, column o % src_row_bytes, at
+// row * src_pitch + column (src_pitch == src_row_bytes: contiguous).
+template <int VB, bool STRIDED>
+FMLM_DEV void span_window(const char* __restrict__ src, char* __restrict__ dst, int64_t w0, int64_t len,
+                          int64_t cpy, uint32_t src_row_bytes, int64_t src_pitch) {
+  typedef typename Span<VB>::V V;
+  V v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
+    v[i] = V{};
+    if (o < cpy) {
+      int64_t so = o;
+      if constexpr (STRIDED) {
+        const uint32_t r = (uint32_t)o / src_row_bytes;
+        so = (int64_t)r * src_pitch + ((uint32_t)o - r * src_row_bytes);
+      }
+      v[i] = *(const V*)(src + so);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
+    if (o < len) *(V*)(dst + o) = v[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pack: grid (window, tensor*heads, sequence).  Sequence b's rows p < min(L_b, N) of head
+// h go to dst rows h*T_pad + cu[b] + p (clamped to [0, T)); the last grid slice (z = B)
+// zero-fills the rows of [0, T_pad) outside [cu[0], cu[B]) (the packed tail [T, T_pad) for
+// consistent metadata).  Without cu_seqlens, sequence b covers rows [b*N, (b+1)*N).
+// Source rows are contiguous when s_sn is the row length (STRIDED otherwise).
+// ---------------------------------------------------------------------------
+template <int VB, bool STRIDED>
+__global__ __launch_bounds__(kSpanThreads) void pack_kernel(PackArgs args, int n_tensors, int hmax, int esz,
+                                                            int B, int N, int D,
+                                                            const int32_t* __restrict__ cu, int T,
+                                                            int T_pad) {
   const int ti = blockIdx.y / hmax, h = blockIdx.y % hmax;
   if (ti >= n_tensors) return;
   const fmlm_pack_tensor& tt = args.t[ti];
   if (h >= tt.heads) return;
-  const int cpr = D * esz / VB;  // chunks per row
   const int64_t row_bytes = (int64_t)D * esz;
   char* const dst = (char*)tt.dst + (int64_t)h * T_pad * row_bytes;
   const int b = blockIdx.z;
   if (b < B) {
     const int start = cu ? cu[b] : b * N;
-    const int len = min(cu ? cu[b + 1] - start : N, N);
-    const int p = blockIdx.x * blockDim.y + threadIdx.y;
-    if (p >= len) return;
-    const int t = start + p;
-    if (t < 0 || t >= T) return;
-    const char* src = (const char*)tt.src +
-                      ((int64_t)b * tt.s_sb + (int64_t)h * tt.s_sh + (int64_t)p * tt.s_sn) * esz;
-    for (int c = threadIdx.x; c < cpr; c += blockDim.x)
-      *(V*)(dst + (int64_t)t * row_bytes + (int64_t)c * VB) = *(const V*)(src + (int64_t)c * VB);
-  } else {  // zero rows outside [c0, c1)
+    int len = min(cu ? cu[b + 1] - start : N, N);
+    if (start < 0 || start >= T) return;
+    len = min(len, T - start);
+    const int64_t bytes = (int64_t)max(len, 0) * row_bytes;
+    const int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin;
+    if (w0 >= bytes) return;
+    const char* src = (const char*)tt.src + ((int64_t)b * tt.s_sb + (int64_t)h * tt.s_sh) * esz;
+    span_window<VB, STRIDED>(src, dst + (int64_t)start * row_bytes, w0, bytes, bytes, (uint32_t)row_bytes,
+                             tt.s_sn * esz);
+  } else {  // zero rows outside [c0, c1): the spans [0, c0) and [c1, T_pad)
     const int c0 = cu ? min(max(cu[0], 0), T) : 0;
     const int c1 = cu ? min(max(cu[B], c0), T) : T;
-    const int nz = c0 + (T_pad - c1);
-    for (int r = blockIdx.x * blockDim.y + threadIdx.y; r < nz; r += gridDim.x * blockDim.y) {
-      const int t = r < c0 ? r : c1 + (r - c0);
-      for (int c = threadIdx.x; c < cpr; c += blockDim.x)
-        *(V*)(dst + (int64_t)t * row_bytes + (int64_t)c * VB) = V{};
+    const int64_t lo = (int64_t)c0 * row_bytes, hi = (int64_t)(T_pad - c1) * row_bytes;
+    for (int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin; w0 < lo + hi; w0 += (int64_t)gridDim.x * Span<VB>::kWin) {
+      if (w0 < lo)
+        span_window<VB, false>(nullptr, dst, w0, lo, 0, 1u, 0);
+      else
+        span_window<VB, false>(nullptr, dst + (int64_t)c1 * row_bytes, w0 - lo, hi, 0, 1u, 0);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
 // Unpack: block (TX chunk lanes x TY rows) over grid (row block of N, head, sequence):
-// dst row (b, h, n) = packed row h*p_sh/D + cu[b] + n for n < L_b, zeros otherwise.
+// dst row (b, h, n) = packed row h*p_sh/D + cu[b] + n for n < L_b, zeros otherwise.  (One
+// 16-byte chunk per thread measured faster here than the span windows pack uses.)
 // ---------------------------------------------------------------------------
 template <int VB>
 __global__ __launch_bounds__(256) void unpack_kernel(const char* __restrict__ packed, int64_t p_sh,
@@ -237,44 +283,101 @@ __global__ __launch_bounds__(256) void unpack_kernel(const char* __restrict__ pa
   }
 }
 
-// ---------------------------------------------------------------------------
-// Segment copy (KV append): block (TX chunk lanes x TY rows) over grid (row blocks, head,
-// segment).  Segment c of head h: rows [src_cu[c], src_cu[c+1]) of src (head stride src_sh
-// elements) go to rows [dst_start[c], dst_start[c] + len) of dst (head stride dst_sh).
-// Lengths and starts are clamped to the row counts of src and dst, so inconsistent offsets
-// cannot address outside either tensor.  The row blocks stride over the segment, so the
-// grid does not depend on segment lengths the host has not read.  A null src writes zero
-// rows (src_rows then only bounds the segment offsets).
-// ---------------------------------------------------------------------------
-template <int VB>
-__global__ __launch_bounds__(256) void segment_copy_kernel(const char* __restrict__ src, int64_t src_sh,
-                                                           int src_rows, const int32_t* __restrict__ src_cu,
-                                                           char* __restrict__ dst, int64_t dst_sh, int dst_rows,
-                                                           const int32_t* __restrict__ dst_start, int D,
-                                                           int esz) {
-  typedef typename VecOf<VB>::type V;
-  const int cpr = D * esz / VB;
-  const int h = blockIdx.y, c = blockIdx.z;
-  const int s0 = min(max(src_cu[c], 0), src_rows);
-  const int d0 = min(max(dst_start[c], 0), dst_rows);
-  const int len = min(min(src_cu[c + 1] - s0, src_rows - s0), dst_rows - d0);
-  char* const dbase = dst + ((int64_t)h * dst_sh + (int64_t)d0 * D) * esz;
-  const int64_t row_bytes = (int64_t)D * esz;
-  if (!src) {
-    for (int r = blockIdx.x * blockDim.y + threadIdx.y; r < len; r += gridDim.x * blockDim.y)
-      for (int k = threadIdx.x; k < cpr; k += blockDim.x) *(V*)(dbase + (int64_t)r * row_bytes + (int64_t)k * VB) = V{};
-    return;
-  }
-  const char* const sbase = src + ((int64_t)h * src_sh + (int64_t)s0 * D) * esz;
-  for (int r = blockIdx.x * blockDim.y + threadIdx.y; r < len; r += gridDim.x * blockDim.y)
-    for (int k = threadIdx.x; k < cpr; k += blockDim.x)
-      *(V*)(dbase + (int64_t)r * row_bytes + (int64_t)k * VB) = *(const V*)(sbase + (int64_t)r * row_bytes + (int64_t)k * VB);
-}
-
 // Block shape for a row-copy kernel: TX lanes across a row's chunks, TY rows.
 static dim3 row_block(int cpr) {
   const int tx = cpr < 256 ? cpr : 256;
   return dim3(tx, 256 / tx);
+}
+
+// ---------------------------------------------------------------------------
+// Segment copy (KV append): grid (windows, head, segment).  Segment c of head h: rows
+// [src_cu[c], src_cu[c+1]) of src (head stride src_sh elements) go to rows
+// [dst_start[c], dst_start[c] + len) of dst (head stride dst_sh).  Lengths and starts are
+// clamped to the row counts of src and dst, so inconsistent offsets cannot address
+// outside either tensor.  The windows stride over the segment, so the grid does not
+// depend on segment lengths the host has not read.  A null src writes zero rows (src_rows
+// then only bounds the segment offsets).
+// ---------------------------------------------------------------------------
+template <int VB>
+__global__ __launch_bounds__(kSpanThreads) void segment_copy_kernel(const char* __restrict__ src, int64_t src_sh,
+                                                                    int src_rows, const int32_t* __restrict__ src_cu,
+                                                                    char* __restrict__ dst, int64_t dst_sh,
+                                                                    int dst_rows, const int32_t* __restrict__ dst_start,
+                                                                    int D, int esz) {
+  const int h = blockIdx.y, c = blockIdx.z;
+  const int s0 = min(max(src_cu[c], 0), src_rows);
+  const int d0 = min(max(dst_start[c], 0), dst_rows);
+  const int len = max(min(min(src_cu[c + 1] - s0, src_rows - s0), dst_rows - d0), 0);
+  const int64_t row_bytes = (int64_t)D * esz;
+  const int64_t bytes = (int64_t)len * row_bytes;
+  const char* const sbase = src ? src + ((int64_t)h * src_sh + (int64_t)s0 * D) * esz : nullptr;
+  char* const dbase = dst + ((int64_t)h * dst_sh + (int64_t)d0 * D) * esz;
+  for (int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin; w0 < bytes; w0 += (int64_t)gridDim.x * Span<VB>::kWin)
+    span_window<VB, false>(sbase, dbase, w0, bytes, src ? bytes : 0, 1u, 0);
+}
+
+// ---------------------------------------------------------------------------
+// KV append in one launch: grid (windows, tensor*heads, batch + 1).  Batch c of head h of
+// the merged entry (rows [o_c, o_{c+1}) with o = cu_old + cu_new) is the old rows
+// [cu_old[c], cu_old[c+1]) followed by the new rows [cu_new[c], cu_new[c+1]); the last
+// grid slice zero-fills rows [o_C, t_old + t_new) (the entry's tail, like a prefilled
+// entry's padding rows).  Offsets are clamped to the buffers' rows; workgroup (0, 0, 0)
+// also writes cu_out = o.
+// ---------------------------------------------------------------------------
+struct AppendArgs {
+  fmlm_append_tensor t[2];
+};
+
+template <int VB>
+__global__ __launch_bounds__(kSpanThreads) void kv_append_kernel(AppendArgs args, int n_tensors, int H, int D,
+                                                                 int esz, int C, int t_old, int t_new,
+                                                                 const int32_t* __restrict__ cu_old,
+                                                                 const int32_t* __restrict__ cu_new,
+                                                                 int32_t* __restrict__ cu_out) {
+  typedef typename Span<VB>::V V;
+  const int c = blockIdx.z;
+  if (cu_out && blockIdx.x == 0 && blockIdx.y == 0 && c == 0)
+    for (int i = threadIdx.x; i <= C; i += blockDim.x) cu_out[i] = cu_old[i] + cu_new[i];
+  const int ti = blockIdx.y / H, h = blockIdx.y % H;
+  if (ti >= n_tensors) return;
+  const fmlm_append_tensor& tt = args.t[ti];
+  const int64_t row_bytes = (int64_t)D * esz;
+  const int rows = t_old + t_new;
+  char* const out = (char*)tt.out + (int64_t)h * rows * row_bytes;
+  auto clampr = [](int x, int hi) { return min(max(x, 0), hi); };
+  if (c < C) {
+    const int a0 = clampr(cu_old[c], t_old), a1 = clampr(cu_old[c + 1], t_old);
+    const int b0 = clampr(cu_new[c], t_new), b1 = clampr(cu_new[c + 1], t_new);
+    const int na = max(a1 - a0, 0), nb = max(b1 - b0, 0);
+    const int o0 = clampr(cu_old[c] + cu_new[c], rows);
+    const int64_t old_bytes = (int64_t)min(na, rows - o0) * row_bytes;
+    const int64_t bytes = (int64_t)min(na + nb, rows - o0) * row_bytes;
+    const char* const sa = (const char*)tt.old + ((int64_t)h * t_old + a0) * row_bytes;
+    const char* const sb = (const char*)tt.add + ((int64_t)h * t_new + b0) * row_bytes;
+    char* const d = out + (int64_t)o0 * row_bytes;
+    for (int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin; w0 < bytes; w0 += (int64_t)gridDim.x * Span<VB>::kWin) {
+      V v[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
+        v[i] = V{};
+        if (o < old_bytes)
+          v[i] = *(const V*)(sa + o);
+        else if (o < bytes)
+          v[i] = *(const V*)(sb + (o - old_bytes));
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
+        if (o < bytes) *(V*)(d + o) = v[i];
+      }
+    }
+  } else {  // the tail rows of the head
+    const int o_end = clampr(cu_old[C] + cu_new[C], rows);
+    const int64_t bytes = (int64_t)(rows - o_end) * row_bytes;
+    for (int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin; w0 < bytes; w0 += (int64_t)gridDim.x * Span<VB>::kWin)
+      span_window<VB, false>(nullptr, out + (int64_t)o_end * row_bytes, w0, bytes, 0, 1u, 0);
+  }
 }
 
 // Widest vector width (bytes) that divides the row size and every address.
@@ -357,14 +460,22 @@ extern "C" int fmlm_pack(const fmlm_pack_tensor* tensors, int32_t n_tensors, int
   hipStream_t s = (hipStream_t)stream;
   int hmax = 0;
   for (int i = 0; i < n_tensors; ++i) hmax = tensors[i].heads > hmax ? tensors[i].heads : hmax;
-  const dim3 blk = row_block((int)((int64_t)D * esz / vb));
-  const int64_t gx = ((int64_t)(N > 0 ? N : 1) + blk.y - 1) / blk.y;
+  // windows per sequence span (at most N rows); the zero slice strides over its rows
+  const int64_t win = (int64_t)kSpanThreads * kPer * vb;
+  const int64_t gx = std::max<int64_t>(1, ((int64_t)(N > 0 ? N : 1) * D * esz + win - 1) / win);
   if ((int64_t)hmax * n_tensors > 65535 || B + 1 > 65535 || gx > (1 << 30)) return FMLM_E_ARG;
   const dim3 grid((unsigned)gx, hmax * n_tensors, B + 1);
-#define FMLM_PACK_CASE(VB)                                                                     \
-  case VB:                                                                                     \
-    hipLaunchKernelGGL(pack_kernel<VB>, grid, blk, 0, s, args, n_tensors, hmax, esz, B, N, D, \
-                       cu_seqlens, T, T_pad);                                                  \
+  // source rows are contiguous when every tensor's row stride is the row length
+  bool strided = false;
+  for (int i = 0; i < n_tensors; ++i) strided = strided || tensors[i].s_sn != D;
+#define FMLM_PACK_CASE(VB)                                                                              \
+  case VB:                                                                                              \
+    if (strided)                                                                                        \
+      hipLaunchKernelGGL((pack_kernel<VB, true>), grid, dim3(kSpanThreads), 0, s, args, n_tensors, hmax, \
+                         esz, B, N, D, cu_seqlens, T, T_pad);                                           \
+    else                                                                                                \
+      hipLaunchKernelGGL((pack_kernel<VB, false>), grid, dim3(kSpanThreads), 0, s, args, n_tensors,     \
+                         hmax, esz, B, N, D, cu_seqlens, T, T_pad);                                     \
     break;
   switch (vb) {
     FMLM_PACK_CASE(16)
@@ -425,18 +536,18 @@ extern "C" int fmlm_copy_segments(int32_t elem_bytes, const void* src, int64_t s
                                              (uint64_t)(dst_sh * esz)});
   if (!vb) return FMLM_E_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 blk = row_block((int)((int64_t)D * esz / vb));
-  // enough row blocks per (head, segment) to fill the GPU several times over at the
-  // average segment length; longer segments are covered by the stride loop
+  // windows per (head, segment) at the average segment length; longer segments are
+  // covered by the stride loop
+  const int64_t win = (int64_t)kSpanThreads * kPer * vb;
   const int64_t avg = ((int64_t)src_rows + C - 1) / C;
-  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>((avg + blk.y - 1) / blk.y, 4096));
+  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>((avg * D * esz + win - 1) / win, 4096));
   const dim3 grid((unsigned)gx, H, C);
   const char* sp = (const char*)src;
   char* dp = (char*)dst;
-#define FMLM_SEG_CASE(VB)                                                                              \
-  case VB:                                                                                             \
-    hipLaunchKernelGGL(segment_copy_kernel<VB>, grid, blk, 0, s, sp, src_sh, src_rows, src_cu, dp, dst_sh, \
-                       dst_rows, dst_start, D, esz);                                                    \
+#define FMLM_SEG_CASE(VB)                                                                                   \
+  case VB:                                                                                                  \
+    hipLaunchKernelGGL(segment_copy_kernel<VB>, grid, dim3(kSpanThreads), 0, s, sp, src_sh, src_rows, src_cu, \
+                       dp, dst_sh, dst_rows, dst_start, D, esz);                                             \
     break;
   switch (vb) {
     FMLM_SEG_CASE(16)
@@ -446,5 +557,56 @@ extern "C" int fmlm_copy_segments(int32_t elem_bytes, const void* src, int64_t s
     FMLM_SEG_CASE(1)
   }
 #undef FMLM_SEG_CASE
+  return launch_status();
+}
+
+extern "C" int fmlm_kv_append(const fmlm_append_tensor* tensors, int32_t n_tensors, int32_t elem_bytes, int32_t H,
+                              int32_t D, int32_t C, int32_t t_old, int32_t t_new, const int32_t* cu_old,
+                              const int32_t* cu_new, int32_t* cu_out, void* stream) {
+  const int esz = elem_bytes;
+  if (!valid_elem_bytes(esz)) return FMLM_E_DTYPE;
+  if (!tensors || n_tensors < 1 || n_tensors > 2 || H < 0 || D < 1 || C < 0 || t_old < 0 || t_new < 0)
+    return FMLM_E_ARG;
+  if (C > 0 && (!cu_old || !cu_new)) return FMLM_E_ARG;
+  const int64_t rows = (int64_t)t_old + t_new;
+  if (rows > 0x7fffffff) return FMLM_E_ARG;
+  if (H == 0 || rows == 0) {  // nothing to move: only the offsets
+    if (!cu_out || C == 0) return 0;
+    AppendArgs args = {};
+    hipLaunchKernelGGL(kv_append_kernel<16>, dim3(1), dim3(kSpanThreads), 0, (hipStream_t)stream, args, 0, 1, D,
+                       esz, C, t_old, t_new, cu_old, cu_new, cu_out);
+    return launch_status();
+  }
+  AppendArgs args = {};
+  int vb = 16;
+  for (int i = 0; i < n_tensors; ++i) {
+    const fmlm_append_tensor& t = tensors[i];
+    if (!t.out || (t_old > 0 && !t.old) || (t_new > 0 && !t.add)) return FMLM_E_ARG;
+    args.t[i] = t;
+    const int v = pick_vec((int64_t)D * esz, {(uint64_t)t.old, (uint64_t)t.add, (uint64_t)t.out});
+    if (!v) return FMLM_E_ALIGN;
+    vb = v < vb ? v : vb;
+  }
+  if ((int64_t)H * n_tensors > 65535 || C + 1 > 65535) return FMLM_E_ARG;
+  // windows per (tensor, head, batch) at the average merged batch length; longer batches
+  // are covered by the stride loop
+  const int64_t win = (int64_t)kSpanThreads * kPer * vb;
+  const int64_t avg = (rows + C) / (C + 1);
+  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>((avg * D * esz + win - 1) / win, 4096));
+  const dim3 grid((unsigned)gx, H * n_tensors, C + 1);
+  hipStream_t s = (hipStream_t)stream;
+#define FMLM_APPEND_CASE(VB)                                                                              \
+  case VB:                                                                                                \
+    hipLaunchKernelGGL(kv_append_kernel<VB>, grid, dim3(kSpanThreads), 0, s, args, n_tensors, H, D, esz, C, \
+                       t_old, t_new, cu_old, cu_new, cu_out);                                             \
+    break;
+  switch (vb) {
+    FMLM_APPEND_CASE(16)
+    FMLM_APPEND_CASE(8)
+    FMLM_APPEND_CASE(4)
+    FMLM_APPEND_CASE(2)
+    FMLM_APPEND_CASE(1)
+  }
+#undef FMLM_APPEND_CASE
   return launch_status();
 }

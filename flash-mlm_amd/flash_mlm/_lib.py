@@ -100,6 +100,12 @@ class AttnParams(ctypes.Structure):
     ]
 
 
+class AppendTensor(ctypes.Structure):
+    """Mirror of fmlm_append_tensor (include/flash_mlm_hip.h)."""
+
+    _fields_ = [("old", _c_ptr), ("add", _c_ptr), ("out", _c_ptr)]
+
+
 class PackTensor(ctypes.Structure):
     """Mirror of fmlm_pack_tensor (include/flash_mlm_hip.h)."""
 
@@ -150,6 +156,11 @@ SIGNATURES = {
     "fmlm_copy_segments": (
         ctypes.c_int,
         [_c_i32, _c_ptr, _c_i64, _c_i32, _c_ptr, _c_ptr, _c_i64, _c_i32, _c_ptr, _c_i32, _c_i32, _c_i32, _c_ptr],
+    ),
+    "fmlm_kv_append": (
+        ctypes.c_int,
+        [ctypes.POINTER(AppendTensor), _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_ptr, _c_ptr,
+         _c_ptr, _c_ptr],
     ),
     "fmlm_attn_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(AttnParams)]),
     "fmlm_attn_schedule": (ctypes.c_int, [ctypes.POINTER(AttnParams), _c_ptr, _c_i64, _c_ptr]),

@@ -360,8 +360,8 @@ class InferenceCache:
         cu_seqlens_kv = old + new offsets.  Rows per head past the last batch are zero, as
         the zero padding rows of a prefilled packed entry are: a later call that asks for a
         shared context (``context_batch_size=1``) attends to every row of the entry.  The
-        copy is a HIP segment copy per tensor and source, stream-ordered; nothing is read
-        back to the host.
+        merge of K and V (and the new offsets) is one HIP launch, stream-ordered; nothing
+        is read back to the host.
         """
         key = self._layer_key(layer_id)
         entry = self._layer_kv.get(key)
@@ -392,32 +392,16 @@ class InferenceCache:
             cu_host = cu_seqlens_kv.to(torch.int64)
             if int(cu_host[0]) != 0 or bool((cu_host[1:] < cu_host[:-1]).any()) or int(cu_host[-1]) > t_new:
                 raise ValueError("cu_seqlens_kv must start at 0, be non-decreasing and end within the new rows")
-        from flash_mlm.host.host_utils import copy_segments
+        from flash_mlm.host.host_utils import kv_append
 
         dev = entry.device
         cu_old = entry.cu_seqlens_kv.to(device=dev, dtype=torch.int32).contiguous()
         cu_new = cu_seqlens_kv.to(device=dev, dtype=torch.int32).contiguous()
-        cu_out = cu_old + cu_new
-        start_old = cu_out[:-1].contiguous()            # batch c's old rows open its segment
-        start_new = (cu_old[1:] + cu_new[:-1]).contiguous()  # its new rows follow them
         rows = t_old + t_new
-        # rows [cu_out[-1], rows) of each head: one zero segment, sized on the device
-        tail_cu = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev), rows - cu_out[-1:]])
-        tail_start = cu_out[-1:].contiguous()
-
-        def merged(old: torch.Tensor, new: torch.Tensor) -> torch.Tensor:
-            out = torch.empty((h_kv * rows, d), dtype=entry.dtype, device=dev)
-            if n_batch > 0:
-                old = old.contiguous()
-                new = new.contiguous()
-                copy_segments(old, t_old, cu_old, out, rows, start_old, n_batch, h_kv, d)
-                copy_segments(new, t_new, cu_new, out, rows, start_new, n_batch, h_kv, d)
-            if rows > 0:
-                copy_segments(None, rows, tail_cu, out, rows, tail_start, 1, h_kv, d)
-            return out
-
-        k_out = merged(entry.k_cache, k_cache)
-        v_out = None if entry.is_mla else merged(entry.v_cache, v_cache)
+        pairs = [(entry.k_cache, k_cache)] + ([] if entry.is_mla else [(entry.v_cache, v_cache)])
+        outs, cu_out = kv_append(pairs, cu_old, cu_new, heads=h_kv, rows_old=t_old, rows_new=t_new)
+        k_out = outs[0]
+        v_out = None if entry.is_mla else outs[1]
         self._layer_kv[key] = LayerKVEntry(
             k_cache=k_out,
             v_cache=v_out,

@@ -680,3 +680,32 @@ def copy_segments(src: torch.Tensor | None, src_rows: int, src_cu: torch.Tensor,
             dst.data_ptr(), dst_rows * D, dst_rows, dst_start.data_ptr(), C, H, D, _lib.stream_of(dst.device),
         )
     _lib.check(rc, "fmlm_copy_segments")
+
+
+def kv_append(pairs, cu_old: torch.Tensor, cu_new: torch.Tensor, *, heads: int, rows_old: int, rows_new: int):
+    """The merge of :meth:`InferenceCache.append_kv_cache` in one HIP launch
+    (fmlm_kv_append): for each (old [heads*rows_old, D], new [heads*rows_new, D]) pair a
+    new head-major buffer whose batch c holds its old rows then its new rows, zero rows
+    past the last batch; returns (buffers, int32 offsets cu_old + cu_new).  No
+    counterpart in the reference."""
+    old0 = pairs[0][0]
+    dev, dt = old0.device, old0.dtype
+    d = int(old0.shape[1])
+    _require_device(cu_old, cu_new, *(t for pr in pairs for t in pr), what="kv_append")
+    rows = rows_old + rows_new
+    C = int(cu_old.numel()) - 1
+    outs, keep = [], []
+    arr = (_lib.AppendTensor * len(pairs))()
+    for i, (old, new) in enumerate(pairs):
+        old, new = old.contiguous(), new.contiguous()
+        out = torch.empty((heads * rows, d), dtype=dt, device=dev)
+        arr[i].old, arr[i].add, arr[i].out = old.data_ptr(), new.data_ptr(), out.data_ptr()
+        outs.append(out)
+        keep += [old, new]
+    cu_out = torch.empty_like(cu_old)
+    lib = _lib.load()
+    with _device_scope(dev):
+        rc = lib.fmlm_kv_append(arr, len(pairs), old0.element_size(), heads, d, C, rows_old, rows_new,
+                                cu_old.data_ptr(), cu_new.data_ptr(), cu_out.data_ptr(), _lib.stream_of(dev))
+    _lib.check(rc, "fmlm_kv_append")
+    return outs, cu_out

@@ -150,6 +150,26 @@ FMLM_API int fmlm_copy_segments(int32_t elem_bytes, const void* src, int64_t src
                                 const int32_t* dst_start, int32_t C, int32_t H, int32_t D, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * KV append in one launch (InferenceCache.append_kv_cache): for up to 2 tensors (K, V),
+ * heads h < H and batches c < C, the merged head-major entry out [H*(t_old+t_new), D]
+ * holds, at rows h*(t_old+t_new) + [o_c, o_{c+1}) with o = cu_old + cu_new, the old rows
+ * [cu_old[c], cu_old[c+1]) of head h of `old` ([H*t_old, D]) followed by the new rows
+ * [cu_new[c], cu_new[c+1]) of head h of `add` ([H*t_new, D]); rows [o_C, t_old+t_new) of
+ * every head are zero.  cu_out (C+1 int32, may be NULL) receives o.  Offsets are clamped
+ * to the buffers' rows.  No counterpart in the reference, which replaces a layer's
+ * context on prefill and lists appends with paged KV on its roadmap (README.md:34-41).
+ * ------------------------------------------------------------------------- */
+typedef struct fmlm_append_tensor {
+  const void* old; /* [H * t_old, D] contiguous */
+  const void* add; /* [H * t_new, D] contiguous */
+  void* out;       /* [H * (t_old + t_new), D] contiguous */
+} fmlm_append_tensor;
+
+FMLM_API int fmlm_kv_append(const fmlm_append_tensor* tensors, int32_t n_tensors, int32_t elem_bytes, int32_t H,
+                            int32_t D, int32_t C, int32_t t_old, int32_t t_new, const int32_t* cu_old,
+                            const int32_t* cu_new, int32_t* cu_out, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Fused MLM attention forward, dense and packed (mlm_kernel_impl.py:65-216, 219-390).
  *
  * For every sequence b < B, head h < H and query position p < L_b

@@ -51,6 +51,8 @@ def test_argument_rejection_without_launch():
     assert lib.fmlm_copy_segments(2, None, 16, 4, None, None, 16, 4, None, 1, 1, 16, None) == -1
     assert lib.fmlm_copy_segments(3, None, 16, 4, None, None, 16, 4, None, 1, 1, 16, None) == -2
     assert lib.fmlm_copy_segments(2, None, 16, 0, None, None, 16, 4, None, 1, 1, 16, None) == 0  # nothing to copy
+    assert lib.fmlm_kv_append(None, 1, 2, 1, 16, 1, 4, 4, None, None, None, None) == -1
+    assert lib.fmlm_kv_append(None, 1, 3, 1, 16, 1, 4, 4, None, None, None, None) == -2  # bad element size
     assert lib.fmlm_pack_metadata(None, 0, 1, 4, 0, None, None, None, None, None, None) == -1
     assert lib.fmlm_tile_map(None, 1, 4, 0, None, None, None, None) == -1
     assert lib.fmlm_attn_fwd(None, None) == -1

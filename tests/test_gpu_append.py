@@ -187,3 +187,57 @@ def test_append_errors(device):
         cache.append_kv_cache(0, k_cache=k, v_cache=k, cu_seqlens_kv=torch.tensor([0, 2, 5], dtype=torch.int32))
     with pytest.raises(ValueError, match="non-decreasing"):
         cache.append_kv_cache(0, k_cache=k, v_cache=k, cu_seqlens_kv=torch.tensor([0, 3, 2], dtype=torch.int32))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_copy_segments_and_zero_segments(dtype, device):
+    """fmlm_copy_segments (the ABI's general segment copy) bit-exact against numpy, with a
+    null source writing zero rows; offsets past the buffers are clamped."""
+    from flash_mlm.host.host_utils import copy_segments
+
+    torch.manual_seed(5400)
+    H, D, src_rows, dst_rows = 3, 64, 50, 70
+    src = torch.randn((H * src_rows, D), device=device).to(dtype)
+    dst = torch.randn((H * dst_rows, D), device=device).to(dtype)
+    ref = _np(dst.float()).copy()
+    src_cu = [0, 10, 10, 45]
+    dst_start = [5, 60, 30]
+    copy_segments(src, src_rows, torch.tensor(src_cu, dtype=torch.int32, device=device), dst, dst_rows,
+                  torch.tensor(dst_start, dtype=torch.int32, device=device), 3, H, D)
+    s, r = _np(src.float()), ref
+    for h in range(H):
+        for c in range(3):
+            n = src_cu[c + 1] - src_cu[c]
+            n = min(n, dst_rows - dst_start[c])
+            r[h * dst_rows + dst_start[c] : h * dst_rows + dst_start[c] + n] = \
+                s[h * src_rows + src_cu[c] : h * src_rows + src_cu[c] + n]
+    np.testing.assert_array_equal(_np(dst.float()), r)
+    # zero rows [20, 33) of every head
+    copy_segments(None, dst_rows, torch.tensor([0, 13], dtype=torch.int32, device=device), dst, dst_rows,
+                  torch.tensor([20], dtype=torch.int32, device=device), 1, H, D)
+    for h in range(H):
+        r[h * dst_rows + 20 : h * dst_rows + 33] = 0
+    np.testing.assert_array_equal(_np(dst.float()), r)
+
+
+@pytest.mark.parametrize("case", ["no_new_rows", "no_old_rows", "empty_batches"])
+def test_append_edge_cases(case, device):
+    """The one-launch merge at its edges: nothing new, an entry of no rows, empty batches;
+    bit-exact against the oracle's merge, zero tail included."""
+    torch.manual_seed(5500)
+    H, D, dtype = 2, 128, torch.float16
+    lengths = {"no_new_rows": [4, 9], "no_old_rows": [0, 0], "empty_batches": [0, 7]}[case]
+    new_len = {"no_new_rows": [0, 0], "no_old_rows": [3, 5], "empty_batches": [0, 2]}[case]
+    cache = InferenceCache()
+    k0, v0, cu0 = _entry(cache, H=H, D=D, mla=False, dtype=dtype, device=device, lengths=lengths, extra_rows=2)
+    cu1 = _cu(new_len)
+    t1 = int(cu1[-1])
+    k1 = torch.randn((H * t1, D), device=device).to(dtype)
+    v1 = torch.randn((H * t1, D), device=device).to(dtype)
+    cache.append_kv_cache(0, k_cache=k1, v_cache=v1, cu_seqlens_kv=cu1.to(device))
+    e = cache._layer_kv["0"]
+    ref_k, ref_cu = pack_ref.append_segments(_np(k0.float()), _np(cu0), _np(k1.float()), _np(cu1), H)
+    ref_v, _ = pack_ref.append_segments(_np(v0.float()), _np(cu0), _np(v1.float()), _np(cu1), H)
+    np.testing.assert_array_equal(_np(e.cu_seqlens_kv), ref_cu)
+    np.testing.assert_array_equal(_np(e.k_cache.float()), ref_k)
+    np.testing.assert_array_equal(_np(e.v_cache.float()), ref_v)
