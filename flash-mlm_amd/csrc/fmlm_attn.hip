@@ -1503,6 +1503,8 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
   }
   float m_i = -INFINITY, l_i = 0.f;
 
+  // the two segments unrolled: a run-time index into w.seg would put w in scratch memory
+#pragma unroll
   for (int si = 0; si < 2; ++si) {
     const KvSeg& s = w.seg[si];
     for (int j0 = 0; j0 < s.n; j0 += C::BKS) {
