@@ -23,6 +23,7 @@
 #include "fmlm_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 
 namespace fmlm {
@@ -701,8 +702,11 @@ struct KeyCursor {
   PageWindow pw;     // paged segment: page ids of the tiles around `tile`
 };
 
-template <typename T, int D, int QB, int NW, int BK>
+// PPB > 0: the ping-pong schedule (8 waves in two groups of 4, one half-step apart) with
+// PPB buffers per tensor; 0: the single-group schedule with K[2], V[3]
+template <typename T, int D, int QB, int NW, int BK, int PPB = 0>
 struct Mfma3Cfg {
+  static constexpr bool PP = PPB > 0;
   static constexpr int NT = NW * 64;
   static constexpr int BQ = NW * QB * 16;
   static constexpr int ROWB = D * 2;          // bytes per K / V row (unpadded)
@@ -711,7 +715,9 @@ struct Mfma3Cfg {
   static constexpr int RPI = 64 / CPR;        // rows per wave-wide direct load
   static constexpr int NINST = BK / RPI;      // wave-wide loads per tile per tensor
   static constexpr int NPW = (NINST + NW - 1) / NW;  // ... per wave
-  static constexpr int LDS_BYTES = 5 * TILEB;  // K[2], V[3]
+  static constexpr int NKBUF = PP ? PPB : 2;
+  static constexpr int NVBUF = PP ? PPB : 3;
+  static constexpr int LDS_BYTES = (NKBUF + NVBUF) * TILEB;
   static constexpr int KC = (D + 31) / 32;
   static constexpr int NDB = D / 16;
   static constexpr int NKB = BK / 16;
@@ -721,16 +727,17 @@ struct Mfma3Cfg {
   static constexpr int NVF = NKS * NDB;   // V fragment (tr16 pair) reads per step
   static_assert(D % 16 == 0 && D >= 16 && D <= 256, "head dim");
   static_assert(BK % 32 == 0 && BK % RPI == 0, "key tile");
+  static_assert(!PP || (NW == 8 && NINST % NW == 0 && PPB >= 3), "ping-pong: two groups of 4 waves, equal loads");
 };
 
-template <typename T, int D, int QB, int NW, int BK, bool PAGED>
+template <typename T, int D, int QB, int NW, int BK, bool PAGED, int PPB>
 __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
-  typedef Mfma3Cfg<T, D, QB, NW, BK> C;
+  typedef Mfma3Cfg<T, D, QB, NW, BK, PPB> C;
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
-  char* const kbuf = smem_raw;                   // [2][TILEB]
-  char* const vbuf = smem_raw + 2 * C::TILEB;    // [3][TILEB]
+  char* const kbuf = smem_raw;                             // [NKBUF][TILEB]
+  char* const vbuf = smem_raw + C::NKBUF * C::TILEB;       // [NVBUF][TILEB]
 
   WorkItem w;
   if (!resolve_work(p, units, n_units, C::BQ, w)) return;
@@ -935,19 +942,9 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     else
       __builtin_amdgcn_s_waitcnt(0);
   };
-  // One pipeline step: sc holds S(t) and mx its row maxima; computes sn = S(t+1) from the
-  // K tile at byte offset kn (from the first K buffer) and its maxima, consumes V(t) at
-  // byte offset vt (from the first V buffer), refills kdst with K(t+2) and vdst with V(t+2).
-  auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
-                  uint32_t kn, uint32_t vt, char* kdst, char* vdst) {
-    if (t + 2 < te) fetch(kcur, kdst, false);
-    if (t + 2 < te) fetch(vcur, vdst, true);
-    if (!wave_active) {  // every query row of this wave is padding: loads and barriers only
-      vwait(t);
-      __syncthreads();
-      return;
-    }
-
+  // Rescale decision for tile t from the row maxima mx of S(t) (sc), and the -inf mask of
+  // the keys past a partial tile's end.
+  auto prepare = [&](int t, f32x4 (&sc)[C::NKB][QB], float (&mx)[QB]) {
     bool need_rescale = false;
     float m_new[QB];
 #pragma unroll
@@ -981,22 +978,28 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) sc[kb][qb][r] = -INFINITY;
     }
+  };
 
-    // ---- one basic block from here to the barrier, written as a sequence of slots
-    // fenced by sched_barrier so the order below is the issue order.  Slot s runs the
-    // MFMAs of operand fragment s: fragments [0, NKF) are K(t+1) fragments (S(t+1),
-    // beside a share of the exp work of P(t)), fragments [NKF, NKF+NVF) are V(t)
-    // fragments (O += V^T P, beside a share of the row-max work of S(t+1)).  The LDS
-    // read of fragment s + C::LEAD is issued at the top of slot s.
-    constexpr int NF = C::NKF + C::NVF;
+  // ---- the fused block of a step, as a sequence of slots fenced by sched_barrier so the
+  // order below is the issue order.  Slot s runs the MFMAs of operand fragment s:
+  // fragments [0, NKF) are K(t+1) fragments (S(t+1) = sn from the K tile at byte offset kn
+  // from the first K buffer, beside a share of the exp work of P(t) from sc), fragments
+  // [NKF, NKF+NVF) are V(t) fragments (O += V^T P from the V tile at byte offset vt from
+  // the first V buffer, beside a share of the row-max work of S(t+1) into mx).  The LDS
+  // read of fragment s + C::LEAD is issued at the top of slot s (within [S0, S1)).  Phase A
+  // (slots [0, NKF)) leaves P(t) in pf for phase B.
+  constexpr int NF = C::NKF + C::NVF;
+  constexpr int NP = C::NKB * QB * 2;    // exp pairs
+  constexpr int NMS = C::NKB * QB + QB;  // row-max steps
+  u32x4 pf[C::NKS][QB];  // P(t) as packed pairs, the B operand of P V
+  float mpart[QB];
+  auto run_slots = [&](auto s0c, auto s1c, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB],
+                       float (&mx)[QB], uint32_t kn, uint32_t vt) {
+    constexpr int S0 = decltype(s0c)::value, S1 = decltype(s1c)::value;
     f32x4 minit[QB];  // -m_i splat: the initial S accumulators
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) minit[qb] = f32x4{-m_i[qb], -m_i[qb], -m_i[qb], -m_i[qb]};
-    constexpr int NP = C::NKB * QB * 2;    // exp pairs
-    constexpr int NMS = C::NKB * QB + QB;  // row-max steps
     v8 fr[C::LEAD + 1];
-    u32x4 pf[C::NKS][QB];  // P(t) as packed pairs, the B operand of P V
-    float mpart[QB];
     auto issue = [&](int r) {
       if (r < C::NKF) {
         const int kc = r / C::NKB, kb = r % C::NKB;
@@ -1038,14 +1041,19 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       }
     };
 #pragma unroll
-    for (int r = 0; r < C::LEAD; ++r) issue(r);
+    for (int r = S0; r < S0 + C::LEAD && r < S1; ++r) issue(r);
     // wave priority: a wave in its MFMA-dense block issues ahead of the other waves on its
     // SIMD (their loads, branches and softmax VALU fill the gaps), the P V phase highest
-    __builtin_amdgcn_s_setprio(1);
+#ifndef FMLM_PP_PRIO_A
+#define FMLM_PP_PRIO_A 1
+#define FMLM_PP_PRIO_B 2
+#endif
+    constexpr int PRA = C::PP ? FMLM_PP_PRIO_A : 1, PRB = C::PP ? FMLM_PP_PRIO_B : 2;
+    __builtin_amdgcn_s_setprio(S0 < C::NKF ? PRA : PRB);
 #pragma unroll
-    for (int sl = 0; sl < NF; ++sl) {
-      if (sl + C::LEAD < NF) issue(sl + C::LEAD);
-      if (sl == C::NKF) __builtin_amdgcn_s_setprio(2);
+    for (int sl = S0; sl < S1; ++sl) {
+      if (sl + C::LEAD < S1) issue(sl + C::LEAD);
+      if (sl == C::NKF && sl != S0) __builtin_amdgcn_s_setprio(PRB);
       const v8 a = fr[sl % (C::LEAD + 1)];
       if (sl < C::NKF) {
         const int kc = sl / C::NKB, kb = sl % C::NKB;
@@ -1069,6 +1077,25 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_setprio(0);
+  };
+  typedef std::integral_constant<int, 0> Slot0;
+  typedef std::integral_constant<int, C::NKF> SlotB;
+  typedef std::integral_constant<int, NF> SlotEnd;
+
+  // One pipeline step (single-group schedule): sc holds S(t) and mx its row maxima;
+  // computes sn = S(t+1) from the K tile at byte offset kn and its maxima, consumes V(t) at
+  // byte offset vt, refills kdst with K(t+2) and vdst with V(t+2).
+  auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
+                  uint32_t kn, uint32_t vt, char* kdst, char* vdst) {
+    if (t + 2 < te) fetch(kcur, kdst, false);
+    if (t + 2 < te) fetch(vcur, vdst, true);
+    if (!wave_active) {  // every query row of this wave is padding: loads and barriers only
+      vwait(t);
+      __syncthreads();
+      return;
+    }
+    prepare(t, sc, mx);
+    run_slots(Slot0{}, SlotEnd{}, sc, sn, mx, kn, vt);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) sbase[qb] = m_i[qb];
     vwait(t);
@@ -1077,39 +1104,140 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
 
   f32x4 sa[C::NKB][QB], sb[C::NKB][QB];
   float mx[QB];
-  if (te > tb) {
-    cursor_seek(kcur, tb, false);
-    cursor_seek(vcur, tb, true);
-    fetch(kcur, kbuf, false);
-    fetch(vcur, vbuf, true);
-    if (te - tb > 1) fetch(kcur, kbuf + C::TILEB, false);
-    if (te - tb > 1) fetch(vcur, vbuf + C::TILEB, true);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (wave_active) {
-      qk(0, sa);
-      row_max(sa, mx);
+  if constexpr (C::PP) {
+    // ---- ping-pong schedule.  Waves w and w + 4 share a SIMD; group gp = w / 4.  A step
+    // is two half-steps: A(i) = S(t+1) beside the exp of P(t), B(i) = O += V(t)^T P(t)
+    // beside the row maxima of S(t+1) (t = tb + i).  Group 0 runs A(i) in slot 2i and B(i)
+    // in slot 2i+1, group 1 one slot later, so in every slot one wave of each SIMD is in
+    // its exp-heavy half and the other in its MFMA-dense half.  A barrier ends each slot.
+    // Buffers: K(j) in K buffer j % NKBUF, read in slots 2j-2 and 2j-1, refilled (with
+    // K(j + NKBUF)) in slot 2j; V(j) in V buffer j % NVBUF, read in slots 2j+1 and 2j+2,
+    // refilled (with V(j + NVBUF)) in slot 2j+3.  A load issued in slot s is first read
+    // in slot s + 2*NBUF - 2, so it may stay in flight over 2*NBUF - 3 slot ends.
+    static_assert(C::NKBUF == C::NVBUF, "one load window for both tensors");
+    constexpr int WIN = 2 * C::NKBUF - 3;  // slots whose loads may be in flight at a slot end
+    const int gp = wave >> 2;
+    const int n = te - tb;
+    if (n > 0) {
+      cursor_seek(kcur, tb, false);
+      cursor_seek(vcur, tb, true);
+#pragma unroll
+      for (int j = 0; j < C::NKBUF; ++j)
+        if (j < n) fetch(kcur, kbuf + j * C::TILEB, false);
+#pragma unroll
+      for (int j = 0; j < C::NVBUF; ++j)
+        if (j < n) fetch(vcur, vbuf + j * C::TILEB, true);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (wave_active) {
+        qk(0, sa);
+        row_max(sa, mx);
+      }
+      __syncthreads();  // every wave is done with K(0): its buffer may be refilled
     }
-    __syncthreads();  // every wave is done with K(0): its buffer may be refilled
+    // the loads of slot s (every wave issues its share of the tile); returns whether any
+    int hist = 0;  // bit k: slot s - k issued loads
+    auto slot_loads = [&](int s) {
+      const int i = s >> 1;
+      bool any = false;
+      if ((s & 1) == 0) {
+        if (i + C::NKBUF < n) {
+          fetch(kcur, kbuf + (i % C::NKBUF) * C::TILEB, false);
+          any = true;
+        }
+      } else if (i >= 1 && i - 1 + C::NVBUF < n) {
+        fetch(vcur, vbuf + ((i - 1) % C::NVBUF) * C::TILEB, true);
+        any = true;
+      }
+      hist = ((hist << 1) | (any ? 1 : 0)) & ((1 << WIN) - 1);
+    };
+    // end of a slot: the loads issued before the last WIN slots have landed (all of them
+    // unless each of those slots issued its share), then the barrier
+    auto slot_end = [&]() {
+      if (hist == (1 << WIN) - 1)
+        __builtin_amdgcn_s_waitcnt(((WIN * C::NPW) & 15) | (7 << 4) | (15 << 8) | (((WIN * C::NPW) >> 4) << 14));
+      else
+        __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    };
+    auto phase_a = [&](int i, uint32_t kn) {
+      if (wave_active) {
+        prepare(tb + i, sa, mx);
+        run_slots(Slot0{}, SlotB{}, sa, sb, mx, kn, 0u);
+      }
+    };
+    auto phase_b = [&](uint32_t vt) {
+      if (wave_active) {
+        run_slots(SlotB{}, SlotEnd{}, sa, sb, mx, 0u, vt);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) sbase[qb] = m_i[qb];
+      }
+      // unconditional, so that S(t) is dead after phase A on every path
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) sa[kb][qb] = sb[kb][qb];
+    };
+    if (n > 0) {
+      if (gp == 1) {  // group 1 starts one slot late
+        slot_loads(0);
+        slot_end();
+      }
+      // step i of the unit: A(i) reads K buffer (i + 1) % NKBUF, B(i) V buffer i % NVBUF;
+      // NKBUF steps per iteration make both offsets constants of the unrolled step
+      auto pp_step = [&](int i, int u) {
+        slot_loads(2 * i + gp);
+        phase_a(i, ((u + 1) % C::NKBUF) * C::TILEB);
+        slot_end();
+        slot_loads(2 * i + 1 + gp);
+        phase_b((u % C::NVBUF) * C::TILEB);
+        slot_end();
+      };
+      int i = 0;
+      for (; i + C::NKBUF <= n; i += C::NKBUF)
+#pragma unroll
+        for (int u = 0; u < C::NKBUF; ++u) pp_step(i + u, u);
+      for (; i < n; ++i) pp_step(i, i % C::NKBUF);
+      if (gp == 0) {  // group 0 ends one slot early
+        slot_loads(2 * n);
+        slot_end();
+      }
+    }
+  } else {
+    if (te > tb) {
+      cursor_seek(kcur, tb, false);
+      cursor_seek(vcur, tb, true);
+      fetch(kcur, kbuf, false);
+      fetch(vcur, vbuf, true);
+      if (te - tb > 1) fetch(kcur, kbuf + C::TILEB, false);
+      if (te - tb > 1) fetch(vcur, vbuf + C::TILEB, true);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (wave_active) {
+        qk(0, sa);
+        row_max(sa, mx);
+      }
+      __syncthreads();  // every wave is done with K(0): its buffer may be refilled
+    }
+    // step i of the unit uses K buffer i % 2 and V buffer i % 3; six steps per iteration
+    // make every buffer offset a constant of its step (an LDS read address is then the
+    // lane's offset register plus an immediate), the remainder takes them at run time
+    auto step_i = [&](int t, int i) {
+      const int cur = (i & 1) * C::TILEB, nxt = C::TILEB - cur;
+      const int v3 = i % 3;
+      const int vc = v3 * C::TILEB, vd = (v3 == 0 ? 2 : v3 - 1) * C::TILEB;
+      step(t, sa, sb, mx, nxt, vc, kbuf + cur, vbuf + vd);
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) sa[kb][qb] = sb[kb][qb];
+    };
+    int t = tb;
+    for (; t + 6 <= te; t += 6)
+#pragma unroll
+      for (int i = 0; i < 6; ++i) step_i(t + i, i);
+    for (; t < te; ++t) step_i(t, t - tb);
   }
-  // step i of the unit uses K buffer i % 2 and V buffer i % 3; six steps per iteration
-  // make every buffer offset a constant of its step (an LDS read address is then the
-  // lane's offset register plus an immediate), the remainder takes them at run time
-  auto step_i = [&](int t, int i) {
-    const int cur = (i & 1) * C::TILEB, nxt = C::TILEB - cur;
-    const int v3 = i % 3;
-    const int vc = v3 * C::TILEB, vd = (v3 == 0 ? 2 : v3 - 1) * C::TILEB;
-    step(t, sa, sb, mx, nxt, vc, kbuf + cur, vbuf + vd);
-#pragma unroll
-    for (int kb = 0; kb < C::NKB; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) sa[kb][qb] = sb[kb][qb];
-  };
-  int t = tb;
-  for (; t + 6 <= te; t += 6)
-#pragma unroll
-    for (int i = 0; i < 6; ++i) step_i(t + i, i);
-  for (; t < te; ++t) step_i(t, t - tb);
 
   // ---- split part: this part's record (O / l as T, then m and l per row) for
   // merge_kernel
@@ -1664,13 +1792,17 @@ static Launch simt_launch() {
 }
 
 // the paged instantiation only for paged contexts, so the contiguous one keeps its code
-template <typename T, int D, int QB, int NW, int BK>
+template <typename T, int D, int QB, int NW, int BK, int PPB = 0>
 static Launch mfma3_launch(bool paged) {
-  typedef Mfma3Cfg<T, D, QB, NW, BK> C;
+  typedef Mfma3Cfg<T, D, QB, NW, BK, PPB> C;
   static_assert(BK == kSplitBK, "split planning assumes the kernel's key tile");
   static_assert(BK == FMLM_PAGE_ROWS, "a paged context tile is one page");
-  const void* fn = paged ? (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK, true>
-                         : (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK, false>;
+  const void* fn = (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK, false, PPB>;
+  if constexpr (PPB == 0) {
+    if (paged) fn = (const void*)&attn_mfma3_kernel<T, D, QB, NW, BK, true, PPB>;
+  } else if (paged) {  // the ping-pong configurations read contiguous contexts only
+    fn = nullptr;
+  }
   return Launch{C::BQ, C::NT, C::LDS_BYTES, fn, true, false, true};
 }
 
@@ -1714,6 +1846,7 @@ static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
       if (k == 1) L = mfma3_launch<T, 64, 2, 4, 64>(paged);
       else if (k == 2) L = mfma3_launch<T, 64, 2, 8, 64>(paged);
       else if (k == 3) L = mfma3_launch<T, 64, 1, 4, 64>(paged);
+      else if (k == 4) L = mfma3_launch<T, 64, 2, 8, 64, 3>(paged);
       else return false;
       return true;
     case 128:
@@ -1721,6 +1854,7 @@ static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
       else if (k == 2) L = mfma3_launch<T, 128, 2, 8, 64>(paged);
       else if (k == 3) L = mfma3_launch<T, 128, 1, 4, 64>(paged);
       else if (k == 4) L = mfma3_launch<T, 128, 1, 8, 64>(paged);
+      else if (k == 5) L = mfma3_launch<T, 128, 2, 8, 64, 3>(paged);
       else return false;
       return true;
     case 256:
@@ -1759,8 +1893,10 @@ static int pick_launch(const fmlm_attn_params& p, Launch& L) {
     default: return FMLM_E_DTYPE;
   }
   if (!ok) return p.tile_config > 1 ? FMLM_E_ARG : FMLM_E_HEAD_DIM;
-  // a paged context needs a kernel whose key tile is one page (not fp32, not per-row lookups)
+  // a paged context needs a kernel whose key tile is one page (not fp32, not per-row
+  // lookups), and a configuration with a paged instantiation
   if (p.ctx_block_table && !(p.flags & FMLM_FLAG_PREFILL) && !L.paged) return FMLM_E_ARG;
+  if (!L.fn) return FMLM_E_ARG;
   return 0;
 }
 

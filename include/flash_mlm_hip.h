@@ -237,9 +237,11 @@ typedef struct fmlm_attn_params {
    * forces compiled configuration k of the head dim (fmlm_attn_workspace_bytes returns
    * FMLM_E_ARG for a k that does not exist).  Configurations, as (query rows per
    * workgroup, waves per workgroup): D = 16, 32: 1 = (128, 4); D = 64: 1 = (128, 4),
-   * 2 = (256, 8), 3 = (64, 4); D = 128: 1 = (128, 4), 2 = (256, 8), 3 = (64, 4),
-   * 4 = (128, 8); D = 256: 1 = (64, 4),
-   * 2 = (128, 8); MLA D = 512: 1 = (128, 8).  Replaces the reference's autotuned
+   * 2 = (256, 8), 3 = (64, 4), 4 = (256, 8) ping-pong; D = 128: 1 = (128, 4),
+   * 2 = (256, 8), 3 = (64, 4), 4 = (128, 8), 5 = (256, 8) ping-pong; D = 256:
+   * 1 = (64, 4), 2 = (128, 8); MLA D = 512: 1 = (128, 8).  Ping-pong: the 8 waves run as
+   * two groups half a key tile apart, so that one wave of each SIMD computes softmax
+   * while the other issues MFMAs.  Replaces the reference's autotuned
    * BLOCK_M / BLOCK_N / num_warps (mlm_kernel.py:57-166).  Ignored by f32 inputs.       */
   int32_t tile_config;
 } fmlm_attn_params;

@@ -342,7 +342,7 @@ def test_packed_head_dim_dtype_sweep(dtype, D, mode, device):
 # ---------------------------------------------------------------------------
 # every compiled tile configuration (fmlm_attn_params.tile_config), forced
 # ---------------------------------------------------------------------------
-TILE_CONFIGS = {16: (1,), 32: (1,), 64: (1, 2, 3), 128: (1, 2, 3, 4), 256: (1, 2)}
+TILE_CONFIGS = {16: (1,), 32: (1,), 64: (1, 2, 3, 4), 128: (1, 2, 3, 4, 5), 256: (1, 2)}
 
 
 def test_tile_config_table_matches_library(device):
@@ -361,6 +361,13 @@ def test_tile_config_table_matches_library(device):
             assert lib.fmlm_attn_workspace_bytes(p) == -1, (D, p.tile_config)
     p.D, p.flags, p.tile_config = 512, _lib.FLAG_MLA, 2
     assert lib.fmlm_attn_workspace_bytes(p) == -1
+    # the ping-pong configurations (D=64: 4, D=128: 5) read contiguous contexts only
+    p.flags, p.ctx_block_table, p.ctx_pages_per_batch = 0, 4096, 1
+    for D, k in ((64, 4), (128, 5)):
+        p.D, p.tile_config = D, k
+        assert lib.fmlm_attn_workspace_bytes(p) == -1, (D, k)
+        p.tile_config = 1
+        assert lib.fmlm_attn_workspace_bytes(p) >= 0, D
 
 
 @pytest.mark.parametrize("D,k", [(D, k) for D, ks in TILE_CONFIGS.items() for k in ks])
