@@ -651,23 +651,6 @@ FMLM_DEV float lane_max_xor16_32(float x) {
   return vmax(__builtin_bit_cast(float, (int)b[0]), __builtin_bit_cast(float, (int)b[1]));
 }
 
-// An empty asm that claims to rewrite x: arithmetic producing x stays before this point
-// and arithmetic consuming it stays after, in the order of the surrounding side effects.
-template <typename X>
-FMLM_DEV void pin(X& x) { asm volatile("" : "+v"(x)); }
-
-
-template <typename T>
-struct Pair;
-template <>
-struct Pair<bf16> {
-  typedef __bf16 type __attribute__((ext_vector_type(2)));
-};
-template <>
-struct Pair<f16> {
-  typedef _Float16 type __attribute__((ext_vector_type(2)));
-};
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Page ids of 64 consecutive key tiles of a paged segment, one per lane of a VGPR: a tile
 // then costs a lane read.  A page id fetched per tile by a vector load would make its use
@@ -1044,16 +1027,11 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     for (int r = S0; r < S0 + C::LEAD && r < S1; ++r) issue(r);
     // wave priority: a wave in its MFMA-dense block issues ahead of the other waves on its
     // SIMD (their loads, branches and softmax VALU fill the gaps), the P V phase highest
-#ifndef FMLM_PP_PRIO_A
-#define FMLM_PP_PRIO_A 1
-#define FMLM_PP_PRIO_B 2
-#endif
-    constexpr int PRA = C::PP ? FMLM_PP_PRIO_A : 1, PRB = C::PP ? FMLM_PP_PRIO_B : 2;
-    __builtin_amdgcn_s_setprio(S0 < C::NKF ? PRA : PRB);
+    __builtin_amdgcn_s_setprio(S0 < C::NKF ? 1 : 2);
 #pragma unroll
     for (int sl = S0; sl < S1; ++sl) {
       if (sl + C::LEAD < S1) issue(sl + C::LEAD);
-      if (sl == C::NKF && sl != S0) __builtin_amdgcn_s_setprio(PRB);
+      if (sl == C::NKF && sl != S0) __builtin_amdgcn_s_setprio(2);
       const v8 a = fr[sl % (C::LEAD + 1)];
       if (sl < C::NKF) {
         const int kc = sl / C::NKB, kb = sl % C::NKB;

@@ -14,8 +14,9 @@
 //     stores with delta for the next kernel.
 //   attn_bwd_dkv_kernel  one workgroup per 64-key tile of a key segment (the main keys of
 //     a sequence, the causal token range of a head, or a context batch), 16 keys per
-//     wave.  It walks every query row that attends to those keys in steps of 32 rows
-//     staged through LDS and accumulates dK^T = Q^T dS and dV^T = dO^T P in registers.
+//     wave.  It walks every query row that attends to those keys in steps of 64 rows
+//     (32 at D >= 256) staged through LDS and accumulates dK^T = Q^T dS and
+//     dV^T = dO^T P in registers.
 //     Keys whose head stride is 0 (the MLA latent) are shared by all heads and take the
 //     queries of every head; with MLA (V = K) both gradients land in dk.
 // Layouts: every product is in the forward's transposed MFMA form, so the accumulator
@@ -728,6 +729,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   auto dl_s = [&](int i) { return lse_s(i) + C::QS; };
 
   const bool mla = C::MLA_ONLY || (p.flags & FMLM_FLAG_MLA);
+  // software-pipelined step (below) for 64-row steps of unpadded tiles
+  constexpr bool PIPE = !C::PAD && !C::MLA_ONLY && C::QS == 64;
   const int kh = blockIdx.y;
   KeyUnit ku;
   if (!resolve_key_unit<CAUSAL>(p, g, n_ctx, C::DKV_KEYS, ku)) return;
@@ -852,6 +855,111 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     const float* const ls = lse_s(buf);
     const float* const dls = dl_s(buf);
 
+    if constexpr (PIPE) {
+      // ---- the step as one sequence of slots fenced by sched_barrier (the order below is
+      // the issue order).  Slot s runs the KB MFMAs of operand fragment s: row slots
+      // (row block rb of 16 query rows, step kc, Q -> S^T or dO -> dP^T; lane (key + 16g)
+      // reg r = row 16rb + 4g + r), then column slots (32-row group grp, column block db,
+      // dO^T -> dV^T with P or Q^T -> dK^T with dS).  The LDS read of fragment s + LEAD is
+      // issued at the top of slot s.  The softmax of row block rb (P and dS, packed as B
+      // operands: element 4h + r of group rb / 2, h = rb % 2) runs beside the MFMAs of
+      // the next row block, the last block's beside the first group's column slots, so
+      // every column slot finds its operands done.
+      constexpr int NRB = C::QS / 16;
+      constexpr int RBS = 2 * C::KC;      // slots per row block
+      constexpr int NR = NRB * RBS;       // row slots
+      constexpr int NCS = 2 * C::NDB;     // column slots per group
+      constexpr int NS = NR + 2 * NCS;
+      constexpr int LEAD = 3;
+      constexpr int NE2 = KB * 2;         // softmax element pairs per row block and lane
+      f32x4 sc[NRB][KB], dp[NRB][KB], L4[NRB], D4[NRB];
+      u32x4 pbw[2][KB], dsw[2][KB];
+      v8 fr[LEAD + 1];
+      auto issue = [&](int r) {
+        if (r < NR) {
+          const int rb = r / RBS, kc = (r % RBS) >> 1;
+          fr[r % (LEAD + 1)] = tr.row((r & 1) ? ot : qt, rb, kc);
+        } else {
+          const int j = r - NR, grp = j / NCS, db = (j % NCS) >> 1;
+          fr[r % (LEAD + 1)] = tr.col((j & 1) ? qt : ot, grp, db);
+        }
+      };
+      // P and dS of elements r, r + 1 of key block kb (pair e2 = 2 kb + r / 2) of row block rb
+      auto soft_pair = [&](int rb, int e2) {
+        const int kb = e2 >> 1, r = (e2 & 1) * 2, grp = rb >> 1, hh = rb & 1;
+        if (r == 0) {
+          pin(sc[rb][kb]);
+          pin(dp[rb][kb]);
+        }
+        const bool kvalid = kok[kb] && key[kb] < lim;
+        f32x2 pv, ds;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          pv[i] = kvalid ? fast_exp2(fmaf(sc[rb][kb][r + i], c, -L4[rb][r + i])) : 0.f;
+          ds[i] = pv[i] * (dp[rb][kb][r + i] - D4[rb][r + i]) * p.scale;
+        }
+        uint32_t wp = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv, typename Pair<T>::type));
+        uint32_t wd = __builtin_bit_cast(uint32_t, __builtin_convertvector(ds, typename Pair<T>::type));
+        pin(wp);
+        pin(wd);
+        pbw[grp][kb][hh * 2 + (r >> 1)] = wp;
+        dsw[grp][kb][hh * 2 + (r >> 1)] = wd;
+      };
+#pragma unroll
+      for (int r = 0; r < LEAD; ++r) issue(r);
+      // two loops (row slots, column slots): one loop over all of them is too large to
+      // unroll, and the fragment ring must stay in registers
+#pragma unroll
+      for (int sl = 0; sl < NR; ++sl) {
+        if (sl + LEAD < NS) issue(sl + LEAD);
+        const v8 a = fr[sl % (LEAD + 1)];
+        {
+          const int rb = sl / RBS, kc = (sl % RBS) >> 1;
+          if (rb > 0 && sl % RBS == 0) {  // statistics of the block whose softmax runs here
+            L4[rb - 1] = *(const f32x4*)(ls + (rb - 1) * 16 + gq * 4);
+            D4[rb - 1] = *(const f32x4*)(dls + (rb - 1) * 16 + gq * 4);
+          }
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            if ((sl & 1) == 0)
+              sc[rb][kb] = Mfma<T>::run(a, kf[kb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[rb][kb]);
+            else
+              dp[rb][kb] = Mfma<T>::run(a, vf[kb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dp[rb][kb]);
+          }
+          if (rb > 0) {
+            const int loc = sl % RBS;
+#pragma unroll
+            for (int e2 = loc * NE2 / RBS; e2 < (loc + 1) * NE2 / RBS; ++e2) soft_pair(rb - 1, e2);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int sl = NR; sl < NS; ++sl) {
+        if (sl + LEAD < NS) issue(sl + LEAD);
+        const v8 a = fr[sl % (LEAD + 1)];
+        {
+          const int j = sl - NR, grp = j / NCS, db = (j % NCS) >> 1;
+          if (j == 0) {
+            L4[NRB - 1] = *(const f32x4*)(ls + (NRB - 1) * 16 + gq * 4);
+            D4[NRB - 1] = *(const f32x4*)(dls + (NRB - 1) * 16 + gq * 4);
+          }
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            if ((j & 1) == 0) {  // (MLA: dV^T joins dK^T after the last step)
+              dvt[kb][db] = Mfma<T>::run(a, __builtin_bit_cast(v8, pbw[grp][kb]), dvt[kb][db]);
+            } else {
+              dkt[kb][db] = Mfma<T>::run(a, __builtin_bit_cast(v8, dsw[grp][kb]), dkt[kb][db]);
+            }
+          }
+          if (grp == 0) {
+#pragma unroll
+            for (int e2 = j * NE2 / NCS; e2 < (j + 1) * NE2 / NCS; ++e2) soft_pair(NRB - 1, e2);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
     // per 32-row group: S and dP for its two 16-row halves (lane (key + 16g) reg r = row
     // 32grp + 16h + 4g + r), P and dS packed as B operands (element 4h + r), then the
     // dV / dK products.  Each fragment read from LDS feeds the KB key blocks.
@@ -905,8 +1013,17 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       }
     }
     }
+    }
     if constexpr (!C::PAD) buf ^= 1;
     cur = nxt;
+  }
+
+  if constexpr (PIPE) {  // the pipelined steps keep dO^T P apart; with V = K it is part of dK
+    if (mla)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) dkt[kb][db] += dvt[kb][db];
   }
 
   // ---- rows: lane (key + 16g) holds d?[key][16db + 4g .. +4]

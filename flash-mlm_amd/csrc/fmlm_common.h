@@ -163,6 +163,24 @@ FMLM_DEV int k_swz(int r) {
   else return kv_swz<D>(r);
 }
 
+// An empty asm that claims to rewrite x: arithmetic producing x stays before this point
+// and arithmetic consuming it stays after, in the order of the surrounding side effects.
+template <typename X>
+FMLM_DEV void pin(X& x) { asm volatile("" : "+v"(x)); }
+
+// two elements of the input type (a packed 32-bit pair)
+template <typename T>
+struct Pair;
+template <>
+struct Pair<bf16> {
+  typedef __bf16 type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct Pair<f16> {
+  typedef _Float16 type __attribute__((ext_vector_type(2)));
+};
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 FMLM_DEV uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const FMLM_LDS char*)p;
 }
