@@ -30,10 +30,12 @@ namespace fmlm {
 
 // ---------------------------------------------------------------------------
 // Work schedule.  A work unit is (sequence b, head h, query tile j) with tiles of BQ
-// real (unpadded) rows.  Units of one (b, h) group share that group's K/V, so a group
-// is kept on one XCD: the dispatcher hands workgroup L to XCD L % 8, so group g goes
-// to XCD g % 8 and its units occupy consecutive slots x + 8*pos of that XCD.  Groups
-// are visited longest-first (estimated keys x tiles), which also balances the XCDs.
+// real (unpadded) rows.  Units of one (b, h) group share that group's K/V, and the
+// groups of one head may share keys too (a shared context, the causal token range), so
+// groups are kept on few XCDs: the dispatcher hands workgroup L to XCD L % 8, and the
+// units of XCD x occupy its consecutive slots x + 8*pos.  The groups of a head are cut
+// into parts by sequence rank and each XCD takes a run of parts in head order (see
+// schedule_kernel); within a part, groups go longest-first (estimated keys x tiles).
 // Slots past an XCD's share are idle (b = -1).  The list is built once per
 // cu_seqlens by schedule_kernel and cached by the host.
 //
@@ -141,13 +143,36 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
   }
   const int x = tid >> 6, lane = tid & 63;
   const int G = B * HG;
+  // One tile per (sequence, head): the sequences of a head may share its keys (a shared
+  // context, the causal token range), so the groups of a head stay on as few XCDs as
+  // possible.  Head h's groups are cut into K = 8 / gcd(H, 8) parts by rank (rank block j,
+  // ranks [jK, jK + K), gives part p rank jK + p for even j, jK + K - 1 - p for odd j,
+  // which evens out the parts' work; longest first) and XCD x takes parts [x PX, (x + 1) PX) of the H K parts
+  // in head order: every XCD gets PX parts, and a head's keys are read by ceil(8 / H)
+  // XCDs or one more (at most two from 8 heads up).  (Head-packed tiles, and unsorted
+  // batches, go round-robin: group g to XCD g % 8.)
+  const bool by_head = sorted && !hpack;
+  const int K = kXcds / min(H & -H, kXcds);
+  const int PX = H * K / kXcds;
+  const int nrank = (B + K - 1) / K;
   int carry = 0;
-  for (int i0 = 0; x + kXcds * i0 < G; i0 += 64) {
-    const int g = x + kXcds * (i0 + lane);
+  for (int i0 = 0; by_head ? i0 < PX * nrank : x + kXcds * i0 < G; i0 += 64) {
+    bool valid;
+    int r = 0;
     int b = 0, h = 0, tiles = 0, S = 1;
-    if (g < G) {
-      const int r = g / HG;
+    if (by_head) {  // this XCD's group i: part q = x PX + i / nrank, its (i % nrank)-th rank
+      const int i = i0 + lane;
+      const int q = x * PX + i / nrank, j = i % nrank, pq = q % K;
+      h = q / K;
+      r = j * K + ((j & 1) ? K - 1 - pq : pq);  // ranks dealt to the parts back and forth
+      valid = i < PX * nrank && r < B;
+    } else {
+      const int g = x + kXcds * (i0 + lane);
+      valid = g < G;
+      r = g / HG;
       h = g - r * HG;
+    }
+    if (valid) {
       b = sorted ? s_order[r] : r;
       tiles = group_tiles(sorted ? s_tiles[b] : seq_tiles(seq_info(p, b).len), h);
       S = sorted ? s_split[b] : 1;

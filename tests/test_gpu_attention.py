@@ -459,6 +459,65 @@ def test_cached_schedule_per_head_count_and_mode(device):
     assert len(meta.kernel_schedules) == 3
 
 
+def _schedule_units(sched):
+    """Decoded work list of a cached schedule buffer: (slot, b, h, tile, s, S) per non-idle
+    unit (header word 0 = slots; int4 units from byte 256: b, h | tile << 16, record,
+    split word)."""
+    words = sched.view(torch.int32).cpu()
+    n = int(words[0])
+    u = words[64:64 + 4 * n].view(n, 4).tolist()
+    out = []
+    for slot, (b, ht, _, w) in enumerate(u):
+        if b < 0:
+            continue
+        S = ((w >> 25) & 15) + 1 if w >= 0 else 1
+        s = (w >> 20) & 31 if w >= 0 else 0
+        out.append((slot, b, ht & 0xFFFF, ht >> 16, s, S))
+    return out
+
+
+@pytest.mark.parametrize("H,lengths,causal", [
+    (12, [300, 64, 1, 511, 200, 0, 77, 128, 129, 400, 5, 256, 90, 33, 480, 260], True),
+    (12, [300, 64, 1, 511, 200, 0, 77, 128, 129, 400, 5, 256, 90, 33, 480, 260], False),
+    (3, [700, 1, 130, 64, 0, 999], False),
+    (5, [130] * 9 + [1], True),
+    (16, [257, 1000, 3, 128], False),
+    (1, [64 * i + 1 for i in range(20)], False),
+])
+def test_schedule_places_every_tile_once(H, lengths, causal, device):
+    """The work list holds every (sequence, head, 128-row query tile) once, each split into
+    its S parts exactly once, and keeps every head on ceil(8 / H) XCDs or one more (slot %
+    8; at most two from 8 heads up); the result matches the oracle."""
+    torch.manual_seed(7200 + H)
+    B, N, D = len(lengths), max(lengths), 64
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, [200], device, torch.bfloat16, cbs=1)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=causal,
+                                    context_batch_size=1)
+    ref = _packed_oracle(q, k, v, lengths, scale, causal=causal, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=1, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+    (sched,) = meta.kernel_schedules.values()
+    units = _schedule_units(sched)
+    seen = {}
+    for slot, b, h, tile, s, S in units:
+        key = (b, h, tile)
+        assert (key, s) not in seen, (key, s)
+        seen[(key, s)] = S
+    want = {(b, h, t) for b, L in enumerate(lengths) for h in range(H) for t in range((L + 127) // 128)}
+    got = {key for key, _ in seen}
+    assert got == want
+    for key in want:  # every part of a split tile, once
+        S = {seen[(k_, s)] for (k_, s) in seen if k_ == key}
+        assert len(S) == 1
+        (S,) = S
+        assert {s for (k_, s) in seen if k_ == key} == set(range(S))
+    for h in range(H):
+        xcds = {slot % 8 for slot, _, hh, _, _, _ in units if hh == h}
+        assert len(xcds) <= (8 + H - 1) // H + 1, (h, xcds)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [16, 64, 128, 256])
 @pytest.mark.parametrize("is_mla", [False, True])
