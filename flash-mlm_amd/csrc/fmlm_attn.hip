@@ -663,18 +663,6 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(con
 // ---------------------------------------------------------------------------
 
 // NaN-propagating max (v_maximum3_f32): no operand canonicalisation, unlike fmaxf
-FMLM_DEV float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-
-// max over lanes l, l^16, l^32, l^48: permlane16/32_swap(x, x) return {x[l], x[l^16]}
-// resp. {x[l], x[l^32]} in some order
-FMLM_DEV float lane_max_xor16_32(float x) {
-  const int xi = __builtin_bit_cast(int, x);
-  const auto a = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
-  x = vmax(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
-  const int yi = __builtin_bit_cast(int, x);
-  const auto b = __builtin_amdgcn_permlane32_swap(yi, yi, false, false);
-  return vmax(__builtin_bit_cast(float, (int)b[0]), __builtin_bit_cast(float, (int)b[1]));
-}
 
 
 // Page ids of 64 consecutive key tiles of a paged segment, one per lane of a VGPR: a tile

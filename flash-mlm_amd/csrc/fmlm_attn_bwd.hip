@@ -462,6 +462,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   const float c = p.scale * kLog2e;  // scores in log2 units
   // MLA: V is K, so the K tile serves both products and no V tile is loaded
   const bool kv_same = C::MLA_ONLY || (p.flags & FMLM_FLAG_MLA);
+  // software-pipelined tile (below) for the double-buffered unpadded tiles
+  constexpr bool PIPE = !C::PAD && C::DQ_NBUF == 2;
 
   const BSeg sc = ctx_seg(p, g, ctx_batch_of(p, b), h);  // context, then main keys
   const BSeg sm = main_seg(p, g, b, h);
@@ -603,6 +605,144 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     if (C::DQ_NBUF == 2 && t + 1 < nt) issue(t + 1, buf ^ 1);
     const char* const kt = kbuf(buf);
     const char* const vt = kv_same ? kt : vbuf(buf);
+    if constexpr (PIPE) {
+      // ---- the tile as one sequence of fenced slots (the order below is the issue
+      // order): S^T slots (step kc, key block kb: kc-major, so an accumulator's next MFMA
+      // is NKB slots away), then dP^T slots (key block kb, step kc: kb-major, so each
+      // block's dP is done a block before the next), then dq^T slots (key step ks, column
+      // block db).  The LDS read of fragment s + LEAD is issued at the top of slot s.
+      // Beside the MFMAs: the tile's masked row max and lazy rescale during block 0's dP
+      // (every S is done), block kb's exp / dS during block kb + 1's dP, the last block's
+      // during key step 0's dq (which needs blocks 0-1 only).  No exp precedes the tile's
+      // max, so a rescale never touches packed dS.
+      constexpr int NSS = C::KC * C::NKB;      // S slots
+      constexpr int NR = 2 * NSS;              // S slots, then dP slots
+      constexpr int NS = NR + C::NKS * C::NDB;
+      constexpr int LEAD = 3;
+      static_assert(C::NKB == 4 && C::NKS == 2, "64-key tiles");
+      f32x4 sb[C::NKB][QB], dpb[C::NKB][QB];
+      u32x4 dsw[C::NKS][QB];
+      v8 fr[LEAD + 1];
+      auto issue = [&](int r) {
+        if (r < NSS) {
+          fr[r % (LEAD + 1)] = row_frag(kt, r % C::NKB, r / C::NKB);
+        } else if (r < NR) {
+          const int j = r - NSS;
+          fr[r % (LEAD + 1)] = row_frag(vt, j / C::KC, j % C::KC);
+        } else {
+          const int j = r - NR;
+          fr[r % (LEAD + 1)] = col_frag(kt, j / C::NDB, j % C::NDB);
+        }
+      };
+      // the tile's row max of block qb (keys past the tile's end masked to -inf)
+      auto row_max_unit = [&](int qb) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < C::NKB; ++kb) {
+          pin(sb[kb][qb]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float z = kb * 16 + gq * 4 + r < nk ? sb[kb][qb][r] * c : -INFINITY;
+            sb[kb][qb][r] = z;
+            mx = vmax(mx, z);
+          }
+        }
+        mx = lane_max_xor16_32(mx);
+        pin(mx);
+        return mx;
+      };
+      float mt[QB];
+      auto rescale_unit = [&]() {
+        bool grow_any = false;
+        float m_new[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const bool grow = mt[qb] > m_i[qb] + kRescaleSlack;
+          m_new[qb] = grow ? mt[qb] : m_i[qb];
+          grow_any = grow_any || grow;
+        }
+        if (__builtin_amdgcn_ballot_w64(grow_any)) {
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            const float alpha = m_i[qb] == -INFINITY ? 0.f : fast_exp2(m_i[qb] - m_new[qb]);
+            m_i[qb] = m_new[qb];
+            l_i[qb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < C::NDB; ++db) dq[db][qb] *= alpha;
+          }
+        }
+      };
+      // 2^(z - m) (dP - delta) of elements r, r + 1 of key block kb, query block qb
+      // (pair e: qb = e / 2, r = 2 (e % 2))
+      auto soft_block = [&](int kb, int e) {
+        const int qb = e >> 1, r = (e & 1) * 2;
+        if (r == 0) pin(dpb[kb][qb]);
+        const float mref = m_i[qb] == -INFINITY ? 0.f : m_i[qb];  // no key yet: every z is -inf
+        f32x2 pv, ds;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          pv[i] = fast_exp2(sb[kb][qb][r + i] - mref);
+          ds[i] = pv[i] * (dpb[kb][qb][r + i] - delta[qb]);
+        }
+        l_i[qb] += pv[0] + pv[1];
+        uint32_t wd = __builtin_bit_cast(uint32_t, __builtin_convertvector(ds, typename Pair<T>::type));
+        pin(wd);
+        dsw[kb >> 1][qb][(kb & 1) * 2 + (r >> 1)] = wd;
+      };
+#pragma unroll
+      for (int r = 0; r < LEAD; ++r) issue(r);
+#pragma unroll
+      for (int sl = 0; sl < NSS; ++sl) {
+        if (sl + LEAD < NS) issue(sl + LEAD);
+        const v8 a = fr[sl % (LEAD + 1)];
+        const int kb = sl % C::NKB, kc = sl / C::NKB;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          sb[kb][qb] = Mfma<T>::run(a, qf[qb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sb[kb][qb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int sl = NSS; sl < NR; ++sl) {
+        if (sl + LEAD < NS) issue(sl + LEAD);
+        const v8 a = fr[sl % (LEAD + 1)];
+        const int j = sl - NSS, kb = j / C::KC, kc = j % C::KC;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          dpb[kb][qb] = Mfma<T>::run(a, df[qb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dpb[kb][qb]);
+        if (kb == 0) {
+          // the row max, then the rescale, all before block 0's exp in block 1's slots:
+          // one query block per slot from slot 1 where block 0 has the slots for it,
+          // else all in slot 0
+          if constexpr (QB + 1 < C::KC) {
+            if (j >= 1 && j <= QB) mt[j - 1] = row_max_unit(j - 1);
+            if (j == QB + 1) rescale_unit();
+          } else if (j == 0) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) mt[qb] = row_max_unit(qb);
+            rescale_unit();
+          }
+        } else {  // block kb - 1's exp / dS
+          const int loc = j % C::KC;
+#pragma unroll
+          for (int e = loc * 2 * QB / C::KC; e < (loc + 1) * 2 * QB / C::KC; ++e) soft_block(kb - 1, e);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int sl = NR; sl < NS; ++sl) {
+        if (sl + LEAD < NS) issue(sl + LEAD);
+        const v8 a = fr[sl % (LEAD + 1)];
+        const int j = sl - NR, ks = j / C::NDB, db = j % C::NDB;
+        if (ks == 0) {  // the last block's exp / dS
+#pragma unroll
+          for (int e = j * 2 * QB / C::NDB; e < (j + 1) * 2 * QB / C::NDB; ++e) soft_block(C::NKB - 1, e);
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) dq[db][qb] = Mfma<T>::run(a, __builtin_bit_cast(v8, dsw[ks][qb]), dq[db][qb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      continue;
+    }
     f32x4 s[C::NKB][QB], dp[C::NKB][QB];
     scores(kt, s);
     // dP^T = V dO^T, same layout as S^T

@@ -181,6 +181,19 @@ struct Pair<f16> {
 };
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+FMLM_DEV float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// max over lanes l, l^16, l^32, l^48: permlane16/32_swap(x, x) return {x[l], x[l^16]}
+// resp. {x[l], x[l^32]} in some order
+FMLM_DEV float lane_max_xor16_32(float x) {
+  const int xi = __builtin_bit_cast(int, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+  x = vmax(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
+  const int yi = __builtin_bit_cast(int, x);
+  const auto b = __builtin_amdgcn_permlane32_swap(yi, yi, false, false);
+  return vmax(__builtin_bit_cast(float, (int)b[0]), __builtin_bit_cast(float, (int)b[1]));
+}
+
 FMLM_DEV uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const FMLM_LDS char*)p;
 }
