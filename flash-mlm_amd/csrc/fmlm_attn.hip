@@ -1361,9 +1361,8 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   // step kc is at (kk ^ 64*(kc%4)) + kb*16*ROWB + 256*(kc/4); the V tr16 fragment of step
   // ks, column block db, half h at (vv ^ 32*(db%8)) + (32 ks + 16 h)*ROWB + 256*(db/8).
   // The XOR terms select the swizzled 16-byte chunk; they touch bits 5..7 only, which the
-  // row and stage offsets leave clear.  The swizzle is the tr16 one: the b128 K reads of
-  // this tile then take two cycles per 16 lanes, which measured cheaper than reading each
-  // K fragment as two conflict-free 8-byte halves (twice the LDS instructions).
+  // row and stage offsets leave clear.  kv_swz serves both read shapes of the tile (b128
+  // K fragments, tr16 V fragments) without bank conflicts.
   int kk, vv;
   {
     const int ksw = kv_swz<D>(l16);
