@@ -11,7 +11,7 @@
 //   attn_bwd_dq_kernel   one workgroup per (query tile, head, sequence), as in the
 //     forward.  One pass over the key set accumulates dq^T = K^T dS^T with an online
 //     softmax (running max, lazy rescale) and yields each row's log2-sum-exp, which it
-//     stores with delta for the next kernel.
+//     stores with scale * delta for the next kernel.
 //   attn_bwd_dkv_kernel  one workgroup per 64-key tile of a key segment (the main keys of
 //     a sequence, the causal token range of a head, or a context batch), 16 keys per
 //     wave.  It walks every query row that attends to those keys in steps of 64 rows
@@ -491,7 +491,10 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
         rd = ld16((const char*)g.dout, doo + col);
         ro = ld16((const char*)p.o, oo + col);
       }
-      qf[qb][kc] = __builtin_bit_cast(v8, rq);
+      v8 qv = __builtin_bit_cast(v8, rq);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[e] = (T)((float)qv[e] * c);  // S in log2 units
+      qf[qb][kc] = qv;
       df[qb][kc] = __builtin_bit_cast(v8, rd);
       const v8 ov = __builtin_bit_cast(v8, ro);
 #pragma unroll
@@ -636,17 +639,20 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
       };
       // the tile's row max of block qb (keys past the tile's end masked to -inf)
       auto row_max_unit = [&](int qb) {
+#pragma unroll
+        for (int kb = 0; kb < C::NKB; ++kb) pin(sb[kb][qb]);
+        if (nk < kBwdBK) {  // a partial tile: keys past its end to -inf
+          asm volatile("");  // (a real branch: full tiles skip the selects)
+#pragma unroll
+          for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (kb * 16 + gq * 4 + r >= nk) sb[kb][qb][r] = -INFINITY;
+        }
         float mx = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < C::NKB; ++kb) {
-          pin(sb[kb][qb]);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float z = kb * 16 + gq * 4 + r < nk ? sb[kb][qb][r] * c : -INFINITY;
-            sb[kb][qb][r] = z;
-            mx = vmax(mx, z);
-          }
-        }
+        for (int kb = 0; kb < C::NKB; ++kb)
+          mx = vmax(mx, vmax(vmax(sb[kb][qb][0], sb[kb][qb][1]), vmax(sb[kb][qb][2], sb[kb][qb][3])));
         mx = lane_max_xor16_32(mx);
         pin(mx);
         return mx;
@@ -662,6 +668,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
           grow_any = grow_any || grow;
         }
         if (__builtin_amdgcn_ballot_w64(grow_any)) {
+          asm volatile("");  // (a real branch: the rescale is rare)
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) {
             const float alpha = m_i[qb] == -INFINITY ? 0.f : fast_exp2(m_i[qb] - m_new[qb]);
@@ -768,7 +775,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
       for (int kb = 0; kb < C::NKB; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float z = kb * 16 + gq * 4 + r < nk ? s[kb][qb][r] * c : -INFINITY;
+          const float z = kb * 16 + gq * 4 + r < nk ? s[kb][qb][r] : -INFINITY;
           s[kb][qb][r] = z;
           mx = fmaxf(mx, z);
         }
@@ -829,7 +836,9 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     if (gq == 0 && row < si.len) {
       const int64_t at = (int64_t)h * p.total_q + si.q0 + row;
       st_lse[at] = any ? m_i[qb] + __log2f(l) : INFINITY;
-      st_delta[at] = delta[qb];
+      // the dK / dV kernel's dS = P (scale dP - scale delta); the latent's kernel (whose
+      // spills move with any change of its code) keeps delta and multiplies by scale
+      st_delta[at] = C::MLA_ONLY ? delta[qb] : delta[qb] * p.scale;
     }
   }
 
@@ -1036,7 +1045,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           pv[i] = kvalid ? fast_exp2(fmaf(sc[rb][kb][r + i], c, -L4[rb][r + i])) : 0.f;
-          ds[i] = pv[i] * (dp[rb][kb][r + i] - D4[rb][r + i]) * p.scale;
+          ds[i] = pv[i] * fmaf(dp[rb][kb][r + i], p.scale, -D4[rb][r + i]);
         }
         uint32_t wp = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv, typename Pair<T>::type));
         uint32_t wd = __builtin_bit_cast(uint32_t, __builtin_convertvector(ds, typename Pair<T>::type));
@@ -1133,7 +1142,10 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
         for (int r = 0; r < 4; ++r) {
           const float pv = kvalid ? fast_exp2(fmaf(sc[kb][r], c, -L4[r])) : 0.f;
           pb[kb][hh * 4 + r] = (T)pv;
-          dsb[kb][hh * 4 + r] = (T)(pv * (dp[kb][r] - D4[r]) * p.scale);
+          if constexpr (C::MLA_ONLY)
+            dsb[kb][hh * 4 + r] = (T)(pv * (dp[kb][r] - D4[r]) * p.scale);
+          else
+            dsb[kb][hh * 4 + r] = (T)(pv * fmaf(dp[kb][r], p.scale, -D4[r]));
         }
       }
     }
