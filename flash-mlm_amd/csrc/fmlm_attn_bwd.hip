@@ -243,8 +243,8 @@ template <int D, int NR>
 FMLM_DEV void dma_rows(const char* src, uint32_t rowb, int last, uint32_t lds, int wave, int lane) {
   typedef BwdCfg<D> C;
   static_assert(!C::PAD && NR % (C::RPI * kBwdNW) == 0, "whole wave-wide loads per wave");
-  // the lane's offsets are recomputed per call (cheap integer work) rather than hoisted
-  // out of the caller's loop, where they would hold registers through the math
+  // the lane's offsets are recomputed per call (the dq kernel has no registers to hold
+  // them; the pipelined dK / dV step precomputes a whole step's, see dma_rows_at)
   int ln = lane;
   asm volatile("" : "+v"(ln));
   const int row0 = wave * C::RPI + ln / C::CPR;
@@ -255,6 +255,26 @@ FMLM_DEV void dma_rows(const char* src, uint32_t rowb, int last, uint32_t lds, i
     const uint32_t r = (uint32_t)min(row, last);
     dma16_sbase(src, r * rowb + 16u * (uint32_t)((ln % C::CPR) ^ kv_swz<D>(row)),
                 __builtin_amdgcn_readfirstlane(lds + i * 1024));
+  }
+}
+
+// The loads of dma_rows with the lane's byte offsets precomputed for a whole tile (no row
+// past the end): off[j] = row_j * rowb + 16 * (chunk ^ kv_swz(row_j)).
+template <int D, int NR>
+FMLM_DEV void dma_rows_at(const char* src, const uint32_t (&off)[NR / (BwdCfg<D>::RPI * kBwdNW)], uint32_t lds,
+                          int wave) {
+#pragma unroll
+  for (int j = 0; j < NR / (BwdCfg<D>::RPI * kBwdNW); ++j)
+    dma16_sbase(src, off[j], __builtin_amdgcn_readfirstlane(lds + (wave + j * kBwdNW) * 1024));
+}
+template <int D, int NR>
+FMLM_DEV void dma_offsets(uint32_t rowb, int lane, int wave, uint32_t (&off)[NR / (BwdCfg<D>::RPI * kBwdNW)]) {
+  typedef BwdCfg<D> C;
+  const int row0 = wave * C::RPI + lane / C::CPR;
+#pragma unroll
+  for (int j = 0; j < NR / (C::RPI * kBwdNW); ++j) {
+    const int row = row0 + j * kBwdNW * C::RPI;
+    off[j] = (uint32_t)row * rowb + 16u * (uint32_t)((lane % C::CPR) ^ kv_swz<D>(row));
   }
 }
 
@@ -929,6 +949,13 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   // through registers into its single buffer after the previous step's reads.
   const int hq_lo = ku.shared ? 0 : kh, hq_hi = ku.shared ? p.H : kh + 1;
   const QuerySteps steps{&p, &ku, hq_hi, C::QS};
+  // the lane's direct-load offsets of a whole step of Q and of dO rows
+  constexpr int NPQ = PIPE ? C::QS / (C::RPI * kBwdNW) : 1;
+  uint32_t q_off[NPQ], o_off[NPQ];
+  if constexpr (PIPE) {
+    dma_offsets<D, C::QS>(__builtin_amdgcn_readfirstlane((uint32_t)p.q_sn * 2u), lane, wave, q_off);
+    dma_offsets<D, C::QS>(__builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), lane, wave, o_off);
+  }
   float lreg = INFINITY, dlreg = 0.f;
   auto prep = [&](const QStep& st, int buf) {
     const SeqInfo si = seq_info(p, st.b);
@@ -972,10 +999,17 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       const int last = min(C::QS, si.len - st.p0) - 1;
       const int64_t qe = row_at(p.q_layout, st.b, st.hq, si.q0, st.p0, p.q_sb, p.q_sh, p.q_sn);
       const int64_t de = row_at(p.o_layout, st.b, st.hq, si.q0, st.p0, g.do_sb, g.do_sh, g.do_sn);
-      dma_rows<D, C::QS>(uniform_ptr((const char*)p.q + qe * 2), __builtin_amdgcn_readfirstlane((uint32_t)p.q_sn * 2u),
-                         last, lds_addr(qbuf(buf)), wave, lane);
-      dma_rows<D, C::QS>(uniform_ptr((const char*)g.dout + de * 2),
-                         __builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), last, lds_addr(obuf(buf)), wave, lane);
+      const char* const qs = uniform_ptr((const char*)p.q + qe * 2);
+      const char* const ds = uniform_ptr((const char*)g.dout + de * 2);
+      if constexpr (PIPE) {
+        if (last == C::QS - 1) {  // a whole step: the precomputed offsets
+          dma_rows_at<D, C::QS>(qs, q_off, lds_addr(qbuf(buf)), wave);
+          dma_rows_at<D, C::QS>(ds, o_off, lds_addr(obuf(buf)), wave);
+          return;
+        }
+      }
+      dma_rows<D, C::QS>(qs, __builtin_amdgcn_readfirstlane((uint32_t)p.q_sn * 2u), last, lds_addr(qbuf(buf)), wave, lane);
+      dma_rows<D, C::QS>(ds, __builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), last, lds_addr(obuf(buf)), wave, lane);
     }
   };
   const TileReader<T, D> tr(l16, gq);
