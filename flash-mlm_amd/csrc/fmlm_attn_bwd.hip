@@ -160,7 +160,7 @@ FMLM_DEV BSeg main_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int 
   s.dvsn = dv_sn;
   const bool causal = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q;
   if (causal) {  // packed K/V: token j is row h*sh + j*sn
-    s.n = b < 0 ? min(p.cu_seqlens_q[p.B], p.total_q) : seq_info(p, b).mainlen;
+    s.n = b < 0 ? min(ldc(p.cu_seqlens_q, p.B), p.total_q) : seq_info(p, b).mainlen;
     s.kbase = (int64_t)h * p.k_sh;
     s.vbase = (int64_t)h * v_sh;
     s.dkbase = (int64_t)h * g.dk_sh;
@@ -391,13 +391,13 @@ FMLM_DEV bool resolve_key_unit(const fmlm_attn_params& p, const fmlm_attn_grads&
   const int32_t* cu = p.cu_seqlens_q;
   const int kh = blockIdx.y;
   const UnitTables ut = unit_tables(p, g);
-  const int n_main = CAUSAL ? (min(cu[p.B], p.total_q) + keys - 1) / keys : ut.k[p.B];
-  const int n_cunits = n_ctx > 0 ? ut.c[n_ctx] : 0;
+  const int n_main = CAUSAL ? (min(ldc(cu, p.B), p.total_q) + keys - 1) / keys : ldc(ut.k, p.B);
+  const int n_cunits = n_ctx > 0 ? ldc(ut.c, n_ctx) : 0;
   const int u = blockIdx.x;
   k.is_ctx = u < n_cunits;
   if (k.is_ctx) {
     k.slot = find_seq(ut.c, n_ctx, u);
-    k.j0 = (u - ut.c[k.slot]) * keys;
+    k.j0 = (u - ldc(ut.c, k.slot)) * keys;
   } else {
     const int um = u - n_cunits;
     if (um >= n_main) return false;
@@ -406,7 +406,7 @@ FMLM_DEV bool resolve_key_unit(const fmlm_attn_params& p, const fmlm_attn_grads&
       k.j0 = um * keys;
     } else {
       k.slot = find_seq(ut.k, p.B, um);
-      k.j0 = (um - ut.k[k.slot]) * keys;
+      k.j0 = (um - ldc(ut.k, k.slot)) * keys;
     }
   }
   k.causal_main = CAUSAL && !k.is_ctx;
@@ -471,11 +471,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
 
   const UnitTables ut = unit_tables(p, g);
   const int u = blockIdx.x, h = blockIdx.y;
-  if (u >= ut.q[p.B]) return;
+  if (u >= ldc(ut.q, p.B)) return;
   const int rk = find_seq(ut.q, p.B, u);  // table entry: sequences by key count, largest first
-  const int b = ut.perm[rk];
+  const int b = ldc(ut.perm, rk);
   const SeqInfo si = seq_info(p, b);
-  const int qpos0 = (u - ut.q[rk]) * C::BQ;
+  const int qpos0 = (u - ldc(ut.q, rk)) * C::BQ;
   if (qpos0 >= si.len) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
@@ -1292,11 +1292,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_p
 
   const UnitTables ut = unit_tables(p, g);
   const int u = blockIdx.x, h = blockIdx.y;
-  if (u >= ut.q[p.B]) return;
+  if (u >= ldc(ut.q, p.B)) return;
   const int rk = find_seq(ut.q, p.B, u);  // table entry: sequences by key count, largest first
-  const int b = ut.perm[rk];
+  const int b = ldc(ut.perm, rk);
   const SeqInfo si = seq_info(p, b);
-  const int qpos0 = (u - ut.q[rk]) * C::R;
+  const int qpos0 = (u - ldc(ut.q, rk)) * C::R;
   if (qpos0 >= si.len) return;
   const int tid = threadIdx.x, row = tid / C::TPR, d0 = (tid % C::TPR) * C::DPT;
   const int pos = qpos0 + row;

@@ -37,8 +37,15 @@ inline int elem_size(int dtype) {
   }
 }
 
+// Element i of a metadata array (sequence offsets, context indices, unit tables) that no
+// kernel writes while it reads it.  The read goes through the constant address space, so a
+// wave-uniform index becomes a scalar load: it waits on the scalar counter, not on the
+// vector-memory counter, and so never waits for the direct tile loads in flight.
+typedef const __attribute__((address_space(4))) int32_t cint32_t;
+FMLM_DEV int ldc(const int32_t* a, int i) { return ((cint32_t*)(uintptr_t)a)[i]; }
+
 // Start of sequence b in packed token space.
-FMLM_DEV int seq_start(const int32_t* cu, int b, int N) { return cu ? cu[b] : b * N; }
+FMLM_DEV int seq_start(const int32_t* cu, int b, int N) { return cu ? ldc(cu, b) : b * N; }
 
 // Index of the sequence whose packed token range [cu[s], cu[s+1]) holds token j
 // (cu non-decreasing, 0 <= j < cu[B]).  Empty sequences are skipped because
@@ -47,7 +54,7 @@ FMLM_DEV int find_seq(const int32_t* cu, int B, int j) {
   int lo = 0, hi = B - 1;
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
-    if (cu[mid] <= j)
+    if (ldc(cu, mid) <= j)
       lo = mid;
     else
       hi = mid - 1;
@@ -64,7 +71,7 @@ struct SeqInfo {
 // context batch of sequence b: ctx_index[b] (clamped) when given, else b for a
 // full-batch context and 0 for a shared one
 FMLM_DEV int ctx_batch_of(const fmlm_attn_params& p, int b) {
-  if (p.ctx_index) return min(max(p.ctx_index[b], 0), max(p.ctx_batch - 1, 0));
+  if (p.ctx_index) return min(max(ldc(p.ctx_index, b), 0), max(p.ctx_batch - 1, 0));
   return p.ctx_batch > 1 ? b : 0;
 }
 
@@ -74,10 +81,10 @@ FMLM_DEV void ctx_range(const fmlm_attn_params& p, int cb, int& c0, int& c1) {
   c1 = p.ctx_len;
   if (p.cu_seqlens_kv) {
     if (p.ctx_block_table) {
-      c1 = p.cu_seqlens_kv[cb + 1] - p.cu_seqlens_kv[cb];
+      c1 = ldc(p.cu_seqlens_kv, cb + 1) - ldc(p.cu_seqlens_kv, cb);
     } else {
-      c0 = min(max(p.cu_seqlens_kv[cb], 0), p.ctx_rows);
-      c1 = min(max(p.cu_seqlens_kv[cb + 1], c0), p.ctx_rows);
+      c0 = min(max(ldc(p.cu_seqlens_kv, cb), 0), p.ctx_rows);
+      c1 = min(max(ldc(p.cu_seqlens_kv, cb + 1), c0), p.ctx_rows);
     }
   }
   if (p.ctx_block_table) c1 = min(max(c1, 0), p.ctx_pages_per_batch * FMLM_PAGE_ROWS);
@@ -89,7 +96,7 @@ FMLM_DEV SeqInfo seq_info(const fmlm_attn_params& p, int b) {
   s.q0 = seq_start(cu, b, p.N);
   int L = p.N;
   if (cu) {
-    L = cu[b + 1] - s.q0;
+    L = ldc(cu, b + 1) - s.q0;
     if (p.N > 0) L = min(L, p.N);
     L = max(min(L, p.total_q - s.q0), 0);
   }
