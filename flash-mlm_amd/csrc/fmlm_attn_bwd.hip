@@ -452,8 +452,10 @@ struct QuerySteps {
     }
     return QStep{hq_hi, k->b_lo, 0};
   }
-  FMLM_DEV QStep next(const QStep& st) const {
-    if (st.p0 + qs < seq_info(*p, st.b).len) return QStep{st.hq, st.b, st.p0 + qs};
+  FMLM_DEV QStep next(const QStep& st) const { return next(st, seq_info(*p, st.b).len); }
+  // the same, given the length of st's sequence
+  FMLM_DEV QStep next(const QStep& st, int len) const {
+    if (st.p0 + qs < len) return QStep{st.hq, st.b, st.p0 + qs};
     return first_from(st.hq, st.b + 1);
   }
 };
@@ -957,8 +959,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     dma_offsets<D, C::QS>(__builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), lane, wave, o_off);
   }
   float lreg = INFINITY, dlreg = 0.f;
-  auto prep = [&](const QStep& st, int buf) {
-    const SeqInfo si = seq_info(p, st.b);
+  // si: the ranges of st's sequence
+  auto prep = [&](const QStep& st, const SeqInfo& si, int buf) {
     if (tid < C::QS) {
       const int pos = st.p0 + tid;
       const bool ok = pos < si.len;
@@ -1014,16 +1016,21 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   };
   const TileReader<T, D> tr(l16, gq);
 
+  // the ranges of the current and the next step's sequences are read once per sequence:
+  // consecutive steps of one sequence reuse them
   QStep cur = steps.first_from(hq_lo, ku.b_lo);
+  SeqInfo si_cur{};
+  if (cur.hq < hq_hi) si_cur = seq_info(p, cur.b);
   int buf = 0;
   if constexpr (!C::PAD)
-    if (cur.hq < hq_hi) prep(cur, 0);
+    if (cur.hq < hq_hi) prep(cur, si_cur, 0);
   while (cur.hq < hq_hi) {
-    const QStep nxt = steps.next(cur);
-    const int lim = ku.causal_main ? seq_info(p, cur.b).mainlen : 0x7fffffff;
+    const QStep nxt = steps.next(cur, si_cur.len);
+    const SeqInfo si_nxt = (nxt.hq < hq_hi && nxt.b != cur.b) ? seq_info(p, nxt.b) : si_cur;
+    const int lim = ku.causal_main ? si_cur.mainlen : 0x7fffffff;
     if constexpr (C::PAD) {
       __syncthreads();  // the previous step's LDS reads are done
-      prep(cur, 0);
+      prep(cur, si_cur, 0);
     } else if (tid < C::QS) {  // this buffer's statistics were last read two steps ago
       lse_s(buf)[tid] = lreg;
       dl_s(buf)[tid] = dlreg;
@@ -1032,7 +1039,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     __syncthreads();                // ... and every other wave's
     // the other buffer was last read by the previous step, which every wave has finished
     if constexpr (!C::PAD)
-      if (nxt.hq < hq_hi) prep(nxt, buf ^ 1);
+      if (nxt.hq < hq_hi) prep(nxt, si_nxt, buf ^ 1);
     const char* const qt = qbuf(buf);
     const char* const ot = obuf(buf);
     const float* const ls = lse_s(buf);
@@ -1202,6 +1209,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     }
     if constexpr (!C::PAD) buf ^= 1;
     cur = nxt;
+    si_cur = si_nxt;
   }
 
   if constexpr (PIPE) {  // the pipelined steps keep dO^T P apart; with V = K it is part of dK
