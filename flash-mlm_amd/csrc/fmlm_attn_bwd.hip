@@ -243,8 +243,8 @@ template <int D, int NR>
 FMLM_DEV void dma_rows(const char* src, uint32_t rowb, int last, uint32_t lds, int wave, int lane) {
   typedef BwdCfg<D> C;
   static_assert(!C::PAD && NR % (C::RPI * kBwdNW) == 0, "whole wave-wide loads per wave");
-  // the lane's offsets are recomputed per call (the dq kernel has no registers to hold
-  // them; the pipelined dK / dV step precomputes a whole step's, see dma_rows_at)
+  // the lane's offsets are recomputed per call: partial tiles and steps, and row pitches
+  // other than the one the pipelined kernels precompute offsets for (see dma_rows_at)
   int ln = lane;
   asm volatile("" : "+v"(ln));
   const int row0 = wave * C::RPI + ln / C::CPR;
@@ -535,6 +535,12 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   };
   auto kbuf = [&](int buf) { return smem_raw + buf * C::TILEB; };
   auto vbuf = [&](int buf) { return smem_raw + (C::DQ_NBUF + buf) * C::TILEB; };
+  // the lane's direct-load offsets of a whole tile at the main segment's K row pitch (the
+  // common case: every full tile whose K and V rows have that pitch)
+  constexpr int NPT = PIPE ? kBwdBK / (C::RPI * kBwdNW) : 1;
+  uint32_t t_off[NPT];
+  const uint32_t t_rowb = __builtin_amdgcn_readfirstlane((uint32_t)sm.ksn * 2u);
+  if constexpr (PIPE) dma_offsets<D, kBwdBK>(t_rowb, lane, wave, t_off);
   auto issue = [&](int t, int buf) {
     const bool m = t >= nt0;
     const int j0 = (m ? t - nt0 : t) * kBwdBK;
@@ -576,6 +582,13 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
       const char* const vp = uniform_ptr((m ? sm.v : sc.v) + vt * 2);
       const uint32_t krowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.ksn : sc.ksn) * 2u);
       const uint32_t vrowb = __builtin_amdgcn_readfirstlane((uint32_t)(m ? sm.vsn : sc.vsn) * 2u);
+      if constexpr (PIPE) {
+        if (last == kBwdBK - 1 && krowb == t_rowb && (kv_same || vrowb == t_rowb)) {
+          dma_rows_at<D, kBwdBK>(kp, t_off, lds_addr(kbuf(buf)), wave);
+          if (!kv_same) dma_rows_at<D, kBwdBK>(vp, t_off, lds_addr(vbuf(buf)), wave);
+          return;
+        }
+      }
       dma_rows<D, kBwdBK>(kp, krowb, last, lds_addr(kbuf(buf)), wave, lane);
       if (!kv_same) dma_rows<D, kBwdBK>(vp, vrowb, last, lds_addr(vbuf(buf)), wave, lane);
     }
