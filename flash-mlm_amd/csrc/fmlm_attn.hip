@@ -70,6 +70,8 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
                                                                  int groups_off, int records_off,
                                                                  int rec_bytes, int hpack) {
   __shared__ int s_tiles[kSortMax];
+  __shared__ int s_kt[kSortMax];            // key tiles per query tile
+  __shared__ long long s_pre[kSortMax + 1];  // head-packed: work before each rank
   __shared__ float s_work[kSortMax];
   __shared__ int s_order[kSortMax];
   __shared__ unsigned char s_split[kSortMax];
@@ -80,8 +82,12 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
   const int B = p.B, H = p.H;
   const bool sorted = B <= kSortMax;
   // head-packed tiles (hpack, MLA): a tile is BQ consecutive rows of the H*L (head,
-  // position) rows of a sequence, since every head reads the same latent.  Sequence b's
-  // tiles t = j + kXcds*i form group (b, j), so group j of every sequence lands on XCD j.
+  // position) rows of a sequence, since every head reads the same latent.  The latent of a
+  // sequence is larger than an XCD's L2, so a sequence's tiles go to as few XCDs as
+  // possible: the sequences in rank order are laid end to end by work (tiles x key tiles),
+  // the total is cut into kXcds equal parts, and each tile goes to the XCD whose part
+  // holds its midpoint (a sequence spans one XCD, or two or three at the cuts).  Unsorted
+  // batches deal tile t of every sequence to XCD t % kXcds.
   const int HG = hpack ? kXcds : H;  // groups per sequence
   auto seq_tiles = [&](int len) { return ((hpack ? H : 1) * len + BQ - 1) / BQ; };
   auto group_tiles = [&](int tiles, int j) { return hpack ? max(0, (tiles - j + kXcds - 1) / kXcds) : tiles; };
@@ -100,6 +106,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
       const int ktiles = (si.ctx + kSplitBK - 1) / kSplitBK + (si.mainlen + kSplitBK - 1) / kSplitBK;
       const float units = (float)tiles * (hpack ? 1 : H);
       s_tiles[b] = tiles;
+      s_kt[b] = ktiles;
       s_work[b] = (float)ktiles;
       atomicAdd(&s_sum[0], units);
       atomicAdd(&s_sum[1], units * ktiles);
@@ -140,6 +147,16 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
       s_order[rank] = b;
     }
     __syncthreads();
+    if (hpack && tid == 0) {  // work before each rank (a tile with no keys counts as one)
+      long long acc = 0;
+      for (int r = 0; r < B; ++r) {
+        s_pre[r] = acc;
+        const int b = s_order[r];
+        acc += (long long)s_tiles[b] * max(s_kt[b], 1);
+      }
+      s_pre[B] = acc;
+    }
+    __syncthreads();
   }
   const int x = tid >> 6, lane = tid & 63;
   const int G = B * HG;
@@ -152,15 +169,28 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
   // XCDs or one more (at most two from 8 heads up).  (Head-packed tiles, and unsorted
   // batches, go round-robin: group g to XCD g % 8.)
   const bool by_head = sorted && !hpack;
+  const bool by_seq = sorted && hpack;
+  // by_seq: the first tile of rank r whose work midpoint lies at or past the start of
+  // XCD x's part, i.e. 8 P_r + (8 i + 4) k >= x W
+  auto first_tile = [&](int r, int xx) {
+    const long long W = s_pre[B], k = max(s_kt[s_order[r]], 1);
+    const long long num = (long long)xx * W - 8 * s_pre[r] - 4 * k;
+    const long long i = num <= 0 ? 0 : (num + 8 * k - 1) / (8 * k);
+    return (int)min(i, (long long)s_tiles[s_order[r]]);
+  };
   const int K = kXcds / min(H & -H, kXcds);
   const int PX = H * K / kXcds;
   const int nrank = (B + K - 1) / K;
   int carry = 0;
-  for (int i0 = 0; by_head ? i0 < PX * nrank : x + kXcds * i0 < G; i0 += 64) {
+  for (int i0 = 0; by_head ? i0 < PX * nrank : by_seq ? i0 < B : x + kXcds * i0 < G; i0 += 64) {
     bool valid;
     int r = 0;
     int b = 0, h = 0, tiles = 0, S = 1;
-    if (by_head) {  // this XCD's group i: part q = x PX + i / nrank, its (i % nrank)-th rank
+    int t0 = 0, tstep = kXcds;  // head-packed: the j-th tile of the group is t0 + tstep * j
+    if (by_seq) {  // rank r's tiles in XCD x's part
+      r = i0 + lane;
+      valid = r < B;
+    } else if (by_head) {  // this XCD's group i: part q = x PX + i / nrank, its (i % nrank)-th rank
       const int i = i0 + lane;
       const int q = x * PX + i / nrank, j = i % nrank, pq = q % K;
       h = q / K;
@@ -174,7 +204,14 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
     }
     if (valid) {
       b = sorted ? s_order[r] : r;
-      tiles = group_tiles(sorted ? s_tiles[b] : seq_tiles(seq_info(p, b).len), h);
+      if (by_seq) {
+        t0 = first_tile(r, x);
+        tstep = 1;
+        tiles = first_tile(r, x + 1) - t0;
+      } else {
+        t0 = h;
+        tiles = group_tiles(sorted ? s_tiles[b] : seq_tiles(seq_info(p, b).len), h);
+      }
       S = sorted ? s_split[b] : 1;
     }
     const int n = tiles * S;
@@ -188,7 +225,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
     const int pos = carry + incl - n;
     int gid0 = 0, rec0 = 0;
     // (h, tile) field of the unit: head-packed tiles carry no head
-    auto hf = [&](int j) { return hpack ? ((h + kXcds * j) << 16) : (h | (j << 16)); };
+    auto hf = [&](int j) { return hpack ? ((t0 + tstep * j) << 16) : (h | (j << 16)); };
     if (S > 1) {
       gid0 = atomicAdd(&s_groups, tiles);
       rec0 = atomicAdd(&s_recs, tiles * S);
@@ -1950,15 +1987,16 @@ static SplitCfg split_cfg(const fmlm_attn_params& p, const Launch& L) {
 // Grid size (1-D): dense units are laid out arithmetically, packed units by the
 // schedule, whose XCD slots are bounded by ceil(total/8) + the largest group (with
 // splits: at most kSplitRounds*slots unsplit units plus rec_cap split parts, a group
-// growing by up to kMaxSplits).
+// growing by up to kMaxSplits).  Head-packed units are dealt to XCDs by work, not by
+// count, so one XCD may hold every unit and every split part.
 static int64_t grid_units(const fmlm_attn_params& p, int bq, const SplitCfg& sc, bool hpack = false) {
   if (!p.cu_seqlens_q) {
     const int64_t groups = (int64_t)p.B * p.H;
     return kXcds * ((groups + kXcds - 1) / kXcds) * ((p.N + bq - 1) / bq);
   }
-  if (hpack) {  // sum over b of ceil(H*L_b/bq) units; each XCD list pads by < 1 per sequence
-    const int64_t units = ((int64_t)p.H * p.total_q + bq - 1) / bq + p.B;
-    return kXcds * ((units + kXcds - 1) / kXcds + p.B + 1);
+  if (hpack) {  // sum over b of ceil(H*L_b/bq) units, and the split parts
+    const int64_t units = ((int64_t)p.H * p.total_q + bq - 1) / bq + p.B + sc.rec_cap;
+    return kXcds * (units + 1);
   }
   const int64_t total = (int64_t)p.H * (p.B + p.total_q / bq + 1);
   const int64_t max_group = (p.N > 0 ? (p.N + bq - 1) / bq : p.total_q / bq + 1) + 1;

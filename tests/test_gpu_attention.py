@@ -518,6 +518,54 @@ def test_schedule_places_every_tile_once(H, lengths, causal, device):
         assert len(xcds) <= (8 + H - 1) // H + 1, (h, xcds)
 
 
+@pytest.mark.parametrize("lengths,ctx_lengths", [
+    ([300, 64, 1, 511, 200, 0, 77, 400], [700, 0, 5, 1300, 64, 10, 300, 900]),
+    ([130, 1, 64, 97, 200], [70, 0, 5, 129, 64]),
+    ([900, 1000, 1100, 1200], [4000, 4000, 4000, 4000]),
+])
+def test_mla_schedule_keeps_sequences_together(lengths, ctx_lengths, device):
+    """Head-packed tiles (the 512-wide latent, 128 of a sequence's H*L (head, row) rows per
+    tile): every (sequence, tile) once, in all its split parts; a sequence's tiles sit on as
+    few XCDs (slot % 8) as its share of the work needs, plus one at each cut; and the XCDs'
+    work (query tiles x key tiles) differs from an equal share by at most one tile's."""
+    torch.manual_seed(7300 + len(lengths))
+    B, H, N, D = len(lengths), 16, max(lengths), 512
+    dtype = torch.bfloat16
+    q = _randn((B, H, N, D), device, dtype, std=0.5)
+    k = _randn((B, H, N, D), device, dtype, std=0.5)
+    cache, kc, _, cu_kv, Tc = _context_cache(B, H, D, True, ctx_lengths, device, dtype, std=0.5)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    scale = 1.0 / math.sqrt(D)
+    out = flash_attn_mlm_compressed(q, k, k, H, meta, scale, cache, 0, is_mla=True, block_n=64)
+    ref = _packed_oracle(q, k, k, lengths, scale, is_mla=True, k_cache=kc, cu_kv=cu_kv, cbs=B, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+    (sched,) = meta.kernel_schedules.values()
+    units = _schedule_units(sched)
+    seen = {}
+    for slot, b, _, tile, s, S in units:
+        assert ((b, tile), s) not in seen, (b, tile, s)
+        seen[((b, tile), s)] = (S, slot % 8)
+    tiles = [(H * L + 127) // 128 for L in lengths]
+    want = {(b, t) for b in range(B) for t in range(tiles[b])}
+    assert {key for key, _ in seen} == want
+    for key in want:
+        S = {seen[(k_, s)][0] for (k_, s) in seen if k_ == key}
+        assert len(S) == 1
+        (S,) = S
+        assert {s for (k_, s) in seen if k_ == key} == set(range(S))
+    kt = [max((c + 63) // 64 + (L + 63) // 64, 1) for c, L in zip(ctx_lengths, lengths)]
+    work = [t * w for t, w in zip(tiles, kt)]
+    W = sum(work)
+    per_xcd = [0] * 8
+    for ((b, _), s), (_, x) in seen.items():
+        if s == 0:
+            per_xcd[x] += kt[b]
+    for b in range(B):
+        xcds = {x for ((bb, _), _), (_, x) in seen.items() if bb == b}
+        assert len(xcds) <= (8 * work[b]) // W + 2, (b, xcds)
+    assert max(abs(w - W / 8) for w in per_xcd) <= max(kt), per_xcd
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [16, 64, 128, 256])
 @pytest.mark.parametrize("is_mla", [False, True])
