@@ -1027,19 +1027,70 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       dma_rows<D, C::QS>(ds, __builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), last, lds_addr(obuf(buf)), wave, lane);
     }
   };
+  // Pipelined kernels: a step's row 0 in Q, dO and the row statistics, derived once per
+  // (head, sequence) and then advanced by one step per step; prep_rows() is prep() with
+  // them (the other kernels compute them per step: they have no scalar registers to spare)
+  struct StepRows {
+    const char* q;
+    const char* d;
+    int64_t at;  // index of the row statistics
+  };
+  auto step_rows = [&](const QStep& st, const SeqInfo& si) {
+    StepRows r;
+    r.q = uniform_ptr((const char*)p.q + row_at(p.q_layout, st.b, st.hq, si.q0, st.p0, p.q_sb, p.q_sh, p.q_sn) * 2);
+    r.d = uniform_ptr((const char*)g.dout + row_at(p.o_layout, st.b, st.hq, si.q0, st.p0, g.do_sb, g.do_sh, g.do_sn) * 2);
+    r.at = (int64_t)st.hq * p.total_q + si.q0 + st.p0;
+    return r;
+  };
+  auto next_rows = [&](const StepRows& r) {
+    return StepRows{uniform_ptr(r.q + (int64_t)C::QS * p.q_sn * 2), uniform_ptr(r.d + (int64_t)C::QS * g.do_sn * 2),
+                    r.at + C::QS};
+  };
+  auto prep_rows = [&](const QStep& st, const SeqInfo& si, const StepRows& rows, int buf) {
+    if constexpr (PIPE) {
+      if (tid < C::QS) {
+        const bool ok = st.p0 + tid < si.len;
+        lreg = ok ? st_lse[rows.at + tid] : INFINITY;  // padding rows: P = 0
+        dlreg = ok ? st_delta[rows.at + tid] : 0.f;
+      }
+      const int last = min(C::QS, si.len - st.p0) - 1;
+      if (last == C::QS - 1) {  // a whole step: the precomputed offsets
+        dma_rows_at<D, C::QS>(rows.q, q_off, lds_addr(qbuf(buf)), wave);
+        dma_rows_at<D, C::QS>(rows.d, o_off, lds_addr(obuf(buf)), wave);
+        return;
+      }
+      dma_rows<D, C::QS>(rows.q, __builtin_amdgcn_readfirstlane((uint32_t)p.q_sn * 2u), last, lds_addr(qbuf(buf)), wave, lane);
+      dma_rows<D, C::QS>(rows.d, __builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), last, lds_addr(obuf(buf)), wave, lane);
+    }
+  };
+
   const TileReader<T, D> tr(l16, gq);
 
   // the ranges of the current and the next step's sequences are read once per sequence:
   // consecutive steps of one sequence reuse them
   QStep cur = steps.first_from(hq_lo, ku.b_lo);
   SeqInfo si_cur{};
+  StepRows rows_cur{};
   if (cur.hq < hq_hi) si_cur = seq_info(p, cur.b);
   int buf = 0;
-  if constexpr (!C::PAD)
+  if constexpr (PIPE) {
+    if (cur.hq < hq_hi) {
+      rows_cur = step_rows(cur, si_cur);
+      prep_rows(cur, si_cur, rows_cur, 0);
+    }
+  } else if constexpr (!C::PAD) {
     if (cur.hq < hq_hi) prep(cur, si_cur, 0);
+  }
   while (cur.hq < hq_hi) {
     const QStep nxt = steps.next(cur, si_cur.len);
     const SeqInfo si_nxt = (nxt.hq < hq_hi && nxt.b != cur.b) ? seq_info(p, nxt.b) : si_cur;
+    StepRows rows_nxt{};
+    if constexpr (PIPE) {
+      if (nxt.b == cur.b && nxt.hq == cur.hq)
+        rows_nxt = next_rows(rows_cur);
+      else if (nxt.hq < hq_hi)
+        rows_nxt = step_rows(nxt, si_nxt);
+    }
     const int lim = ku.causal_main ? si_cur.mainlen : 0x7fffffff;
     if constexpr (C::PAD) {
       __syncthreads();  // the previous step's LDS reads are done
@@ -1051,8 +1102,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the step have landed
     __syncthreads();                // ... and every other wave's
     // the other buffer was last read by the previous step, which every wave has finished
-    if constexpr (!C::PAD)
+    if constexpr (PIPE) {
+      if (nxt.hq < hq_hi) prep_rows(nxt, si_nxt, rows_nxt, buf ^ 1);
+    } else if constexpr (!C::PAD) {
       if (nxt.hq < hq_hi) prep(nxt, si_nxt, buf ^ 1);
+    }
     const char* const qt = qbuf(buf);
     const char* const ot = obuf(buf);
     const float* const ls = lse_s(buf);
@@ -1223,6 +1277,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     if constexpr (!C::PAD) buf ^= 1;
     cur = nxt;
     si_cur = si_nxt;
+    if constexpr (PIPE) rows_cur = rows_nxt;
   }
 
   if constexpr (PIPE) {  // the pipelined steps keep dO^T P apart; with V = K it is part of dK
