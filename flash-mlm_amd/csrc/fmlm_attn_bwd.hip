@@ -55,9 +55,11 @@ struct BwdCfg {
   static constexpr int NPW = kBwdBK / RPI / kBwdNW;  // wave-wide loads per tile and tensor
   static constexpr int NKB = kBwdBK / 16;
   static constexpr int NKS = kBwdBK / 32;
-  // dkv kernel: 16-key blocks per wave (at D = 128 two blocks spill, which measured
-  // slower than one)
-  static constexpr int KB = (D <= 64 || D >= 512) ? 2 : 1;
+  // dkv kernel: 16-key blocks per wave.  Two at the 512-wide latent (one wave per SIMD);
+  // one elsewhere: at D = 128 two spill, and at D <= 64 one block per wave halves the
+  // work per unit (a shared context's units walk every query of the batch, so smaller
+  // units balance the grid) and lets three waves share a SIMD
+  static constexpr int KB = D >= 512 ? 2 : 1;
   static constexpr int DKV_KEYS = kBwdNW * 16 * KB;  // keys per dkv workgroup
   static constexpr int QS = D >= 256 ? 32 : 64;   // query rows per dkv step (32-row groups)
   // dK/dV kernel: a query step's Q and dO rows (tiles like the dq kernel's) and its lse
