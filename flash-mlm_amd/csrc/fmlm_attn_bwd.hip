@@ -41,7 +41,11 @@ struct BwdCfg {
   static constexpr int KC = D / 32;               // 32-wide contraction steps over D
   static constexpr int NDB = D / 16;              // 16-wide column blocks
   static constexpr int C8 = D / 8;                // 16-byte chunks per row
-  static constexpr int QB = D >= 256 ? 1 : 2;     // 16-row query blocks per wave (dq kernel)
+  // 16-row query blocks per wave (dq kernel): two at D = 128 (each K / V fragment then
+  // feeds two MFMAs); one at D >= 256 (registers) and at D <= 64, where twice the
+  // workgroups balance the grid (a batch with few query tiles per slot otherwise runs a
+  // nearly empty second round) and four waves fit on a SIMD
+  static constexpr int QB = D == 128 ? 2 : 1;
   static constexpr int BQ = kBwdNW * QB * 16;     // query rows per dq workgroup
   // dq kernel key tiles: unpadded rows whose 16-byte chunks are swizzled by kv_swz,
   // filled by direct global->LDS loads of RPI rows per wave-wide load.  The 512-wide
