@@ -66,10 +66,10 @@ struct BwdCfg {
   static constexpr int KB = D >= 512 ? 2 : 1;
   static constexpr int DKV_KEYS = kBwdNW * 16 * KB;  // keys per dkv workgroup
   static constexpr int QS = D >= 256 ? 32 : 64;   // query rows per dkv step (32-row groups)
-  // dK/dV kernel: a query step's Q and dO rows (tiles like the dq kernel's) and its lse
-  // and delta, in two buffers (the next step loads during the current one's math), one
-  // register-staged buffer for the latent
-  static constexpr int DKV_NBUF = PAD ? 1 : 2;
+  // dK/dV kernel: a query step's Q and dO rows (tiles like the dq kernel's; padded rows
+  // for the latent) and its lse and delta, in two buffers (the next step loads during
+  // the current one's math)
+  static constexpr int DKV_NBUF = 2;
   static constexpr int STEPB = QS * ROWB;
   static constexpr int DKV_SB = 2 * STEPB + 2 * QS * 4;  // bytes per step buffer
   static constexpr int DKV_LDS = DKV_NBUF * DKV_SB;
@@ -281,6 +281,22 @@ FMLM_DEV void dma_offsets(uint32_t rowb, int lane, int wave, uint32_t (&off)[NR 
   for (int j = 0; j < NR / (C::RPI * kBwdNW); ++j) {
     const int row = row0 + j * kBwdNW * C::RPI;
     off[j] = (uint32_t)row * rowb + 16u * (uint32_t)((lane % C::CPR) ^ kv_swz<D>(row));
+  }
+}
+
+// Direct global->LDS loads of NR padded rows (the 512-wide latent: one row is one
+// wave-wide 16-byte load): row r from the wave-uniform row-0 address src at pitch rowb
+// bytes (rows past `last` repeat row `last`) to LDS byte address lds + r * ROWB, row r by
+// wave r % kBwdNW.  Nothing waits here.
+template <int D, int NR>
+FMLM_DEV void dma_rows_padded(const char* src, uint32_t rowb, int last, uint32_t lds, int wave, int lane) {
+  typedef BwdCfg<D> C;
+  static_assert(C::PAD && C::CPR == 64 && NR % kBwdNW == 0, "one wave-wide load per padded row");
+#pragma unroll
+  for (int j = 0; j < NR / kBwdNW; ++j) {
+    const int row = __builtin_amdgcn_readfirstlane(wave + j * kBwdNW);
+    const uint32_t r = (uint32_t)min(row, last);
+    dma16_sbase(uniform_ptr(src + (size_t)r * rowb), 16u * (uint32_t)lane, __builtin_amdgcn_readfirstlane(lds + row * C::ROWB));
   }
 }
 
@@ -987,35 +1003,15 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       lreg = ok ? st_lse[at] : INFINITY;  // padding rows: P = 0
       dlreg = ok ? st_delta[at] : 0.f;
     }
-    if constexpr (C::PAD) {
-      constexpr int QCH = C::QS * C::C8;             // 16-byte chunks per step and tensor
-      constexpr int QPT = (QCH + C::NT - 1) / C::NT;  // ... per thread
-      u32x4 qreg[QPT], dreg[QPT];
-#pragma unroll
-      for (int li = 0; li < QPT; ++li) {
-        const int it = tid + li * C::NT;
-        const int r = it / C::C8, c8 = it % C::C8;
-        const int pos = st.p0 + r;
-        qreg[li] = u32x4{0u, 0u, 0u, 0u};
-        dreg[li] = qreg[li];
-        if ((QCH % C::NT == 0 || it < QCH) && pos < si.len) {
-          qreg[li] = ld16((const char*)p.q, row_at(p.q_layout, st.b, st.hq, si.q0, pos, p.q_sb, p.q_sh, p.q_sn) + c8 * 8);
-          dreg[li] = ld16((const char*)g.dout,
-                          row_at(p.o_layout, st.b, st.hq, si.q0, pos, g.do_sb, g.do_sh, g.do_sn) + c8 * 8);
-        }
-      }
-#pragma unroll
-      for (int li = 0; li < QPT; ++li) {
-        const int it = tid + li * C::NT;
-        if (QCH % C::NT != 0 && it >= QCH) continue;
-        const int at = (it / C::C8) * C::ROWB + (it % C::C8) * 16;
-        *(u32x4*)(qbuf(buf) + at) = qreg[li];
-        *(u32x4*)(obuf(buf) + at) = dreg[li];
-      }
-      if (tid < C::QS) {
-        lse_s(buf)[tid] = lreg;
-        dl_s(buf)[tid] = dlreg;
-      }
+    if constexpr (C::PAD) {  // padded rows, one direct load per row
+      const int last = min(C::QS, si.len - st.p0) - 1;
+      const int64_t qe = row_at(p.q_layout, st.b, st.hq, si.q0, st.p0, p.q_sb, p.q_sh, p.q_sn);
+      const int64_t de = row_at(p.o_layout, st.b, st.hq, si.q0, st.p0, g.do_sb, g.do_sh, g.do_sn);
+      dma_rows_padded<D, C::QS>(uniform_ptr((const char*)p.q + qe * 2), __builtin_amdgcn_readfirstlane((uint32_t)p.q_sn * 2u),
+                                last, lds_addr(qbuf(buf)), wave, lane);
+      dma_rows_padded<D, C::QS>(uniform_ptr((const char*)g.dout + de * 2),
+                                __builtin_amdgcn_readfirstlane((uint32_t)g.do_sn * 2u), last, lds_addr(obuf(buf)), wave,
+                                lane);
     } else {
       const int last = min(C::QS, si.len - st.p0) - 1;
       const int64_t qe = row_at(p.q_layout, st.b, st.hq, si.q0, st.p0, p.q_sb, p.q_sh, p.q_sn);
@@ -1084,7 +1080,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       rows_cur = step_rows(cur, si_cur);
       prep_rows(cur, si_cur, rows_cur, 0);
     }
-  } else if constexpr (!C::PAD) {
+  } else {
     if (cur.hq < hq_hi) prep(cur, si_cur, 0);
   }
   while (cur.hq < hq_hi) {
@@ -1098,10 +1094,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
         rows_nxt = step_rows(nxt, si_nxt);
     }
     const int lim = ku.causal_main ? si_cur.mainlen : 0x7fffffff;
-    if constexpr (C::PAD) {
-      __syncthreads();  // the previous step's LDS reads are done
-      prep(cur, si_cur, 0);
-    } else if (tid < C::QS) {  // this buffer's statistics were last read two steps ago
+    if (tid < C::QS) {  // this buffer's statistics were last read two steps ago
       lse_s(buf)[tid] = lreg;
       dl_s(buf)[tid] = dlreg;
     }
@@ -1110,7 +1103,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     // the other buffer was last read by the previous step, which every wave has finished
     if constexpr (PIPE) {
       if (nxt.hq < hq_hi) prep_rows(nxt, si_nxt, rows_nxt, buf ^ 1);
-    } else if constexpr (!C::PAD) {
+    } else {
       if (nxt.hq < hq_hi) prep(nxt, si_nxt, buf ^ 1);
     }
     const char* const qt = qbuf(buf);
@@ -1280,7 +1273,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
     }
     }
     }
-    if constexpr (!C::PAD) buf ^= 1;
+    buf ^= 1;
     cur = nxt;
     si_cur = si_nxt;
     if constexpr (PIPE) rows_cur = rows_nxt;
