@@ -78,9 +78,9 @@ struct BwdCfg {
   static constexpr int WPS = D >= 512 ? 1 : 2;
   static constexpr bool MLA_ONLY = D >= 512;  // the 512-wide head dim exists for the MLA latent only
   // dq kernel: two buffers per tensor (the next tile loads during the current one's
-  // math) where they fit beside the other workgroups of a CU, one at D >= 256; the
-  // latent needs no V tile (V = K)
-  static constexpr int DQ_NBUF = D <= 128 ? 2 : 1;
+  // math) where they fit beside the other workgroups of a CU: one at D = 256, two at
+  // D <= 128 and for the latent (one workgroup per CU, no V tile since V = K)
+  static constexpr int DQ_NBUF = (D <= 128 || PAD) ? 2 : 1;
   static constexpr int DQ_LDS = DQ_NBUF * (MLA_ONLY ? 1 : 2) * TILEB;
   static_assert(D % 32 == 0 && D >= 32 && D <= 512, "head dim");
 };
@@ -566,32 +566,19 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   auto issue = [&](int t, int buf) {
     const bool m = t >= nt0;
     const int j0 = (m ? t - nt0 : t) * kBwdBK;
-    if constexpr (C::PAD) {  // register-staged; single buffer, so nothing reads it meanwhile
-      constexpr int LPT = kBwdBK * C::CPR / C::NT;  // 16-byte chunks per thread and tensor
+    if constexpr (C::PAD) {  // padded rows, one direct load per row
       const int n = m ? sm.n : sc.n;
       const char* const kp = m ? sm.k : sc.k;
       const char* const vp = m ? sm.v : sc.v;
       const int64_t ksn = m ? sm.ksn : sc.ksn, vsn = m ? sm.vsn : sc.vsn;
       const int64_t kt = m ? sm.kbase + (int64_t)j0 * ksn : key_elem(sc, sc.kbase, ksn, j0);
-      const int64_t vt = m ? sm.vbase + (int64_t)j0 * vsn : key_elem(sc, sc.vbase, vsn, j0);
-      u32x4 kreg[LPT], vreg[LPT];
-#pragma unroll
-      for (int li = 0; li < LPT; ++li) {  // rows past the segment end are 0
-        const int it = tid + li * C::NT;
-        const int row = it / C::CPR, c8 = it % C::CPR;
-        kreg[li] = u32x4{0u, 0u, 0u, 0u};
-        vreg[li] = kreg[li];
-        if (j0 + row < n) {
-          kreg[li] = ld16(kp, kt + (int64_t)row * ksn + c8 * 8);
-          if (!kv_same) vreg[li] = ld16(vp, vt + (int64_t)row * vsn + c8 * 8);
-        }
-      }
-#pragma unroll
-      for (int li = 0; li < LPT; ++li) {
-        const int it = tid + li * C::NT;
-        const int at = (it / C::CPR) * C::ROWB + (it % C::CPR) * 16;
-        *(u32x4*)(kbuf(buf) + at) = kreg[li];
-        if (!kv_same) *(u32x4*)(vbuf(buf) + at) = vreg[li];
+      const int last = min(kBwdBK, n - j0) - 1;  // rows past the segment end repeat it
+      dma_rows_padded<D, kBwdBK>(uniform_ptr(kp + kt * 2), __builtin_amdgcn_readfirstlane((uint32_t)ksn * 2u), last,
+                                 lds_addr(kbuf(buf)), wave, lane);
+      if (!kv_same) {
+        const int64_t vt = m ? sm.vbase + (int64_t)j0 * vsn : key_elem(sc, sc.vbase, vsn, j0);
+        dma_rows_padded<D, kBwdBK>(uniform_ptr(vp + vt * 2), __builtin_amdgcn_readfirstlane((uint32_t)vsn * 2u), last,
+                                   lds_addr(vbuf(buf)), wave, lane);
       }
     } else {
       // (segment fields picked one by one: a reference to either would put both in memory)
