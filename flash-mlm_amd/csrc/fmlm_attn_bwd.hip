@@ -49,8 +49,8 @@ struct BwdCfg {
   static constexpr int BQ = kBwdNW * QB * 16;     // query rows per dq workgroup
   // dq kernel key tiles: unpadded rows whose 16-byte chunks are swizzled by kv_swz,
   // filled by direct global->LDS loads of RPI rows per wave-wide load.  The 512-wide
-  // latent (PAD) instead stages its tile through registers into rows padded to D + 16
-  // elements: its accumulators leave no room for the direct-load pipeline (it spilled).
+  // latent (PAD) reads rows padded to D + 16 elements, one wave-wide direct load per row:
+  // the swizzled addressing's per-chunk bases do not fit beside its accumulators.
   static constexpr int CPR = D / 8;               // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;            // rows per wave-wide load
   static constexpr bool PAD = D >= 512;
@@ -1274,37 +1274,63 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
         for (int db = 0; db < C::NDB; ++db) dkt[kb][db] += dvt[kb][db];
   }
 
-  // ---- rows: lane (key + 16g) holds d?[key][16db + 4g .. +4]
+  // ---- rows: lane (key + 16g) holds d?[key][16db + 4g .. +4].  The paged / contiguous
+  // choice sits outside the block loops, so each loop converts and stores one 16-column
+  // block at a time (with the branch inside, the 512-wide latent read every accumulator
+  // out at once and spilled).  At D >= 256 the keys are laundered, so that their
+  // addresses are recomputed here rather than kept live across the step loop from the K
+  // loads, which spilled them (at D <= 128 the registers this frees changed the step
+  // loop's allocation: the D = 64 kernel went to four waves per SIMD and ran slower)
+  int kst[KB];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
-    if (!kok[kb]) continue;
+    kst[kb] = key[kb];
+    if constexpr (D >= 256) asm volatile("" : "+v"(kst[kb]));
+  }
+  if (s.pages) {  // float32 gradients, added atomically
 #pragma unroll
-    for (int db = 0; db < C::NDB; ++db) {
-      T k4[4], v4[4];
+    for (int kb = 0; kb < KB; ++kb) {
+      if (!kok[kb]) continue;
+      float* const dkf = (float*)s.dk + key_elem(s, s.dkbase, s.dksn, kst[kb]) + gq * 4;
+      float* const dvf = (float*)s.dv + key_elem(s, s.dvbase, s.dvsn, kst[kb]) + gq * 4;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        k4[r] = (T)dkt[kb][db][r];
-        if constexpr (C::MLA_ONLY) {
-          v4[r] = (T)0.f;
-        } else {
-          v4[r] = (T)dvt[kb][db][r];
-        }
-      }
-      if (s.pages) {  // float32 gradients, added atomically
-        float* dkf = (float*)s.dk + key_elem(s, s.dkbase, s.dksn, key[kb]) + db * 16 + gq * 4;
-        float* dvf = (float*)s.dv + key_elem(s, s.dvbase, s.dvsn, key[kb]) + db * 16 + gq * 4;
+      for (int db = 0; db < C::NDB; ++db) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) atomicAdd(dkf + r, dkt[kb][db][r]);
+        for (int r = 0; r < 4; ++r) atomicAdd(dkf + db * 16 + r, dkt[kb][db][r]);
         if constexpr (!C::MLA_ONLY) {
           if (!mla)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) atomicAdd(dvf + r, dvt[kb][db][r]);
+            for (int r = 0; r < 4; ++r) atomicAdd(dvf + db * 16 + r, dvt[kb][db][r]);
         }
-        continue;
       }
-      *(u32x2*)(s.dk + (s.dkbase + (int64_t)key[kb] * s.dksn + db * 16 + gq * 4) * 2) = *(const u32x2*)k4;
-      if (!mla)
-        *(u32x2*)(s.dv + (s.dvbase + (int64_t)key[kb] * s.dvsn + db * 16 + gq * 4) * 2) = *(const u32x2*)v4;
+    }
+    return;
+  }
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    if (!kok[kb]) continue;
+    char* const dkr = s.dk + (s.dkbase + (int64_t)kst[kb] * s.dksn + gq * 4) * 2;
+    char* const dvr = s.dv + (s.dvbase + (int64_t)kst[kb] * s.dvsn + gq * 4) * 2;
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) {
+      T k4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = dkt[kb][db][r];
+        // the latent's accumulators fill the AGPRs: read each one out where it is stored
+        // (copied out all at once after the step loop, they did not fit the VGPRs)
+        if constexpr (C::MLA_ONLY) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(dkt[kb][db][r]));
+        k4[r] = (T)x;
+      }
+      *(u32x2*)(dkr + db * 32) = *(const u32x2*)k4;
+      if constexpr (!C::MLA_ONLY) {
+        if (!mla) {
+          T v4[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v4[r] = (T)dvt[kb][db][r];
+          *(u32x2*)(dvr + db * 32) = *(const u32x2*)v4;
+        }
+      }
     }
   }
 }
