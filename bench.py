@@ -141,10 +141,14 @@ def _prefill_paged(cache, k_cache, v_cache, cu_kv, *, hk: int, H: int, D: int, m
                                  is_mla=mla, num_heads=H, head_dim=D)
 
 
-def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
+def make_case(cfg: int, device: torch.device, *, variant: str = "", batch: int = 0,
+              query_lens: tuple[int, int] | None = None, head_dim: int = 0) -> Case:
     """Build BASELINE config `cfg` (1..5; config 5 variant "prefill" is 5b, variant
     "paged" / "paged_seq" store configs 3-5's context as a paged KV pool, pages shuffled /
-    in key order) with
+    in key order; for configs 3 and 4, `batch`, `query_lens` = (lo, hi) and `head_dim`
+    replace the sequence count, the per-sequence query length range (N: the range's top
+    rounded up to 64) and the head dim: shapes for the tile-configuration sweep, not
+    BASELINE configs) with
     seeded synthetic inputs: lengths from a CPU generator seeded 1000+cfg (query
     lengths first, then context lengths), tensors from a device generator with the
     same seed, fp32 normal * std cast to the config dtype."""
@@ -206,6 +210,16 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
             lq = torch.randint(512, 2048 + 1, (B,), generator=gcpu)
             lc = torch.full((B,), 8192)
             cbs, mla, causal = B, True, False
+        if (batch or query_lens or head_dim) and cfg in (3, 4):
+            B, D = batch or B, head_dim or D
+            lo, hi = query_lens or (int(lq.min()), int(lq.max()))
+            N = (hi + 63) // 64 * 64
+            lq = torch.randint(lo, hi + 1, (B,), generator=gcpu)
+            if cfg == 3:
+                lc = torch.randint(512, 2048 + 1, (B,), generator=gcpu)
+                cbs = B
+        elif batch or query_lens or head_dim:
+            raise ValueError("--batch / --query-lens / --head-dim apply to configs 3 and 4 only")
         prefill = variant == "prefill"
         scale = 1.0 / math.sqrt(D)
         q = _randn((B, H, N, D), gdev, device, dt, std)
@@ -246,8 +260,11 @@ def make_case(cfg: int, device: torch.device, *, variant: str = "") -> Case:
             4: "cfg4 packed causal_query_seq_attn bf16 B=16 H=12 D=64, shared ctx 4096",
             5: "cfg5 MLA bf16 B=8 64 heads : 1 latent D=512, cached latent ctx 8192/seq",
         }
+        shape = ""
+        if batch or query_lens or head_dim:
+            shape = f" [sweep shape: B={B}, D={D}, query lengths U[{int(lq.min())}..{int(lq.max())}], N={N}]"
         return Case(
-            cfg, names[cfg] + (" (prefill=True)" if prefill else "") + (f" ({variant} KV context)" if variant.startswith("paged") else ""),
+            cfg, names[cfg] + shape + (" (prefill=True)" if prefill else "") + (f" ({variant} KV context)" if variant.startswith("paged") else ""),
             dt, H, D,
             [int(x) for x in lq], lengths_ctx, causal, prefill, mla,
             call=call,
@@ -366,6 +383,10 @@ def _kernel_class(name: str) -> str | None:
     return None
 
 
+# shape overrides (--batch / --query-lens) handed to the counter passes' child processes
+_SHAPE_ARGS: list[str] = []
+
+
 def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s: float, tile: int = 0) -> dict:
     """One `rocprofv3 --pmc <counter>` run of this script's --profile driver in a child
     process.  Returns {"attn": mean KiB per attention dispatch, "copy": KiB of the
@@ -387,6 +408,7 @@ def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s
         cmd += ["--variant", variant]
     if tile:
         cmd += ["--tile-config", str(tile)]
+    cmd += _SHAPE_ARGS
     env = dict(os.environ, TMPDIR="/tmp")
     try:
         # rocprofv3 may exit non-zero after writing complete results; the CSV decides
@@ -573,6 +595,12 @@ def main() -> None:
     ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--tile-config", type=int, default=0,
                     help="force the attention kernel's tile configuration k (0: the library's choice)")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="configs 3 and 4: sequence count (tile-configuration sweep shapes)")
+    ap.add_argument("--query-lens", default="",
+                    help="configs 3 and 4: per-sequence query lengths LO:HI (tile-configuration sweep shapes)")
+    ap.add_argument("--head-dim", type=int, default=0,
+                    help="configs 3 and 4: head dim (tile-configuration sweep shapes)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes that measure HBM traffic")
     ap.add_argument(
@@ -583,6 +611,13 @@ def main() -> None:
         "and one call of each copy kernel; prints no JSON line",
     )
     args = ap.parse_args()
+    query_lens = tuple(int(x) for x in args.query_lens.split(":")) if args.query_lens else None
+    if args.batch:
+        _SHAPE_ARGS.extend(["--batch", str(args.batch)])
+    if args.query_lens:
+        _SHAPE_ARGS.extend(["--query-lens", args.query_lens])
+    if args.head_dim:
+        _SHAPE_ARGS.extend(["--head-dim", str(args.head_dim)])
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
@@ -611,7 +646,8 @@ def main() -> None:
         from flash_mlm.host import host as hh
 
         hh._TILE_CONFIG = args.tile_config
-    case = make_case(args.config, device, variant=args.variant)
+    case = make_case(args.config, device, variant=args.variant, batch=args.batch, query_lens=query_lens,
+                     head_dim=args.head_dim)
     print(f"[bench] {case.workload}: built inputs", file=sys.stderr, flush=True)
 
     if args.profile:

@@ -233,7 +233,9 @@ typedef struct fmlm_attn_params {
   int64_t ctx_page_stride;
   int32_t ctx_pages_per_batch;
   /* Tile configuration of the bf16/f16 attention kernel: 0 = chosen by the library from
-   * the head dim and the work (query tiles against the GPU's workgroup slots); k >= 1
+   * the head dim and the query rows per sequence (D = 64 and 128: configuration 3 when
+   * total_q <= 64 * B, i.e. sequences of at most 64 query rows on average, else 1; other
+   * head dims: 1); k >= 1
    * forces compiled configuration k of the head dim (fmlm_attn_workspace_bytes returns
    * FMLM_E_ARG for a k that does not exist).  Configurations, as (query rows per
    * workgroup, waves per workgroup): D = 16, 32: 1 = (128, 4); D = 64: 1 = (128, 4),

@@ -403,6 +403,74 @@ def test_every_tile_config(D, k, mode, device):
     _close(unpack_from_kernel(out, meta, H), ref)
 
 
+def test_library_tile_choice_by_query_rows(device):
+    # tile_config 0 at D = 64 / 128: configuration 3 (64 query rows per workgroup) when the
+    # sequences average at most 64 query rows (total_q <= 64 B), configuration 1 (128 rows)
+    # otherwise.  The workspace holds the schedule's work units, whose count follows the
+    # workgroup's row count, so its size shows which configuration was chosen.
+    from flash_mlm import _lib
+
+    lib = _lib.load()
+    for D in (64, 128):
+        for B, total_q, want in ((40, 64 * 40, 3), (40, 64 * 40 + 1, 1), (7, 7 * 30, 3), (7, 7 * 900, 1)):
+            p = _lib.AttnParams()
+            p.dtype, p.B, p.H, p.D, p.N, p.total_q = _lib.DTYPE_BF16, B, 8, D, 1024, total_q
+            p.cu_seqlens_q = 4096  # packed rows (sizing reads no device memory)
+            ws = {}
+            for k in (0, 1, 3):
+                p.tile_config = k
+                ws[k] = lib.fmlm_attn_workspace_bytes(p)
+            assert ws[1] > 0 and ws[3] > 0 and ws[1] != ws[3], (D, B, total_q, ws)
+            assert ws[0] == ws[want], (D, B, total_q, ws)
+    # other head dims keep configuration 1 for short sequences
+    p.D, p.B, p.total_q = 256, 40, 64 * 40
+    p.tile_config = 0
+    w0 = lib.fmlm_attn_workspace_bytes(p)
+    p.tile_config = 1
+    assert w0 == lib.fmlm_attn_workspace_bytes(p)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("mode", ["ctx", "causal_shared", "paged"])
+def test_short_query_sequences_library_tile(D, mode, device):
+    # sequences of at most 64 query rows: the library's choice is the 64-row configuration
+    torch.manual_seed(8500 + D)
+    dtype = torch.bfloat16 if mode != "ctx" else torch.float16
+    scale = 1.0 / math.sqrt(D)
+    lengths = [1, 64, 17, 0, 40, 63, 5, 33, 64, 2]
+    B, H, N = len(lengths), 3, 64
+    causal = mode == "causal_shared"
+    q, kk, v = (_randn((B, H, N, D), device, dtype) for _ in range(3))
+    if mode == "causal_shared":
+        ctx, cbs = [300], 1
+    else:
+        ctx, cbs = [5, 0, 130, 700, 64, 3, 1, 90, 257, 40], B
+    cache, kc, vc, cu_kv, Tc = _context_cache(cbs, H, D, False, ctx, device, dtype)
+    if mode == "paged":  # the same context rows in 64-row pages, pool in reverse page order
+        lens = (cu_kv[1:] - cu_kv[:-1]).tolist()
+        need = [(n + 63) // 64 for n in lens]
+        P = sum(need)
+        bt = torch.zeros((len(lens), max(need)), dtype=torch.int32)
+        kp, vp = (torch.zeros((H, P * 64, D), dtype=dtype, device=device) for _ in range(2))
+        pg = 0
+        for c, (n, npg) in enumerate(zip(lens, need)):
+            for j in range(npg):
+                slot, r0 = P - 1 - (pg + j), int(cu_kv[c]) + 64 * j
+                m = min(64, n - 64 * j)
+                bt[c, j] = slot
+                kp[:, slot * 64 : slot * 64 + m] = kc.view(H, Tc, D)[:, r0 : r0 + m]
+                vp[:, slot * 64 : slot * 64 + m] = vc.view(H, Tc, D)[:, r0 : r0 + m]
+            pg += npg
+        cache = InferenceCache()
+        cache.prefill_paged_kv_cache(0, k_pages=kp.view(H, P, 64, D), v_pages=vp.view(H, P, 64, D),
+                                     block_table=bt.to(device), context_lens=torch.tensor(lens, dtype=torch.int32),
+                                     is_mla=False, num_heads=H, head_dim=D)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, kk, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=causal)
+    ref = _packed_oracle(q, kk, v, lengths, scale, causal=causal, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=cbs, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
+
+
 # ---------------------------------------------------------------------------
 # split-KV: few work units over long key ranges are cut into parts whose partial
 # results a second kernel merges (the schedule decides; these shapes have far fewer
