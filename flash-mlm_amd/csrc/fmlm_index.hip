@@ -172,15 +172,20 @@ struct PackArgs {
 // head), one contiguous run of rows to another contiguous run, with zero rows around.
 // A workgroup takes a window of kWin bytes of one such destination span: every thread
 // moves kPer vectors of VB bytes, issuing all its loads before its stores, and the
-// threads of one vector index cover kSpanThreads * VB consecutive bytes.
+// threads of one vector index cover kSpanThreads * VB consecutive bytes.  The KV append
+// moves one vector per thread (kAppendPer): its windows are sized to the average batch
+// and longer batches loop, and the smaller windows balance that loop better (config 3
+// append 0.69 -> 0.75 of HBM peak, config 5 0.63 -> 0.69; the pack kernel measured best
+// at four, 1.5x slower at eight; non-temporal stores were slower in every kernel).
 // ---------------------------------------------------------------------------
 constexpr int kSpanThreads = 256;
 constexpr int kPer = 4;
+constexpr int kAppendPer = 1;
 
-template <int VB>
+template <int VB, int PER = kPer>
 struct Span {
   typedef typename VecOf<VB>::type V;
-  static constexpr int64_t kWin = (int64_t)kSpanThreads * kPer * VB;
+  static constexpr int64_t kWin = (int64_t)kSpanThreads * PER * VB;
 };
 
 // Bytes [w0, w0 + kWin) of a destination span of `len` bytes: offsets below `cpy` come from
@@ -355,10 +360,11 @@ __global__ __launch_bounds__(kSpanThreads) void kv_append_kernel(AppendArgs args
     const char* const sa = (const char*)tt.old + ((int64_t)h * t_old + a0) * row_bytes;
     const char* const sb = (const char*)tt.add + ((int64_t)h * t_new + b0) * row_bytes;
     char* const d = out + (int64_t)o0 * row_bytes;
-    for (int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin; w0 < bytes; w0 += (int64_t)gridDim.x * Span<VB>::kWin) {
-      V v[kPer];
+    typedef Span<VB, kAppendPer> W;
+    for (int64_t w0 = (int64_t)blockIdx.x * W::kWin; w0 < bytes; w0 += (int64_t)gridDim.x * W::kWin) {
+      V v[kAppendPer];
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {
+      for (int i = 0; i < kAppendPer; ++i) {
         const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
         v[i] = V{};
         if (o < old_bytes)
@@ -367,7 +373,7 @@ __global__ __launch_bounds__(kSpanThreads) void kv_append_kernel(AppendArgs args
           v[i] = *(const V*)(sb + (o - old_bytes));
       }
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {
+      for (int i = 0; i < kAppendPer; ++i) {
         const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
         if (o < bytes) *(V*)(d + o) = v[i];
       }
@@ -590,7 +596,7 @@ extern "C" int fmlm_kv_append(const fmlm_append_tensor* tensors, int32_t n_tenso
   if ((int64_t)H * n_tensors > 65535 || C + 1 > 65535) return FMLM_E_ARG;
   // windows per (tensor, head, batch) at the average merged batch length; longer batches
   // are covered by the stride loop
-  const int64_t win = (int64_t)kSpanThreads * kPer * vb;
+  const int64_t win = (int64_t)kSpanThreads * kAppendPer * vb;
   const int64_t avg = (rows + C) / (C + 1);
   const int64_t gx = std::max<int64_t>(1, std::min<int64_t>((avg * D * esz + win - 1) / win, 4096));
   const dim3 grid((unsigned)gx, H * n_tensors, C + 1);
