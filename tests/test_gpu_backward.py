@@ -95,21 +95,23 @@ def test_backward_compressed_with_context(dtype, D, mla, causal, device):
 
 
 @pytest.mark.parametrize("D", [32, 256])
-def test_backward_compressed_head_dims(D, device):
-    gen = torch.Generator().manual_seed(7100 + D)
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_compressed_head_dims(D, causal, device):
+    gen = torch.Generator().manual_seed(7100 + D + causal)
     lengths = [33, 64, 5]
     B, H, N, dtype = len(lengths), 2, 64, torch.bfloat16
     scale = 0.3
     q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
     cache, kc, vc, cu_kv, total = _packed_cache([20, 65, 1], H=H, D=D, mla=False, dtype=dtype, device=device, gen=gen)
     meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
-    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=causal)
     dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
     out.backward(dout)
     from flash_mlm import unpack_from_kernel
     g = ar.mlm_attention_packed_backward(
         _np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)), lengths, scale, k_cache=_np(kc),
-        v_cache=_np(vc), cu_seqlens_kv=cu_kv, total_context_len=total, context_batch_size=B)
+        v_cache=_np(vc), cu_seqlens_kv=cu_kv, total_context_len=total, context_batch_size=B,
+        causal_query_seq_attn=causal)
     for got, ref, name in ((q.grad, g[0], "dq"), (k.grad, g[1], "dk"), (v.grad, g[2], "dv"),
                            (kc.grad, g[3], "dkc"), (vc.grad, g[4], "dvc")):
         _close(got, ref, name)

@@ -147,7 +147,7 @@ def _scatter_to_pages(grad_ctx, block_table, lens, H_kv, P, D):
     return pool
 
 
-@pytest.mark.parametrize("mla,D", [(False, 128), (True, 64), (False, 16)])
+@pytest.mark.parametrize("mla,D", [(False, 128), (True, 64), (False, 16), (False, 256)])
 @pytest.mark.parametrize("shared_page", [False, True])
 def test_paged_context_backward(mla, D, shared_page, device):
     """Backward over a paged context (float32 accumulation of the pool gradient): q/k/v
