@@ -172,15 +172,19 @@ struct PackArgs {
 // head), one contiguous run of rows to another contiguous run, with zero rows around.
 // A workgroup takes a window of kWin bytes of one such destination span: every thread
 // moves kPer vectors of VB bytes, issuing all its loads before its stores, and the
-// threads of one vector index cover kSpanThreads * VB consecutive bytes.  The KV append
-// moves one vector per thread (kAppendPer): its windows are sized to the average batch
-// and longer batches loop, and the smaller windows balance that loop better (config 3
-// append 0.69 -> 0.75 of HBM peak, config 5 0.63 -> 0.69; the pack kernel measured best
-// at four, 1.5x slower at eight; non-temporal stores were slower in every kernel).
+// threads of one vector index cover kSpanThreads * VB consecutive bytes.  Pack and the KV
+// append size their grids to the average sequence (batch) length, and longer ones loop
+// over further windows: a grid sized to the longest left many workgroups with nothing to
+// copy.  Their windows are smaller than the other span kernels' (kPackPer, kAppendPer
+// vectors per thread), which balances that loop.  Measured against kPer-vector windows:
+// pack with an N-sized grid -> average-sized with two vectors, config 3 0.67 -> 0.78 of
+// HBM peak, config 5 0.67 -> 0.69, config 4 0.33 -> 0.42; append with one vector, config 3
+// 0.69 -> 0.75, config 5 0.63 -> 0.69.  Non-temporal stores were slower in every kernel.
 // ---------------------------------------------------------------------------
 constexpr int kSpanThreads = 256;
 constexpr int kPer = 4;
 constexpr int kAppendPer = 1;
+constexpr int kPackPer = 2;
 
 template <int VB, int PER = kPer>
 struct Span {
@@ -192,13 +196,13 @@ struct Span {
 // src at the same offset, the rest are zero.  src_row_bytes / src_pitch (bytes) read a
 // strided source: offset o is row o / src_row_bytes, column o % src_row_bytes, at
 // row * src_pitch + column (src_pitch == src_row_bytes: contiguous).
-template <int VB, bool STRIDED>
+template <int VB, bool STRIDED, int PER = kPer>
 FMLM_DEV void span_window(const char* __restrict__ src, char* __restrict__ dst, int64_t w0, int64_t len,
                           int64_t cpy, uint32_t src_row_bytes, int64_t src_pitch) {
   typedef typename Span<VB>::V V;
-  V v[kPer];
+  V v[PER];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
     v[i] = V{};
     if (o < cpy) {
@@ -211,7 +215,7 @@ FMLM_DEV void span_window(const char* __restrict__ src, char* __restrict__ dst, 
     }
   }
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
+  for (int i = 0; i < PER; ++i) {
     const int64_t o = w0 + ((int64_t)i * kSpanThreads + threadIdx.x) * VB;
     if (o < len) *(V*)(dst + o) = v[i];
   }
@@ -242,11 +246,11 @@ __global__ __launch_bounds__(kSpanThreads) void pack_kernel(PackArgs args, int n
     if (start < 0 || start >= T) return;
     len = min(len, T - start);
     const int64_t bytes = (int64_t)max(len, 0) * row_bytes;
-    const int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin;
-    if (w0 >= bytes) return;
     const char* src = (const char*)tt.src + ((int64_t)b * tt.s_sb + (int64_t)h * tt.s_sh) * esz;
-    span_window<VB, STRIDED>(src, dst + (int64_t)start * row_bytes, w0, bytes, bytes, (uint32_t)row_bytes,
-                             tt.s_sn * esz);
+    typedef Span<VB, kPackPer> W;
+    for (int64_t w0 = (int64_t)blockIdx.x * W::kWin; w0 < bytes; w0 += (int64_t)gridDim.x * W::kWin)
+      span_window<VB, STRIDED, kPackPer>(src, dst + (int64_t)start * row_bytes, w0, bytes, bytes,
+                                         (uint32_t)row_bytes, tt.s_sn * esz);
   } else {  // zero rows outside [c0, c1): the spans [0, c0) and [c1, T_pad)
     const int c0 = cu ? min(max(cu[0], 0), T) : 0;
     const int c1 = cu ? min(max(cu[B], c0), T) : T;
@@ -466,9 +470,11 @@ extern "C" int fmlm_pack(const fmlm_pack_tensor* tensors, int32_t n_tensors, int
   hipStream_t s = (hipStream_t)stream;
   int hmax = 0;
   for (int i = 0; i < n_tensors; ++i) hmax = tensors[i].heads > hmax ? tensors[i].heads : hmax;
-  // windows per sequence span (at most N rows); the zero slice strides over its rows
-  const int64_t win = (int64_t)kSpanThreads * kPer * vb;
-  const int64_t gx = std::max<int64_t>(1, ((int64_t)(N > 0 ? N : 1) * D * esz + win - 1) / win);
+  // windows per sequence span at the average sequence length (longer sequences loop over
+  // further windows); the zero slice strides over its rows
+  const int64_t win = (int64_t)kSpanThreads * kPackPer * vb;
+  const int64_t avg = B > 0 ? std::min<int64_t>(N, ((int64_t)T + B - 1) / B) : N;
+  const int64_t gx = std::max<int64_t>(1, ((int64_t)(avg > 0 ? avg : 1) * D * esz + win - 1) / win);
   if ((int64_t)hmax * n_tensors > 65535 || B + 1 > 65535 || gx > (1 << 30)) return FMLM_E_ARG;
   const dim3 grid((unsigned)gx, hmax * n_tensors, B + 1);
   // source rows are contiguous when every tensor's row stride is the row length
