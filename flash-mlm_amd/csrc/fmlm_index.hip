@@ -255,11 +255,16 @@ __global__ __launch_bounds__(kSpanThreads) void pack_kernel(PackArgs args, int n
     const int c0 = cu ? min(max(cu[0], 0), T) : 0;
     const int c1 = cu ? min(max(cu[B], c0), T) : T;
     const int64_t lo = (int64_t)c0 * row_bytes, hi = (int64_t)(T_pad - c1) * row_bytes;
-    for (int64_t w0 = (int64_t)blockIdx.x * Span<VB>::kWin; w0 < lo + hi; w0 += (int64_t)gridDim.x * Span<VB>::kWin) {
-      if (w0 < lo)
-        span_window<VB, false>(nullptr, dst, w0, lo, 0, 1u, 0);
+    // windows [0, nlo) cover the span [0, c0), the rest the span [c1, T_pad) from its own
+    // offset 0 (a shared byte range would skip the first bytes of the second span when
+    // lo is not a whole number of windows)
+    constexpr int64_t kWin = Span<VB>::kWin;
+    const int64_t nlo = (lo + kWin - 1) / kWin, nwin = nlo + (hi + kWin - 1) / kWin;
+    for (int64_t i = blockIdx.x; i < nwin; i += gridDim.x) {
+      if (i < nlo)
+        span_window<VB, false>(nullptr, dst, i * kWin, lo, 0, 1u, 0);
       else
-        span_window<VB, false>(nullptr, dst + (int64_t)c1 * row_bytes, w0 - lo, hi, 0, 1u, 0);
+        span_window<VB, false>(nullptr, dst + (int64_t)c1 * row_bytes, (i - nlo) * kWin, hi, 0, 1u, 0);
     }
   }
 }
@@ -579,9 +584,12 @@ extern "C" int fmlm_kv_append(const fmlm_append_tensor* tensors, int32_t n_tenso
   if (!valid_elem_bytes(esz)) return FMLM_E_DTYPE;
   if (!tensors || n_tensors < 1 || n_tensors > 2 || H < 0 || D < 1 || C < 0 || t_old < 0 || t_new < 0)
     return FMLM_E_ARG;
-  if (C > 0 && (!cu_old || !cu_new)) return FMLM_E_ARG;
   const int64_t rows = (int64_t)t_old + t_new;
   if (rows > 0x7fffffff) return FMLM_E_ARG;
+  // every launch below reads cu_old[0..C] and cu_new[0..C] (the tail slice reads index C
+  // even when C == 0); the only call that launches nothing is the empty one
+  const bool launches = (H > 0 && rows > 0) || (cu_out && C > 0);
+  if (launches && (!cu_old || !cu_new)) return FMLM_E_ARG;
   if (H == 0 || rows == 0) {  // nothing to move: only the offsets
     if (!cu_out || C == 0) return 0;
     AppendArgs args = {};

@@ -53,6 +53,14 @@ def test_argument_rejection_without_launch():
     assert lib.fmlm_copy_segments(2, None, 16, 0, None, None, 16, 4, None, 1, 1, 16, None) == 0  # nothing to copy
     assert lib.fmlm_kv_append(None, 1, 2, 1, 16, 1, 4, 4, None, None, None, None) == -1
     assert lib.fmlm_kv_append(None, 1, 3, 1, 16, 1, 4, 4, None, None, None, None) == -2  # bad element size
+    # a launch reads cu_old / cu_new up to index C, so null offsets are rejected even when
+    # C == 0 (the tail slice reads index 0); nothing to move and no cu_out is accepted
+    t = (_lib.AppendTensor * 1)()
+    t[0].old = t[0].add = t[0].out = 256
+    assert lib.fmlm_kv_append(t, 1, 2, 1, 16, 0, 4, 4, None, None, None, None) == -1
+    assert lib.fmlm_kv_append(t, 1, 2, 1, 16, 0, 4, 4, None, 256, None, None) == -1
+    assert lib.fmlm_kv_append(t, 1, 2, 1, 16, 0, 4, 4, 256, None, None, None) == -1
+    assert lib.fmlm_kv_append(t, 1, 2, 0, 16, 0, 4, 4, None, None, None, None) == 0  # no heads, no offsets out
     assert lib.fmlm_pack_metadata(None, 0, 1, 4, 0, None, None, None, None, None, None) == -1
     assert lib.fmlm_tile_map(None, 1, 4, 0, None, None, None, None) == -1
     assert lib.fmlm_attn_fwd(None, None) == -1

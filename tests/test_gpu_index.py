@@ -218,6 +218,36 @@ def test_pack_non_contiguous_source(device):
     np.testing.assert_array_equal(_np(hu.pack_for_kernel(x, meta, flatten_for_kernel=True).float()), ref)
 
 
+@pytest.mark.parametrize("c0", [0, 5, 37])
+def test_pack_offsets_not_starting_at_zero(c0, device):
+    """fmlm_pack with cu_seqlens[0] > 0: sequence b's rows land at packed rows
+    cu[b] + p and every other row of [0, T_pad) is zero, also when the leading span
+    [0, cu[0]) is not a whole number of the kernel's zero-fill windows."""
+    from flash_mlm import _lib
+
+    B, H, N, D = 3, 2, 40, 64
+    L = [9, 0, 23]
+    cu = [c0]
+    for n in L:
+        cu.append(cu[-1] + n)
+    T = cu[-1] + 3
+    T_pad = T + 200
+    x = torch.randn(B, H, N, D, device=device).to(torch.bfloat16)
+    dst = torch.full((H * T_pad, D), 3.0, device=device, dtype=torch.bfloat16)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=device)
+    t = (_lib.PackTensor * 1)()
+    t[0].src, t[0].s_sb, t[0].s_sh, t[0].s_sn = x.data_ptr(), H * N * D, N * D, D
+    t[0].dst, t[0].heads = dst.data_ptr(), H
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.fmlm_pack(t, 1, 2, B, N, D, cu_t.data_ptr(), T, T_pad, stream), "fmlm_pack")
+    want = np.zeros((H, T_pad, D), np.float32)
+    xn = _np(x.float())
+    for b in range(B):
+        want[:, cu[b] : cu[b] + L[b]] = xn[b, :, : L[b]]
+    np.testing.assert_array_equal(_np(dst.float()).reshape(H, T_pad, D), want)
+
+
 def test_pack_unpack_full_size_round_trip(device):
     # BASELINE config 3 shape: size-independent properties (round trip, zero padding, checksums)
     g = torch.Generator().manual_seed(1003)
