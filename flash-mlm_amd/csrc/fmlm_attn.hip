@@ -32,25 +32,35 @@ namespace fmlm {
 // Work schedule.  A work unit is (sequence b, head h, query tile j) with tiles of BQ
 // real (unpadded) rows.  Units of one (b, h) group share that group's K/V, and the
 // groups of one head may share keys too (a shared context, the causal token range), so
-// groups are kept on few XCDs: the dispatcher hands workgroup L to XCD L % 8, and the
-// units of XCD x occupy its consecutive slots x + 8*pos.  The groups of a head are cut
-// into parts by sequence rank and each XCD takes a run of parts in head order (see
-// schedule_kernel); within a part, groups go longest-first (estimated keys x tiles).
-// Slots past an XCD's share are idle (b = -1).  The list is built once per
-// cu_seqlens by schedule_kernel and cached by the host.
+// groups are kept on few XCDs: units meant for XCD x go to queue x, whose entries are
+// run by workgroups the dispatcher hands to XCD x (workgroup w goes to XCD w % 8).  The
+// groups of a head are cut into parts by sequence rank and each XCD takes a run of parts
+// in head order (see schedule_kernel); within a part, groups go longest-first (estimated
+// keys x tiles).
+// The list is built once per cu_seqlens by schedule_kernel and cached by the host.
+//
+// Queues.  Queue x holds header[8 + x] units at units + x * cap (cap = header[5], a
+// bound on the whole launch's units, so one queue never overflows whatever the
+// placement).  A launch runs one unit per workgroup over G >= cap workgroups: workgroup
+// w takes entry w / 8 of queue w % 8 (entries [0, G_x) of queue x, G_x = ceil((G - x) /
+// 8), are taken this way, in dispatch order); a workgroup whose queue has no such entry
+// is a spare and takes, by its rank among the spares, one of the entries past G_y of the
+// queues y that hold more than G_y (see workgroup_unit).  Placements keep the queues
+// about equally long, so overflow entries are few and most spares exit at once.
+// Head-packed launches run 8 * cap workgroups (every entry its static workgroup's).
 //
 // Split-KV: when the units would fill the GPU's workgroup slots for fewer than
 // kSplitRounds rounds, each query tile's key range is cut into S parts (a split group);
-// every part is a unit that writes a partial record (O / l, m, l per row) and a second
-// kernel, merge_kernel, combines each group's records into the output.  (Merging inside
-// the attention kernel would need device-scope release/acquire between workgroups,
-// which writes back and invalidates an XCD's whole L2 each time.)
+// every part is a unit that writes a partial record (O / l as fp32, then m and l per
+// row) and a second kernel, merge_kernel, combines each group's records into the output.
+// (Merging inside the attention kernel would need device-scope release/acquire between
+// workgroups, which writes back and invalidates an XCD's whole L2 each time.)
 //
-// Unit encoding (int4): x = b (-1: idle), y = h | tile << 16, z = first record of the
-// split group, w = -1 (no split) or group | s << 20 | (S - 1) << 25.
-// Schedule buffer: [0, 256) header (n_units, n_groups, groups / records offsets, record
-// bytes), units at 256, then the group list (int4: b, h | tile << 16, first record, S),
-// then the records.
+// Unit encoding (int4): x = b, y = h | tile << 16, z = first record of the split group,
+// w = -1 (no split) or group | s << 20 | (S - 1) << 25.
+// Schedule buffer: [0, 256) header (units, n_groups, groups / records offsets, record
+// bytes, queue capacity, queue lengths), the queues at 256, then the
+// group list (int4: b, h | tile << 16, first record, S), then the records.
 // ---------------------------------------------------------------------------
 constexpr int kXcds = 8;
 constexpr int kSchedThreads = 512;  // one wave per XCD
@@ -59,10 +69,18 @@ constexpr int kSplitBK = 64;        // key tile of the split-capable kernel
 constexpr int kMaxSplits = 16;
 constexpr int kMinSplitTiles = 8;   // key tiles per part at least
 constexpr float kSplitRounds = 1.5f;
+// schedule header fields (int32 index)
+constexpr int kHdrUnits = 0;      // units in all queues
+constexpr int kHdrGroups = 1;     // split groups
+constexpr int kHdrGroupsOff = 2;  // byte offsets of the group list and the records
+constexpr int kHdrRecordsOff = 3;
+constexpr int kHdrRecBytes = 4;
+constexpr int kHdrCap = 5;        // entries per queue
+constexpr int kHdrQueueLen = 8;   // [8, 16): entries of queue x
 
 
 __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn_params p, int BQ,
-                                                                 int capacity, int slots,
+                                                                 int cap_q, int slots,
                                                                  int rec_cap,
                                                                  int4* __restrict__ units,
                                                                  int32_t* __restrict__ header,
@@ -233,27 +251,27 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const fmlm_attn
     }
     for (int j = 0; j < tiles; ++j) {
       for (int sp = 0; sp < S; ++sp) {
-        const int64_t slot = (int64_t)x + (int64_t)kXcds * (pos + j * S + sp);
+        const int64_t qpos = (int64_t)pos + j * S + sp;  // < cap_q: cap_q bounds the launch's units
         const int wv = S > 1 ? (gid0 + j) | (sp << 20) | ((S - 1) << 25) : -1;
-        if (slot < capacity) units[slot] = make_int4(b, hf(j), rec0 + j * S, wv);
+        if (qpos < cap_q) {
+          units[(int64_t)x * cap_q + qpos] = make_int4(b, hf(j), rec0 + j * S, wv);
+        }
       }
     }
     carry += __shfl(incl, 63);
   }
   if (lane == 0) s_len[x] = carry;
   __syncthreads();
-  int maxlen = 0;
-  for (int i = 0; i < kXcds; ++i) maxlen = max(maxlen, s_len[i]);
-  for (int q = carry + lane; q < maxlen; q += 64) {
-    const int64_t slot = (int64_t)x + (int64_t)kXcds * q;
-    if (slot < capacity) units[slot] = make_int4(-1, 0, 0, 0);
-  }
+  if (tid < kXcds) header[kHdrQueueLen + tid] = min(s_len[tid], cap_q);
   if (tid == 0) {
-    header[0] = (int)min((int64_t)kXcds * maxlen, (int64_t)capacity);
-    header[1] = s_groups;
-    header[2] = groups_off;
-    header[3] = records_off;
-    header[4] = rec_bytes;
+    int total = 0;
+    for (int i = 0; i < kXcds; ++i) total += min(s_len[i], cap_q);
+    header[kHdrUnits] = total;
+    header[kHdrGroups] = s_groups;
+    header[kHdrGroupsOff] = groups_off;
+    header[kHdrRecordsOff] = records_off;
+    header[kHdrRecBytes] = rec_bytes;
+    header[kHdrCap] = cap_q;
   }
 }
 
@@ -295,31 +313,37 @@ FMLM_DEV int64_t seg_row(const KvSeg& s, int i, bool is_v, const int32_t* cu, in
   return base + (int64_t)bb * sb + (int64_t)(i - cu[bb]) * sn;
 }
 
-// Resolve the workgroup's unit.  Returns false for an idle workgroup.
-FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const int32_t* n_units,
-                           int BQ, WorkItem& w, bool hpack = false) {
+FMLM_DEV int4 ldc4(const int4* a, int i) {
+  const int32_t* q = (const int32_t*)(a + i);
+  return make_int4(ldc(q, 0), ldc(q, 1), ldc(q, 2), ldc(q, 3));
+}
+
+// Unit u of a call: packed calls read queue entry u, dense calls map slot u (XCD u % 8,
+// position u / 8; group g = (b, h) has its ceil(N/BQ) tiles at consecutive positions of
+// XCD g % 8).  Returns false for a unit with nothing to do (an idle dense slot, or an entry
+// of a schedule built for other shapes).
+FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, int u, int BQ, WorkItem& w, bool hpack = false) {
   int b, h, tile;
   w.split_s = 0;
   w.split_n = 1;
   w.split_group = 0;
   w.rec0 = 0;
+  w.qcount = 0;
   if (p.cu_seqlens_q) {
-    if ((int)blockIdx.x >= *n_units) return false;
-    const int4 u = units[blockIdx.x];
-    b = u.x;
-    h = u.y & 0xffff;
-    tile = (int)((uint32_t)u.y >> 16);
-    if (b < 0 || b >= p.B || h >= p.H) return false;  // idle, or a schedule of other shapes
-    if (u.w >= 0) {
-      w.split_group = u.w & 0xfffff;
-      w.split_s = (u.w >> 20) & 31;
-      w.split_n = ((u.w >> 25) & 15) + 1;
-      w.rec0 = u.z;
+    const int4 un = ldc4(units, u);
+    b = un.x;
+    h = un.y & 0xffff;
+    tile = (int)((uint32_t)un.y >> 16);
+    if (b < 0 || b >= p.B || h >= p.H) return false;
+    if (un.w >= 0) {
+      w.split_group = un.w & 0xfffff;
+      w.split_s = (un.w >> 20) & 31;
+      w.split_n = ((un.w >> 25) & 15) + 1;
+      w.rec0 = un.z;
     }
   } else {
-    // dense: group g = (b, h) on XCD g % 8, its ceil(N/BQ) tiles on consecutive slots
     const int nt = (p.N + BQ - 1) / BQ;
-    const int x = blockIdx.x % kXcds, pos = blockIdx.x / kXcds;
+    const int x = u % kXcds, pos = u / kXcds;
     const int g = (pos / nt) * kXcds + x;
     tile = pos % nt;
     if (g >= p.B * p.H) return false;
@@ -410,6 +434,47 @@ FMLM_DEV bool resolve_work(const fmlm_attn_params& p, const int4* units, const i
 
 
 // ---------------------------------------------------------------------------
+// The unit of a workgroup (one unit per workgroup): dense calls map workgroup w to slot w
+// of the arithmetic layout; packed calls take queue entries (see the schedule comment
+// above).
+// ---------------------------------------------------------------------------
+// workgroups w < G with w % 8 == q: their static units are entries [0, G_q) of queue q
+FMLM_DEV int queue_static(int G, int q) { return (G - q + kXcds - 1) / kXcds; }
+
+// entry w / 8 of queue w % 8, or -1 past the queue's end (the unit of workgroup w of a
+// launch over 8 * cap workgroups, where every entry is some workgroup's)
+FMLM_DEV int queue_first(const int32_t* hdr, int w) {
+  const int x = w % kXcds, j = w / kXcds;
+  return j < ldc(hdr, kHdrQueueLen + x) ? x * ldc(hdr, kHdrCap) + j : -1;
+}
+
+// The unit of workgroup w of a packed launch over G workgroups, G at least the schedule's
+// units: its static entry w / 8 of queue w % 8 when the queue has one, else (a spare)
+// the overflow entry (an entry past G_q of some queue q) whose rank in queue order equals
+// the spare's rank in workgroup order, or -1.  Spares number sum_q (G_q - min(len_q,
+// G_q)), at least the overflow entries' sum_q max(len_q - G_q, 0) since sum_q G_q = G >=
+// sum_q len_q, so every entry is some workgroup's.  Uniform scalar arithmetic on the
+// eight queue lengths: no atomics, nothing carried between launches.
+FMLM_DEV int workgroup_unit(const int32_t* hdr) {
+  const int G = gridDim.x, w = blockIdx.x, x = w % kXcds, j0 = w / kXcds;
+  const int cap = ldc(hdr, kHdrCap);
+  if (j0 < ldc(hdr, kHdrQueueLen + x)) return x * cap + j0;
+  // spares before w: queue q's spare positions j < j0 (j <= j0 for q < x)
+  int r = 0;
+  for (int q = 0; q < kXcds; ++q) {
+    const int gq = queue_static(G, q);
+    r += max(0, min(gq, j0 + (q < x ? 1 : 0)) - min(ldc(hdr, kHdrQueueLen + q), gq));
+  }
+  for (int q = 0; q < kXcds; ++q) {
+    const int gq = queue_static(G, q), ov = max(0, ldc(hdr, kHdrQueueLen + q) - gq);
+    if (r < ov) return q * cap + gq + r;
+    r -= ov;
+  }
+  return -1;
+}
+
+
+// ---------------------------------------------------------------------------
 // MFMA kernel (bf16 / fp16)
 // ---------------------------------------------------------------------------
 
@@ -442,14 +507,15 @@ constexpr float kRescaleSlack = 8.0f;
 template <typename T, int D, int QB, int NW, int BK>
 __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(const fmlm_attn_params p,
                                                                const int4* __restrict__ units,
-                                                               const int32_t* __restrict__ n_units) {
+                                                               const int32_t* __restrict__ hdr) {
   typedef MfmaCfg<T, D, QB, NW, BK> C;
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
   T* const lds = (T*)smem_raw;
 
+  const int u = p.cu_seqlens_q ? workgroup_unit(hdr) : (int)blockIdx.x;
   WorkItem w;
-  if (!resolve_work(p, units, n_units, C::BQ, w)) return;
+  if (u < 0 || !resolve_work(p, units, u, C::BQ, w)) return;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -699,9 +765,6 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(con
 // by the explicit wait + barrier of step 4 instead.
 // ---------------------------------------------------------------------------
 
-// NaN-propagating max (v_maximum3_f32): no operand canonicalisation, unlike fmaxf
-
-
 // Page ids of 64 consecutive key tiles of a paged segment, one per lane of a VGPR: a tile
 // then costs a lane read.  A page id fetched per tile by a vector load would make its use
 // wait for every outstanding vector memory operation, the in-flight tile loads too; the
@@ -765,15 +828,16 @@ struct Mfma3Cfg {
 
 template <typename T, int D, int QB, int NW, int BK, bool PAGED, int PPB>
 __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
-    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
+    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ hdr) {
   typedef Mfma3Cfg<T, D, QB, NW, BK, PPB> C;
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
   char* const kbuf = smem_raw;                             // [NKBUF][TILEB]
   char* const vbuf = smem_raw + C::NKBUF * C::TILEB;       // [NVBUF][TILEB]
 
+  const int u = p.cu_seqlens_q ? workgroup_unit(hdr) : (int)blockIdx.x;
   WorkItem w;
-  if (!resolve_work(p, units, n_units, C::BQ, w)) return;
+  if (u < 0 || !resolve_work(p, units, u, C::BQ, w)) return;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1267,13 +1331,12 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     for (; t < te; ++t) step_i(t, t - tb);
   }
 
-  // ---- split part: this part's record (O / l as T, then m and l per row) for
+  // ---- split part: this part's record (O / l, then m and l per row, all fp32) for
   // merge_kernel
   if (w.split_n > 1) {
-    const int32_t* hdr = n_units;
-    char* const records = (char*)hdr + hdr[3];
-    const int64_t rec_bytes = hdr[4];
-    const int64_t ml_off = (int64_t)C::BQ * D * 2;  // m [BQ] then l [BQ] (fp32)
+    char* const records = (char*)hdr + ldc(hdr, kHdrRecordsOff);
+    const int64_t rec_bytes = ldc(hdr, kHdrRecBytes);
+    const int64_t ml_off = (int64_t)C::BQ * D * 4;  // m [BQ] then l [BQ]
     char* const mine = records + (int64_t)(w.rec0 + w.split_s) * rec_bytes;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -1282,12 +1345,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       const float l = lsum[qb][0];
       const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-      for (int db = 0; db < C::NDB; ++db) {
-        T v4[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v4[r] = (T)(o[db][qb][r] * inv);
-        *(u32x2*)(mine + ((int64_t)row * D + db * 16 + g * 4) * 2) = *(const u32x2*)v4;
-      }
+      for (int db = 0; db < C::NDB; ++db)
+        *(f32x4*)(mine + ((int64_t)row * D + db * 16 + g * 4) * 4) = o[db][qb] * inv;
       if (g == 0) {
         ((float*)(mine + ml_off))[row] = m_i[qb];
         ((float*)(mine + ml_off))[C::BQ + row] = l;
@@ -1345,7 +1404,7 @@ struct MlaRowsCfg {
 
 template <typename T, bool PAGED>
 __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
-    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
+    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ hdr) {
   typedef MlaRowsCfg C;
   typedef typename Mfma<T>::v8 v8;
   constexpr int D = C::D, BK = C::BK;
@@ -1354,8 +1413,11 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   // packed calls use head-packed tiles: 128 consecutive rows of the sequence's H*len
   // (head, position) rows, all heads reading the same latent
   const bool hpack = p.cu_seqlens_q != nullptr;
+  // the grid covers the queue slots (8 * cap workgroups), workgroup w taking entry w / 8
+  // of queue w % 8: a sequence's tiles stay on the XCDs the schedule put them on
+  const int u = hpack ? queue_first(hdr, blockIdx.x) : (int)blockIdx.x;
   WorkItem w;
-  if (!resolve_work(p, units, n_units, C::BQ, w, hpack)) return;
+  if (u < 0 || !resolve_work(p, units, u, C::BQ, w, hpack)) return;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1628,14 +1690,15 @@ FMLM_DEV float4 load4<float>(const float* p) {
 // float4 (a row's lanes cover one contiguous key row).
 template <typename T, int D>
 __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
-    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ n_units) {
+    const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ hdr) {
   typedef SimtCfg<D> C;
   extern __shared__ __align__(16) char smem_raw[];
   float* Kf = (float*)smem_raw;
   float* Vf = Kf + C::BKS * D;
 
+  const int u = p.cu_seqlens_q ? workgroup_unit(hdr) : (int)blockIdx.x;
   WorkItem w;
-  if (!resolve_work(p, units, n_units, C::RPW, w)) return;
+  if (u < 0 || !resolve_work(p, units, u, C::RPW, w)) return;
   const int tid = threadIdx.x;
   const int row = tid / C::TPR;
   const int part = tid % C::TPR;
@@ -1726,8 +1789,9 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
 // ---------------------------------------------------------------------------
 // Split-KV merge: for every split group (query tile (b, h, tile) whose key range was
 // cut into S parts), O = sum_s 2^(m_s - M) l_s O_s / sum_s 2^(m_s - M) l_s with
-// M = max_s m_s, over the parts' records (O_s = part output / l_s as T, m_s in log2
-// units, l_s its row sum).  Grid-stride over groups; 8 columns of a row per thread.
+// M = max_s m_s, over the parts' records (O_s = part output / l_s as fp32, m_s in log2
+// units, l_s its row sum), so the merged row is rounded to the output type once, as an
+// unsplit row is.  Grid-stride over groups; 8 columns of a row per thread.
 // ---------------------------------------------------------------------------
 constexpr int kMergeRows = 128;  // largest split-capable query tile
 
@@ -1736,12 +1800,12 @@ __global__ __launch_bounds__(256) void merge_kernel(const fmlm_attn_params p, in
                                                     const int32_t* __restrict__ header) {
   typedef typename Mfma<T>::v8 v8;
   __shared__ float s_w[kMergeRows][kMaxSplits];  // per row: part weights / their sum
-  const int n_groups = header[1];
-  const int4* groups = (const int4*)((const char*)header + header[2]);
-  const char* records = (const char*)header + header[3];
-  const int64_t rec_bytes = header[4];
+  const int n_groups = header[kHdrGroups];
+  const int4* groups = (const int4*)((const char*)header + header[kHdrGroupsOff]);
+  const char* records = (const char*)header + header[kHdrRecordsOff];
+  const int64_t rec_bytes = header[kHdrRecBytes];
   const int D = p.D;
-  const int64_t ml_off = (int64_t)BQ * D * 2;
+  const int64_t ml_off = (int64_t)BQ * D * 4;
   for (int gi = blockIdx.x; gi < n_groups; gi += gridDim.x) {
     const int4 gr = groups[gi];
     const int b = gr.x, h = gr.y & 0xffff, tile = (int)((uint32_t)gr.y >> 16), S = gr.w;
@@ -1778,18 +1842,22 @@ __global__ __launch_bounds__(256) void merge_kernel(const fmlm_attn_params p, in
     __syncthreads();
     for (int idx = threadIdx.x; idx < qcount * (D / 8); idx += blockDim.x) {
       const int row = idx / (D / 8), c8 = idx - row * (D / 8);
-      const char* src = rec0 + ((int64_t)row * D + c8 * 8) * 2;
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      const char* src = rec0 + ((int64_t)row * D + c8 * 8) * 4;
+      f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
 #pragma unroll 4
       for (int sp = 0; sp < S; ++sp) {
-        const v8 ov = *(const v8*)(src + sp * rec_bytes);
+        const f32x4 x0 = *(const f32x4*)(src + sp * rec_bytes);
+        const f32x4 x1 = *(const f32x4*)(src + sp * rec_bytes + 16);
         const float ws = s_w[row][sp];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += ws * (float)ov[e];
+        a0 += ws * x0;
+        a1 += ws * x1;
       }
       v8 res;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) res[e] = (T)acc[e];
+      for (int e = 0; e < 4; ++e) {
+        res[e] = (T)a0[e];
+        res[4 + e] = (T)a1[e];
+      }
       *(v8*)((char*)p.o + (o_row0 + (int64_t)row * p.o_sn + c8 * 8) * 2) = res;
     }
     __syncthreads();  // s_w is rewritten for the next group
@@ -1818,7 +1886,6 @@ static Launch simt_launch() {
   return Launch{C::RPW, C::NT, C::LDS_BYTES, (const void*)&attn_simt_kernel<T, D>};
 }
 
-// the paged instantiation only for paged contexts, so the contiguous one keeps its code
 template <typename T, int D, int QB, int NW, int BK, int PPB = 0>
 static Launch mfma3_launch(bool paged) {
   typedef Mfma3Cfg<T, D, QB, NW, BK, PPB> C;
@@ -1948,83 +2015,89 @@ static int allow_lds(const Launch& L) {
   return 0;
 }
 
-// Split-KV sizing: the GPU's workgroup slots for this kernel (CUs x resident
-// workgroups), the record capacity and the record size.
+// Resident workgroup slots of a kernel (CUs x workgroups per CU), once per kernel; 0 on
+// a query error.
+static int resident_slots(const Launch& L) {
+  static std::mutex mu;
+  static const void* fns[64];
+  static int slots_of[64];
+  static int n_fns = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_fns; ++i)
+    if (fns[i] == L.fn) return slots_of[i];
+  int dev = 0, cus = 0, per_cu = 0;
+  if (allow_lds(L) != 0 || hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, L.fn, L.threads, L.lds) != hipSuccess)
+    return 0;
+  const int slots = cus * (per_cu > 0 ? per_cu : 1);
+  if (n_fns < 64) {
+    fns[n_fns] = L.fn;
+    slots_of[n_fns++] = slots;
+  }
+  return slots;
+}
+
+// Split-KV sizing: the GPU's workgroup slots for this kernel, the record capacity and
+// the record size.
 struct SplitCfg {
   int slots = 0;
   int rec_cap = 0;        // 0: no split
-  int64_t rec_bytes = 0;  // per record: rows x (D elements + m + l)
+  int64_t rec_bytes = 0;  // per record: rows x (D fp32 + m + l)
 };
 
 static SplitCfg split_cfg(const fmlm_attn_params& p, const Launch& L) {
   SplitCfg sc;
   if (!L.split || !p.cu_seqlens_q) return sc;
-  static std::mutex mu;
-  static const void* fns[64];
-  static int slots_of[64];
-  static int n_fns = 0;
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    for (int i = 0; i < n_fns; ++i)
-      if (fns[i] == L.fn) sc.slots = slots_of[i];
-    if (sc.slots == 0) {
-      int dev = 0, cus = 0, per_cu = 0;
-      if (allow_lds(L) != 0 || hipGetDevice(&dev) != hipSuccess ||
-          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, L.fn, L.threads, L.lds) != hipSuccess)
-        return sc;
-      sc.slots = cus * (per_cu > 0 ? per_cu : 1);
-      if (n_fns < 64) {
-        fns[n_fns] = L.fn;
-        slots_of[n_fns++] = sc.slots;
-      }
-    }
-  }
+  sc.slots = resident_slots(L);
+  if (sc.slots == 0) return sc;
   // every sequence's tiles but its last are full, so there are at least
   // H * (total_q - B*bq) / bq units: when that already fills kSplitRounds rounds, the
   // schedule cannot split (and no records or merge launch are needed)
   const int64_t min_units = (int64_t)p.H * (((int64_t)p.total_q - (int64_t)p.B * L.bq) / L.bq);
   if (min_units >= (int64_t)(kSplitRounds * sc.slots) || L.bq > kMergeRows) return SplitCfg{};
   sc.rec_cap = 3 * sc.slots;
-  const int esz = elem_size(p.dtype);
-  sc.rec_bytes = ((int64_t)L.bq * (p.D * esz + 8) + 15) / 16 * 16;
+  sc.rec_bytes = ((int64_t)L.bq * (p.D * 4 + 8) + 15) / 16 * 16;
   return sc;
 }
 
-// Grid size (1-D): dense units are laid out arithmetically, packed units by the
-// schedule, whose XCD slots are bounded by ceil(total/8) + the largest group (with
-// splits: at most kSplitRounds*slots unsplit units plus rec_cap split parts, a group
-// growing by up to kMaxSplits).  Head-packed units are dealt to XCDs by work, not by
-// count, so one XCD may hold every unit and every split part.
-static int64_t grid_units(const fmlm_attn_params& p, int bq, const SplitCfg& sc, bool hpack = false) {
-  if (!p.cu_seqlens_q) {
-    const int64_t groups = (int64_t)p.B * p.H;
-    return kXcds * ((groups + kXcds - 1) / kXcds) * ((p.N + bq - 1) / bq);
-  }
-  if (hpack) {  // sum over b of ceil(H*L_b/bq) units, and the split parts
-    const int64_t units = ((int64_t)p.H * p.total_q + bq - 1) / bq + p.B + sc.rec_cap;
-    return kXcds * (units + 1);
-  }
-  const int64_t total = (int64_t)p.H * (p.B + p.total_q / bq + 1);
-  const int64_t max_group = (p.N > 0 ? (p.N + bq - 1) / bq : p.total_q / bq + 1) + 1;
-  int64_t g = kXcds * ((total + kXcds - 1) / kXcds + max_group);
-  if (sc.rec_cap > 0) {
-    const int64_t split_total = (int64_t)(kSplitRounds * sc.slots) + sc.rec_cap;
-    const int64_t gs = kXcds * ((split_total + kXcds - 1) / kXcds + kMaxSplits * max_group);
-    g = gs > g ? gs : g;
-  }
-  return g;
+// Units of a dense call: slots of 8 XCDs x ceil(B*H / 8) groups x ceil(N / bq) tiles.
+static int64_t dense_units(const fmlm_attn_params& p, int bq) {
+  return (int64_t)kXcds * (((int64_t)p.B * p.H + kXcds - 1) / kXcds) * ((p.N + bq - 1) / bq);
 }
 
-// Schedule buffer layout (see schedule_kernel): header, units, groups, records.
+// Entries per queue of a packed call: a bound on the launch's units, so that one queue
+// can take all of them whatever the placement.  Sequence b has ceil(L_b / bq) <= L_b / bq
+// + 1 query tiles per head (head-packed: ceil(H L_b / bq) in all); with splits, which
+// happen only below kSplitRounds * slots unsplit units, add every split part.
+static int64_t queue_cap(const fmlm_attn_params& p, int bq, const SplitCfg& sc, bool hpack) {
+  int64_t units = hpack ? ((int64_t)p.H * p.total_q + bq - 1) / bq + p.B
+                        : (int64_t)p.H * (((int64_t)p.total_q + bq - 1) / bq + p.B);
+  if (sc.rec_cap > 0) {
+    const int64_t split_units = (int64_t)(kSplitRounds * sc.slots) + 1 + sc.rec_cap;
+    units = split_units > units ? split_units : units;
+  }
+  return units;
+}
+
+// Grid (one unit per workgroup): a dense call's slots; cap workgroups for a packed call
+// (spares take what overflows a queue's static entries), 8 * cap head-packed.
+static int64_t grid_size(const fmlm_attn_params& p, const Launch& L, const SplitCfg& sc) {
+  if (!p.cu_seqlens_q) return dense_units(p, L.bq);
+  const int64_t cap = queue_cap(p, L.bq, sc, L.hpack);
+  return L.hpack ? kXcds * cap : cap;
+}
+
+// Schedule buffer layout (see schedule_kernel): header, 8 queues, groups, records.
 struct SchedLayout {
-  int64_t units_off, groups_off, records_off, bytes;
+  int64_t cap, units_off, groups_off, records_off, bytes;
 };
 
 static SchedLayout sched_layout(const fmlm_attn_params& p, int bq, const SplitCfg& sc, bool hpack) {
   SchedLayout l;
+  l.cap = queue_cap(p, bq, sc, hpack);
   l.units_off = 256;
-  l.groups_off = l.units_off + grid_units(p, bq, sc, hpack) * (int64_t)sizeof(int4);
+  l.groups_off = l.units_off + kXcds * l.cap * (int64_t)sizeof(int4);
   l.groups_off = (l.groups_off + 255) / 256 * 256;
   l.records_off = l.groups_off + (int64_t)sc.rec_cap * (int64_t)sizeof(int4);
   l.records_off = (l.records_off + 255) / 256 * 256;
@@ -2059,12 +2132,12 @@ static int check_params(const fmlm_attn_params& p) {
 static int launch_schedule(const fmlm_attn_params& p, const Launch& L, const SplitCfg& sc, char* sched,
                            hipStream_t s) {
   const SchedLayout l = sched_layout(p, L.bq, sc, L.hpack);
-  const int64_t cap = grid_units(p, L.bq, sc, L.hpack);
-  // the unit's 16-bit tile field: tiles of N rows, or of H*N (H*total_q) rows head-packed
+  // the unit's 16-bit tile field: tiles of N rows, or of H*N (H*total_q) rows head-packed;
+  // queue entries are addressed with 32-bit indices
   const int64_t rows = L.hpack ? (int64_t)p.H * (p.N > 0 ? p.N : p.total_q) : p.N;
-  if (cap > 0x7fffffff || p.H > 0xffff || (rows + L.bq - 1) / L.bq > 0xffff) return FMLM_E_ARG;
+  if (kXcds * l.cap > 0x7fffffff || p.H > 0xffff || (rows + L.bq - 1) / L.bq > 0xffff) return FMLM_E_ARG;
   int32_t* header = (int32_t*)sched;
-  hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, s, p, L.bq, (int)cap,
+  hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, s, p, L.bq, (int)l.cap,
                      sc.slots, sc.rec_cap, (int4*)(sched + l.units_off), header,
                      (int4*)(sched + l.groups_off), (int)l.groups_off, (int)l.records_off,
                      (int)sc.rec_bytes, (int)L.hpack);
@@ -2079,28 +2152,28 @@ static int launch_attention(const fmlm_attn_params& p, const Launch& L, const Sp
   int rc = allow_lds(L);
   if (rc) return rc;
   int4* units = nullptr;
-  int32_t* n_units = nullptr;
+  int32_t* header = nullptr;
   if (p.cu_seqlens_q) {
-    n_units = (int32_t*)sched;
+    header = (int32_t*)sched;
     units = (int4*)(sched + 256);
     if (build) {
       rc = launch_schedule(p, L, sc, sched, s);
       if (rc) return rc;
     }
   }
-  const int64_t gx = grid_units(p, L.bq, sc, L.hpack);
+  const int64_t gx = grid_size(p, L, sc);
   if (gx <= 0) return 0;
   if (gx > 0x7fffffff) return FMLM_E_ARG;
   fmlm_attn_params pc = p;
-  void* args[] = {(void*)&pc, (void*)&units, (void*)&n_units};
+  void* args[] = {(void*)&pc, (void*)&units, (void*)&header};
   hipError_t e = hipLaunchKernel(L.fn, dim3((unsigned)gx), dim3(L.threads), args, (size_t)L.lds, s);
   if (e != hipSuccess) return (int)e;
   if (sc.rec_cap > 0) {  // split groups (if the schedule made any) are merged here
     const dim3 mg((unsigned)(sc.rec_cap < 1024 ? sc.rec_cap : 1024));
     if (p.dtype == FMLM_DTYPE_BF16)
-      hipLaunchKernelGGL(merge_kernel<bf16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
+      hipLaunchKernelGGL(merge_kernel<bf16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)header);
     else
-      hipLaunchKernelGGL(merge_kernel<f16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)n_units);
+      hipLaunchKernelGGL(merge_kernel<f16>, mg, dim3(256), 0, s, p, L.bq, (const int32_t*)header);
   }
   return launch_status();
 }

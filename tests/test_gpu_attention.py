@@ -506,6 +506,32 @@ def test_split_kv_long_key_ranges(dtype, D, mode, device):
     # the cached schedule (and its split records) is reused: same result again
     out2 = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache if not prefill else InferenceCache(), 0, **kw)
     assert torch.equal(out, out2)
+    # The split parts keep O / l in fp32, so a split row is rounded to the output type once,
+    # as an unsplit row is: its error stays within half an output ulp of the same heads
+    # computed unsplit (the inputs repeated along the head axis until the schedule has
+    # units enough not to split).  The two differ by more than summation order: each part
+    # rounds its P against its own running maximum.
+    got = unpack_from_kernel(out, meta, H).float().cpu().numpy().astype(np.float64)
+    err_split = float(np.abs(got - ref).max())
+    R = 32
+    while True:
+        qR, kR, vR = (x.repeat(1, R, 1, 1) for x in (q, k, v))
+        cacheR = InferenceCache()
+        if not prefill:
+            hv = lambda t: t.view(H, Tc, D).repeat(R, 1, 1).reshape(H * R * Tc, D)  # noqa: E731
+            cacheR.prefill_kv_cache(0, k_cache=hv(kc), v_cache=hv(vc), total_context_len=Tc, cu_seqlens_kv=cu_kv.to(device),
+                                    context_batch_size=cbs if mode == "shared_ctx" else B, is_mla=False,
+                                    num_heads=H * R, head_dim=D)
+        metaR = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+        outR = flash_attn_mlm_compressed(qR, kR, vR, H * R, metaR, scale, cacheR, 0, **kw)
+        (schedR,) = metaR.kernel_schedules.values()
+        if int(schedR[:8].view(torch.int32)[1]) == 0:
+            break
+        R *= 2
+    unsplit = unpack_from_kernel(outR, metaR, H * R)[:, :H].float().cpu().numpy().astype(np.float64)
+    err_unsplit = float(np.abs(unsplit - ref).max())
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    assert err_split <= err_unsplit + ulp / 2 * float(np.abs(ref).max()), (err_split, err_unsplit)
 
 
 def test_cached_schedule_per_head_count_and_mode(device):
@@ -528,19 +554,21 @@ def test_cached_schedule_per_head_count_and_mode(device):
 
 
 def _schedule_units(sched):
-    """Decoded work list of a cached schedule buffer: (slot, b, h, tile, s, S) per non-idle
-    unit (header word 0 = slots; int4 units from byte 256: b, h | tile << 16, record,
-    split word)."""
+    """Decoded work list of a cached schedule buffer: (xcd, b, h, tile, s, S) per unit.
+    Header words: 5 = entries per queue (cap), 8 + x = length of queue x (the units meant
+    for XCD x); units of 4 int32 from byte 256, queue x at entry x * cap: b,
+    h | tile << 16, record, split word."""
     words = sched.view(torch.int32).cpu()
-    n = int(words[0])
-    u = words[64:64 + 4 * n].view(n, 4).tolist()
+    cap = int(words[5])
     out = []
-    for slot, (b, ht, _, w) in enumerate(u):
-        if b < 0:
-            continue
-        S = ((w >> 25) & 15) + 1 if w >= 0 else 1
-        s = (w >> 20) & 31 if w >= 0 else 0
-        out.append((slot, b, ht & 0xFFFF, ht >> 16, s, S))
+    for x in range(8):
+        n = int(words[8 + x])
+        assert 0 <= n <= cap
+        base = 64 + 4 * x * cap
+        for b, ht, _, w in words[base:base + 4 * n].view(n, 4).tolist():
+            S = ((w >> 25) & 15) + 1 if w >= 0 else 1
+            s = (w >> 20) & 31 if w >= 0 else 0
+            out.append((x, b, ht & 0xFFFF, ht >> 16, s, S))
     return out
 
 
@@ -554,8 +582,8 @@ def _schedule_units(sched):
 ])
 def test_schedule_places_every_tile_once(H, lengths, causal, device):
     """The work list holds every (sequence, head, 128-row query tile) once, each split into
-    its S parts exactly once, and keeps every head on ceil(8 / H) XCDs or one more (slot %
-    8; at most two from 8 heads up); the result matches the oracle."""
+    its S parts exactly once, and keeps every head on ceil(8 / H) XCDs or one more (its
+    queues; at most two from 8 heads up); the result matches the oracle."""
     torch.manual_seed(7200 + H)
     B, N, D = len(lengths), max(lengths), 64
     scale = 1.0 / math.sqrt(D)
@@ -582,8 +610,32 @@ def test_schedule_places_every_tile_once(H, lengths, causal, device):
         (S,) = S
         assert {s for (k_, s) in seen if k_ == key} == set(range(S))
     for h in range(H):
-        xcds = {slot % 8 for slot, _, hh, _, _, _ in units if hh == h}
+        xcds = {x for x, _, hh, _, _, _ in units if hh == h}
         assert len(xcds) <= (8 + H - 1) // H + 1, (h, xcds)
+
+
+def test_schedule_overflow_taken_by_spares(device):
+    """One head, a sequence of 60 query tiles beside seven of one row: the long sequence's
+    queue (its tiles' split parts) holds more entries than its XCD has workgroups in the
+    launch (cap of them in all), so spare workgroups of the other XCDs take the overflow by
+    rank; every row matches the oracle."""
+    torch.manual_seed(7290)
+    H, lengths = 1, [60 * 128, 1, 1, 1, 1, 1, 1, 1]
+    B, N, D = len(lengths), max(lengths), 64
+    scale = 1.0 / math.sqrt(D)
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, [200], device, torch.bfloat16, cbs=1)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=True,
+                                    context_batch_size=1)
+    (sched,) = meta.kernel_schedules.values()
+    words = sched.view(torch.int32).cpu()
+    G = int(words[5])  # workgroups of the launch: the queue capacity
+    lens = [int(words[8 + x]) for x in range(8)]
+    overflow = sum(max(n - (G - x + 7) // 8, 0) for x, n in enumerate(lens))
+    assert overflow > 0, (G, lens)
+    ref = _packed_oracle(q, k, v, lengths, scale, causal=True, k_cache=kc, v_cache=vc, cu_kv=cu_kv, cbs=1, Tc=Tc)
+    _close(unpack_from_kernel(out, meta, H), ref)
 
 
 @pytest.mark.parametrize("lengths,ctx_lengths", [
@@ -594,7 +646,7 @@ def test_schedule_places_every_tile_once(H, lengths, causal, device):
 def test_mla_schedule_keeps_sequences_together(lengths, ctx_lengths, device):
     """Head-packed tiles (the 512-wide latent, 128 of a sequence's H*L (head, row) rows per
     tile): every (sequence, tile) once, in all its split parts; a sequence's tiles sit on as
-    few XCDs (slot % 8) as its share of the work needs, plus one at each cut; and the XCDs'
+    few XCDs (queues) as its share of the work needs, plus one at each cut; and the XCDs'
     work (query tiles x key tiles) differs from an equal share by at most one tile's."""
     torch.manual_seed(7300 + len(lengths))
     B, H, N, D = len(lengths), 16, max(lengths), 512
@@ -632,6 +684,48 @@ def test_mla_schedule_keeps_sequences_together(lengths, ctx_lengths, device):
         xcds = {x for ((bb, _), _), (_, x) in seen.items() if bb == b}
         assert len(xcds) <= (8 * work[b]) // W + 2, (b, xcds)
     assert max(abs(w - W / 8) for w in per_xcd) <= max(kt), per_xcd
+
+
+@pytest.mark.parametrize("seed", [7, 8])
+def test_schedule_unbalanced_heads_every_tile(seed, device):
+    """A shape whose by-head placement puts more units on one XCD than an even share (4
+    heads, 64 sequences of 256-4096 query rows over 0-8192 context rows, no split): every
+    (sequence, head, query tile) is in the work list once, and every row of the output
+    matches a per-sequence fp32 attention on the GPU."""
+    g = torch.Generator().manual_seed(seed)
+    B, H, D = 64, 4, 64
+    lengths = torch.randint(256, 4097, (B,), generator=g).tolist()
+    ctx = torch.randint(0, 8193, (B,), generator=g).tolist()
+    N = max(lengths)
+    torch.manual_seed(seed)
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, False, ctx, device, torch.bfloat16)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    scale = 1.0 / math.sqrt(D)
+    from flash_mlm.host.host import tile_config
+
+    with tile_config(1):  # 128-row query tiles
+        out = unpack_from_kernel(flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64), meta, H)
+    (sched,) = meta.kernel_schedules.values()
+    units = _schedule_units(sched)
+    assert all(S == 1 for *_, S in units)
+    got = sorted((b, h, t) for _, b, h, t, _, _ in units)
+    want = sorted((b, h, t) for b, L in enumerate(lengths) for h in range(H) for t in range((L + 127) // 128))
+    assert got == want
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        kcv, vcv = kc.view(H, Tc, D), vc.view(H, Tc, D)
+        for b, L in enumerate(lengths):
+            c0, c1 = int(cu_kv[b]), int(cu_kv[b + 1])
+            K = torch.cat([kcv[:, c0:c1].float(), k[b, :, :L].float()], dim=1)
+            V = torch.cat([vcv[:, c0:c1].float(), v[b, :, :L].float()], dim=1)
+            s = torch.matmul(q[b, :, :L].float(), K.transpose(1, 2).contiguous()) * scale
+            ref = torch.matmul(torch.softmax(s, dim=-1), V)
+            err = (out[b, :, :L].float() - ref).abs() - (ATOL + RTOL * ref.abs())
+            assert float(err.max()) <= 0, (b, float(err.max()))
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
