@@ -22,7 +22,8 @@ class PackMetadata:
     optional host copy of ``cu_seqlens`` filled by :func:`build_pack_metadata`; it lets
     the launchers size padded workspaces without a device-to-host synchronisation.
     ``kernel_schedules`` caches the attention kernel's device work lists built from
-    ``cu_seqlens`` (one per kernel tile size), so repeated layers skip rebuilding them.
+    ``cu_seqlens`` (one per kernel tile size), so repeated layers skip rebuilding them;
+    ``launch_memo`` the parameter blocks of earlier compressed calls on this metadata.
     """
 
     B: int
@@ -36,6 +37,7 @@ class PackMetadata:
     q_tile_starts_q: torch.Tensor
     cu_seqlens_host: tuple[int, ...] | None = field(default=None, repr=False, compare=False)
     kernel_schedules: dict = field(default_factory=dict, repr=False, compare=False)
+    launch_memo: dict = field(default_factory=dict, repr=False, compare=False)
 
     def host_cu_seqlens(self) -> tuple[int, ...]:
         if self.cu_seqlens_host is None:

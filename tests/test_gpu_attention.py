@@ -203,6 +203,53 @@ def _context_cache(B, H, D, is_mla, ctx_lengths, device, dtype=torch.float16, cb
     return cache, k_cache, v_cache, cu_kv, Tc
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("is_mla", [False, True])
+def test_repeated_calls_follow_their_inputs(is_mla, causal, device):
+    """A repeated call with the same tensors reuses the first call's launch parameters
+    (the launch memo): it must still read the current contents of q/k/v (changed in
+    place), a context replaced by a new prefill, and, with causal_query_seq_attn, re-pack
+    this call's K/V; a call on new tensors of the same shape must not reuse them."""
+    torch.manual_seed(7400 + 2 * is_mla + causal)
+    lengths, ctx = [70, 1, 130, 0, 64], [40, 0, 7, 129, 64]
+    B, H, N, D = len(lengths), 3, max(lengths), 64
+    scale = 0.125
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, is_mla, ctx, device, torch.bfloat16)
+
+    def run():
+        out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, is_mla=is_mla, block_n=64,
+                                        causal_query_seq_attn=causal)
+        ref = _packed_oracle(q, k, v, lengths, scale, is_mla=is_mla, causal=causal, k_cache=kc,
+                             v_cache=None if is_mla else vc, cu_kv=cu_kv, cbs=B, Tc=Tc)
+        _close(unpack_from_kernel(out, meta, H), ref)
+
+    run()
+    run()
+    assert len(meta.launch_memo) == 1
+    for t in (q, k, v):
+        t.copy_(_randn(t.shape, device, torch.bfloat16))
+        run()
+    cache, kc, vc, cu_kv, Tc = _context_cache(B, H, D, is_mla, [x + 3 for x in ctx], device, torch.bfloat16)
+    run()
+    q, k, v = (_randn((B, H, N, D), device, torch.bfloat16) for _ in range(3))
+    run()
+    # dense: the same, on the module-level memo
+    cache, kc, vc, _, Tc = _context_cache(B, H, D, is_mla, [16] * B, device, torch.bfloat16)
+
+    def run_dense():
+        out = flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0, is_mla=is_mla)
+        ref = ar.mlm_attention_dense(_np(q), _np(k), _np(v), scale, k_cache=_np(kc),
+                                     v_cache=None if is_mla else _np(vc), context_len=16, context_batch_size=B,
+                                     is_mla=is_mla)
+        _close(out, ref)
+
+    run_dense()
+    q.copy_(_randn(q.shape, device, torch.bfloat16))
+    run_dense()
+
+
 @pytest.mark.parametrize("is_mla", [False, True])
 def test_compressed_matches_reference_with_cache(is_mla, device):
     torch.manual_seed(1)
