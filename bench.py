@@ -8,7 +8,9 @@ HBM: for the default workload (packed varlen fp16 with a
 full-batch cached context) that is flash_attn_mlm_compressed + unpack_from_kernel
 (pack metadata is built once and memoised, as in the reference's own benchmark).
 Prints one JSON line: effective attention TFLOP/s (padding excluded, formula
-4*H*D*sum_b Lq_b*(Lctx_b + Lmain_b)), ms per step, the host time of one API call, the
+4*H*D*sum_b Lq_b*(Lctx_b + Lmain_b)), ms per step (the K timed steps run after the
+kernel-timing loops, at settled clocks; the same steps are then run once more with HIP
+events around each, "step_device_ms"), the host time of one API call, the
 attention kernel's roofline fraction against the MI355X dense fp16/bf16 MFMA peak
 (kernel time: mean of HIP-event timings on its launch stream over back-to-back launches;
 also with L2/MALL flushed before each launch), the kernel's HBM bytes per launch from two
@@ -286,8 +288,9 @@ def _median(xs):
 def _time_steps(case: "Case", steps: int, warmup: int) -> tuple[float, float, float]:
     """(ms per step, median host us of the attention API call, median host us of a whole
     step): K steps back to back between two device synchronisations.  The host times are
-    what the Python API costs the caller per call (validation, parameter block, launch);
-    the launches are asynchronous, so they overlap the GPU's work."""
+    what the Python API costs the caller per call (the launch memo's lookup, the output
+    allocation, the launch); the launches are asynchronous, so they overlap the GPU's
+    work."""
     for _ in range(warmup):
         case.step()
     torch.cuda.synchronize()
@@ -304,6 +307,22 @@ def _time_steps(case: "Case", steps: int, warmup: int) -> tuple[float, float, fl
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     return ms, _median(call_us), _median(step_us)
+
+
+def _step_events(case: "Case", steps: int) -> dict:
+    """Device time of each of `steps` steps run as the timed ones are (after them, the
+    clocks already settled), from HIP events on the current stream (the one the steps
+    launch on) around each step: mean, median, first and maximum in ms."""
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for e0, e1 in events:
+        e0.record()
+        case.step()
+        e1.record()
+    torch.cuda.synchronize()
+    t = [e0.elapsed_time(e1) for e0, e1 in events]
+    return {"mean": round(sum(t) / len(t), 5), "median": round(_median(t), 5), "first": round(t[0], 5),
+            "max": round(max(t), 5)}
 
 
 def _launch_stream(attention):
@@ -417,7 +436,7 @@ def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s
         files = list(out.rglob("*counter_collection.csv"))
         if not files:
             raise RuntimeError(f"rocprofv3 --pmc {counter} wrote no counter file")
-        vals: dict[str, list[float]] = {}
+        rows: list[tuple[int, str, float]] = []  # (dispatch id, kernel class, KiB)
         for f in files:
             with open(f, newline="") as fh:
                 for row in csv.DictReader(fh):
@@ -425,15 +444,21 @@ def _counter_pass(counter: str, cfg: int, variant: str, launches: int, timeout_s
                         continue
                     kind = _kernel_class(row["Kernel_Name"])
                     if kind is not None:
-                        vals.setdefault(kind, []).append(float(row["Counter_Value"]))
-        attn, copies = vals.get("attn", []), vals.get("copy", [])
+                        rows.append((int(row["Dispatch_Id"]), kind, float(row["Counter_Value"])))
+        rows.sort()
+        attn = [v for _, kind, v in rows if kind == "attn"]
+        copies = [v for _, kind, v in rows if kind == "copy"]
         if len(attn) < launches or not copies:
             raise RuntimeError(f"rocprofv3 --pmc {counter}: {len(attn)} attention dispatches, "
                                f"{len(copies)} copies")
         res = {"attn": sum(attn[-launches:]) / launches, "copy": max(copies)}
+        # the copy kernels' profiled calls come after the last attention launch; earlier
+        # dispatches (the pack the case's setup runs for causal_query_seq_attn) are not them
+        last_attn = max(i for i, kind, _ in rows if kind == "attn")
         for kind in ("pack", "unpack", "kv_append"):
-            if kind in vals:
-                res[kind] = sum(vals[kind])
+            vals = [v for i, k, v in rows if k == kind and i > last_attn]
+            if vals:
+                res[kind] = sum(vals)
         return res
     finally:
         shutil.rmtree(out, ignore_errors=True)
@@ -669,15 +694,19 @@ def main() -> None:
         print(f"[bench] profiled {args.steps} attention launches and the copy kernels", file=sys.stderr, flush=True)
         return
 
-    ms, call_us, step_us = _time_steps(case, args.steps, args.warmup)
-    print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step; host {call_us:.1f} us per attention API call, "
-          f"{step_us:.1f} us per step (medians)", file=sys.stderr, flush=True)
+    # the kernel-timing loops first: the timed steps then run at settled clocks, whatever
+    # the GPU did while this process built its inputs
     kms, kmed = _kernel_device_ms(case.attention, args.kernel_reps)
     print(f"[bench] attention launch on the device: mean {kms:.4f} ms, median {kmed:.4f} ms over "
           f"{args.kernel_reps} back-to-back launches", file=sys.stderr, flush=True)
     fms, fmean = _kernel_ms(case.attention, args.kernel_reps)
     print(f"[bench] attention kernel with cold caches: median {fms:.4f} ms, mean {fmean:.4f} ms over "
           f"{args.kernel_reps} flushed launches", file=sys.stderr, flush=True)
+    ms, call_us, step_us = _time_steps(case, args.steps, args.warmup)
+    print(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step; host {call_us:.1f} us per attention API call, "
+          f"{step_us:.1f} us per step (medians)", file=sys.stderr, flush=True)
+    step_ev = _step_events(case, args.steps)
+    print(f"[bench] the same steps with HIP events around each: {step_ev}", file=sys.stderr, flush=True)
 
     F = case.flops
     value = F / (ms * 1e-3) / 1e12
@@ -731,6 +760,7 @@ def main() -> None:
         "ms_per_step": round(ms, 5),
         "host_us_per_call": round(call_us, 2),
         "host_us_per_step": round(step_us, 2),
+        "step_device_ms": step_ev,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
