@@ -774,8 +774,9 @@ struct PageWindow {
   int first;  // first tile of the window
 };
 FMLM_DEV void page_window_reset(PageWindow& w) { w.first = -(1 << 30); }
-// first row of tile `tile` of a paged segment (page ids clamped to the pool)
-FMLM_DEV const char* page_row0(const KvSeg& s, const char* base, int tile, PageWindow& w) {
+// byte offset of tile `tile`'s page from the paged segment's page 0 (page ids clamped to
+// the pool)
+FMLM_DEV int64_t page_offset(const KvSeg& s, int tile, PageWindow& w) {
   tile = __builtin_amdgcn_readfirstlane(tile);
   if ((unsigned)(tile - w.first) >= 64u) {
     w.first = tile;
@@ -786,7 +787,11 @@ FMLM_DEV const char* page_row0(const KvSeg& s, const char* base, int tile, PageW
   }
   int pg = __builtin_amdgcn_readlane(w.ids, tile - w.first);
   pg = min(max(pg, 0), max(s.npool - 1, 0));
-  return base + (int64_t)pg * s.page_elems * 2;
+  return (int64_t)pg * s.page_elems * 2;
+}
+// first row of tile `tile` of a paged segment
+FMLM_DEV const char* page_row0(const KvSeg& s, const char* base, int tile, PageWindow& w) {
+  return base + page_offset(s, tile, w);
 }
 
 // walks the key tiles of a work item for the direct loads (see attn_mfma3_kernel)
@@ -796,6 +801,19 @@ struct KeyCursor {
   uint32_t rowb;
   int left, seg, tile;
   PageWindow pw;     // paged segment: page ids of the tiles around `tile`
+};
+
+// the single-group schedule's walk: K and V of a key tile are loaded together, so one
+// position (segment, keys left, tile, page) serves both tensors
+struct PairCursor {
+  const char* pk;  // row 0 of the current K / V tile
+  const char* pv;
+  const char* bk;  // the segment's first K / V row (paged: row 0 of page 0 of the pool)
+  const char* bv;
+  uint32_t rowk, rowv;  // row pitches in bytes
+  int left, seg, tile;
+  bool full_pitch;  // both pitches equal the main K pitch of the precomputed lane offsets
+  PageWindow pw;
 };
 
 // PPB > 0: the ping-pong schedule (8 waves in two groups of 4, one half-step apart) with
@@ -909,7 +927,9 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     sbase[qb] = 0.f;
   }
   const bool wave_active = wave * QB * 16 < w.qcount;
-  KeyCursor kcur, vcur;
+  KeyCursor kcur, vcur;  // ping-pong schedule
+  PairCursor pc;         // single-group schedule
+  const uint32_t kl = lds_addr(kbuf), vl = lds_addr(vbuf);
 
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
@@ -965,6 +985,78 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   uint32_t oc_k[C::NPW], oc_v[C::NPW];
   lane_offsets(oc_rowb, BK, false, oc_k);
   lane_offsets(oc_rowb, BK, true, oc_v);
+  // the paired cursor at the start of segment sg / on key tile t
+  auto pair_seg = [&](PairCursor& cr, int sg) {
+    const KvSeg& sgm = w.seg[sg];
+    cr.seg = sg;
+    cr.tile = 0;
+    cr.left = __builtin_amdgcn_readfirstlane(sgm.n);
+    cr.rowk = __builtin_amdgcn_readfirstlane((uint32_t)sgm.ksn * 2u);
+    cr.rowv = __builtin_amdgcn_readfirstlane((uint32_t)sgm.vsn * 2u);
+    cr.full_pitch = cr.rowk == oc_rowb && cr.rowv == oc_rowb;
+    cr.bk = uniform_ptr(sgm.k + sgm.kbase * 2);
+    cr.bv = uniform_ptr(sgm.v + sgm.vbase * 2);
+    cr.pk = cr.bk;
+    cr.pv = cr.bv;
+    page_window_reset(cr.pw);
+  };
+  // paged context tile `tile`: the page of K and V from one table read
+  auto pair_page = [&](PairCursor& cr) {
+    if constexpr (PAGED) {
+      const int64_t off = page_offset(w.seg[0], cr.tile, cr.pw);
+      cr.pk = uniform_ptr(cr.bk + off);
+      cr.pv = uniform_ptr(cr.bv + off);
+    }
+  };
+  auto pair_seek = [&](PairCursor& cr, int t) {
+    const int sg = t < nt0 ? 0 : 1;
+    pair_seg(cr, sg);
+    const int skip = sg == 0 ? t : t - nt0;
+    cr.left -= skip * BK;
+    cr.tile = skip;
+    if (PAGED && sg == 0 && ctx_paged) {
+      if (cr.left > 0) pair_page(cr);
+    } else {
+      cr.pk += (size_t)skip * BK * cr.rowk;
+      cr.pv += (size_t)skip * BK * cr.rowv;
+    }
+  };
+  // load the cursor's K tile into LDS byte address kdst and its V tile into vdst (K's loads
+  // issued first), then advance to the next tile
+  auto fetch_pair = [&](PairCursor& cr, uint32_t kdst, uint32_t vdst) {
+    uint32_t ok[C::NPW], ov[C::NPW];
+    if (cr.left >= BK && cr.full_pitch) {
+#pragma unroll
+      for (int j = 0; j < C::NPW; ++j) {
+        ok[j] = oc_k[j];
+        ov[j] = oc_v[j];
+      }
+    } else {
+      lane_offsets(cr.rowk, cr.left - 1, false, ok);
+      lane_offsets(cr.rowv, cr.left - 1, true, ov);
+    }
+#pragma unroll
+    for (int j = 0; j < C::NPW; ++j) {
+      const int i = wave + j * NW;
+      if (C::NINST % NW == 0 || i < C::NINST)
+        dma16_sbase(cr.pk, ok[j], __builtin_amdgcn_readfirstlane(kdst + i * 1024));
+    }
+#pragma unroll
+    for (int j = 0; j < C::NPW; ++j) {
+      const int i = wave + j * NW;
+      if (C::NINST % NW == 0 || i < C::NINST)
+        dma16_sbase(cr.pv, ov[j], __builtin_amdgcn_readfirstlane(vdst + i * 1024));
+    }
+    cr.left -= BK;
+    cr.tile += 1;
+    if (PAGED && cr.seg == 0 && ctx_paged) {  // one page per context tile
+      if (cr.left > 0) pair_page(cr);
+    } else {
+      cr.pk += (size_t)BK * cr.rowk;
+      cr.pv += (size_t)BK * cr.rowv;
+    }
+    if (cr.left <= 0 && cr.seg == 0 && w.seg[1].n > 0) pair_seg(cr, 1);
+  };
   // load the cursor's tile into LDS dst and advance to the next tile
   auto fetch = [&](Cursor& cr, char* dst, bool is_v) {
     const uint32_t lds0 = lds_addr(dst);
@@ -1178,9 +1270,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   // computes sn = S(t+1) from the K tile at byte offset kn and its maxima, consumes V(t) at
   // byte offset vt, refills kdst with K(t+2) and vdst with V(t+2).
   auto step = [&](int t, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB], float (&mx)[QB],
-                  uint32_t kn, uint32_t vt, char* kdst, char* vdst) {
-    if (t + 2 < te) fetch(kcur, kdst, false);
-    if (t + 2 < te) fetch(vcur, vdst, true);
+                  uint32_t kn, uint32_t vt, uint32_t kdst, uint32_t vdst) {
+    if (t + 2 < te) fetch_pair(pc, kdst, vdst);
     if (!wave_active) {  // every query row of this wave is padding: loads and barriers only
       vwait(t);
       __syncthreads();
@@ -1297,12 +1388,9 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     }
   } else {
     if (te > tb) {
-      cursor_seek(kcur, tb, false);
-      cursor_seek(vcur, tb, true);
-      fetch(kcur, kbuf, false);
-      fetch(vcur, vbuf, true);
-      if (te - tb > 1) fetch(kcur, kbuf + C::TILEB, false);
-      if (te - tb > 1) fetch(vcur, vbuf + C::TILEB, true);
+      pair_seek(pc, tb);
+      fetch_pair(pc, kl, vl);
+      if (te - tb > 1) fetch_pair(pc, kl + C::TILEB, vl + C::TILEB);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (wave_active) {
@@ -1318,7 +1406,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       const int cur = (i & 1) * C::TILEB, nxt = C::TILEB - cur;
       const int v3 = i % 3;
       const int vc = v3 * C::TILEB, vd = (v3 == 0 ? 2 : v3 - 1) * C::TILEB;
-      step(t, sa, sb, mx, nxt, vc, kbuf + cur, vbuf + vd);
+      step(t, sa, sb, mx, nxt, vc, kl + cur, vl + vd);
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb)
 #pragma unroll
