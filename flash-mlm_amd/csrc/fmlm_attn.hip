@@ -1181,7 +1181,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   constexpr int NP = C::NKB * QB * 2;    // exp pairs
   constexpr int NMS = C::NKB * QB + QB;  // row-max steps
   u32x4 pf[C::NKS][QB];  // P(t) as packed pairs, the B operand of P V
-  float mpart[QB];
+  float mpart[QB], mhold[QB];
   auto run_slots = [&](auto s0c, auto s1c, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB],
                        float (&mx)[QB], uint32_t kn, uint32_t vt) {
     constexpr int S0 = decltype(s0c)::value, S1 = decltype(s1c)::value;
@@ -1220,8 +1220,16 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
         const int qb = k / C::NKB, kb = k % C::NKB;
         pin(sn[kb][qb]);
         const f32x4 x = sn[kb][qb];
-        const float m4 = vmax(vmax(x[0], x[1]), vmax(x[2], x[3]));
-        mpart[qb] = kb == 0 ? m4 : vmax(mpart[qb], m4);
+        // one running max3 chain over the 4 * NKB values of the row block, a value held
+        // back per block so that every step folds two new values (8 ops at NKB = 4)
+        if (kb == 0) {
+          mpart[qb] = vmax(vmax(x[0], x[1]), x[2]);
+        } else {
+          mpart[qb] = vmax(vmax(mpart[qb], mhold[qb]), x[0]);
+          mpart[qb] = vmax(vmax(mpart[qb], x[1]), x[2]);
+        }
+        mhold[qb] = x[3];
+        if (kb == C::NKB - 1) mpart[qb] = vmax(mpart[qb], mhold[qb]);
         pin(mpart[qb]);
       } else {
         const int qb = k - C::NKB * QB;
