@@ -397,6 +397,8 @@ def _kernel_class(name: str) -> str | None:
         return "pack"
     if "fmlm::kv_append_kernel" in name:
         return "kv_append"
+    if "bwd" in name:
+        return "bwd"
     if "attn_" in name and "schedule" not in name:
         return "attn"
     return None
@@ -573,6 +575,27 @@ def hbm_kernels(case: Case, reps: int = 30, traffic: dict | None = None) -> dict
     return out
 
 
+def _backward_call(case: Case):
+    """(fmlm_attn_bwd on this workload's prepared call: a callable, the gradient block and
+    the tensors it points to), or None without a prepared call.  Runs the forward once
+    first: the backward reads its output."""
+    from flash_mlm import _lib
+    from flash_mlm.host import host as hh
+
+    plan = case.attention
+    if plan is None:
+        return None
+    plan()
+    out = plan.keep[1]
+    dout = torch.randn(out.shape, device=out.device).to(out.dtype)
+    g, keep = hh._backward_args(plan, out, dout, want_ctx=True)
+
+    def call():
+        _lib.check(plan.lib.fmlm_attn_bwd(plan.params, g, plan.stream), "fmlm_attn_bwd")
+
+    return call, g, (keep, out, dout)
+
+
 def backward_kernels(case: Case, reps: int = 20) -> dict | None:
     """fmlm_attn_bwd (the dq kernel, then the dK/dV kernels of the main keys and of the
     context) on this workload's prepared call, gradients of q, k, v and of the cached
@@ -580,17 +603,11 @@ def backward_kernels(case: Case, reps: int = 20) -> dict | None:
     Effective work = 2.5x the forward's FLOPs (the products dP = dO V^T, dV = P^T dO,
     dq = dS K, dK = dS^T q besides S = q K^T), padding excluded; the kernels also
     recompute S twice for dq (the row statistics, then dS), which is not counted."""
-    from flash_mlm import _lib
-    from flash_mlm.host import host as hh
-
-    plan = case.attention
-    if plan is None:
+    bc = _backward_call(case)
+    if bc is None:
         return None
-    plan()  # the forward output the backward reads
-    out = plan.keep[1]
-    dout = torch.randn(out.shape, device=out.device).to(out.dtype)
-    g, keep = hh._backward_args(plan, out, dout, want_ctx=True)
-    ms = _event_ms(lambda: _lib.check(plan.lib.fmlm_attn_bwd(plan.params, g, plan.stream), "fmlm_attn_bwd"), reps)
+    call, g, _keep = bc
+    ms = _event_ms(call, reps)
     F = 2.5 * case.flops
     peak = MFMA_PEAK_TFLOPS[case.dtype]
     return {"ms": round(ms, 5), "effective_gflop": round(F / 1e9, 4), "tflops": round(F / (ms * 1e-3) / 1e12, 3),
@@ -632,8 +649,8 @@ def main() -> None:
         "--profile",
         action="store_true",
         help="profiling driver for rocprofv3: one 256 MiB device copy (calibrates the HBM byte "
-        "counters), --warmup attention launches, then --steps bare attention launches back to back "
-        "and one call of each copy kernel; prints no JSON line",
+        "counters), --warmup attention launches, then --steps bare attention launches back to back, "
+        "one call of each copy kernel and --steps backward launches; prints no JSON line",
     )
     args = ap.parse_args()
     query_lens = tuple(int(x) for x in args.query_lens.split(":")) if args.query_lens else None
@@ -681,6 +698,9 @@ def main() -> None:
         torch.cuda.synchronize()
         dst.copy_(src)  # 256 MiB read + 256 MiB write
         torch.cuda.synchronize()
+        # the backward's arguments (this runs the forward once, before the launches below, so
+        # that the copy kernels still follow the last attention launch)
+        bc = _backward_call(case)
         for _ in range(args.warmup):  # as the timed bench: the clocks settle first
             case.attention()
         torch.cuda.synchronize()
@@ -691,7 +711,13 @@ def main() -> None:
         for name, (fn, _, _) in copy_kernel_calls(case).items():
             fn()
             torch.cuda.synchronize()
-        print(f"[bench] profiled {args.steps} attention launches and the copy kernels", file=sys.stderr, flush=True)
+        # then --steps backward launches (the counter passes of the backward kernels)
+        if bc is not None:
+            for _ in range(args.steps):
+                bc[0]()
+            torch.cuda.synchronize()
+        print(f"[bench] profiled {args.steps} attention launches, the copy kernels and {args.steps} backward "
+              "launches", file=sys.stderr, flush=True)
         return
 
     # the kernel-timing loops first: the timed steps then run at settled clocks, whatever
