@@ -806,12 +806,13 @@ struct KeyCursor {
 // the single-group schedule's walk: K and V of a key tile are loaded together, so one
 // position (segment, keys left, tile, page) serves both tensors
 struct PairCursor {
-  const char* pk;  // row 0 of the current K / V tile
+  const char* pk;  // row 0 of the next K / V tile to load
   const char* pv;
   const char* bk;  // the segment's first K / V row (paged: row 0 of page 0 of the pool)
   const char* bv;
+  int64_t stk, stv;     // bytes from one tile's row 0 to the next's
   uint32_t rowk, rowv;  // row pitches in bytes
-  int left, seg, tile;
+  int ft;               // the next tile to load (index over both segments)
   bool full_pitch;  // both pitches equal the main K pitch of the precomputed lane offsets
   PageWindow pw;
 };
@@ -929,7 +930,10 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   const bool wave_active = wave * QB * 16 < w.qcount;
   KeyCursor kcur, vcur;  // ping-pong schedule
   PairCursor pc;         // single-group schedule
-  const uint32_t kl = lds_addr(kbuf), vl = lds_addr(vbuf);
+  // LDS byte addresses of the buffers, kept in registers (the empty asm stops the compiler
+  // from recomputing them from the shared aperture at every use)
+  uint32_t kl = lds_addr(kbuf), vl = lds_addr(vbuf);
+  asm volatile("" : "+s"(kl), "+s"(vl));
 
   const int nt0 = (w.seg[0].n + BK - 1) / BK;
   const int nt1 = (w.seg[1].n + BK - 1) / BK;
@@ -937,6 +941,10 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   // key tiles [tb, te) of this unit: all of them, or part s of S of a split group
   const int tb = (int)((int64_t)w.split_s * ntiles / w.split_n);
   const int te = (int)((int64_t)(w.split_s + 1) * ntiles / w.split_n);
+  // the partial last tile of each segment (-1: none) and the keys it holds; every other
+  // tile holds BK keys
+  const int pt0 = (w.seg[0].n % BK) ? nt0 - 1 : -1, pt1 = (w.seg[1].n % BK) ? ntiles - 1 : -1;
+  const int nk0 = w.seg[0].n - (nt0 - 1) * BK, nk1 = w.seg[1].n - (nt1 - 1) * BK;
 
   // ---- direct loads.  A cursor walks the key tiles of the context then the main segment
   // (linear addressing: the dispatcher routes per-row lookups elsewhere): p is the
@@ -988,11 +996,10 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   // the paired cursor at the start of segment sg / on key tile t
   auto pair_seg = [&](PairCursor& cr, int sg) {
     const KvSeg& sgm = w.seg[sg];
-    cr.seg = sg;
-    cr.tile = 0;
-    cr.left = __builtin_amdgcn_readfirstlane(sgm.n);
     cr.rowk = __builtin_amdgcn_readfirstlane((uint32_t)sgm.ksn * 2u);
     cr.rowv = __builtin_amdgcn_readfirstlane((uint32_t)sgm.vsn * 2u);
+    cr.stk = (int64_t)cr.rowk * BK;
+    cr.stv = (int64_t)cr.rowv * BK;
     cr.full_pitch = cr.rowk == oc_rowb && cr.rowv == oc_rowb;
     cr.bk = uniform_ptr(sgm.k + sgm.kbase * 2);
     cr.bv = uniform_ptr(sgm.v + sgm.vbase * 2);
@@ -1000,10 +1007,10 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     cr.pv = cr.bv;
     page_window_reset(cr.pw);
   };
-  // paged context tile `tile`: the page of K and V from one table read
-  auto pair_page = [&](PairCursor& cr) {
+  // paged context tile t: the page of K and V from one table read
+  auto pair_page = [&](PairCursor& cr, int t) {
     if constexpr (PAGED) {
-      const int64_t off = page_offset(w.seg[0], cr.tile, cr.pw);
+      const int64_t off = page_offset(w.seg[0], t, cr.pw);
       cr.pk = uniform_ptr(cr.bk + off);
       cr.pv = uniform_ptr(cr.bv + off);
     }
@@ -1011,29 +1018,31 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   auto pair_seek = [&](PairCursor& cr, int t) {
     const int sg = t < nt0 ? 0 : 1;
     pair_seg(cr, sg);
-    const int skip = sg == 0 ? t : t - nt0;
-    cr.left -= skip * BK;
-    cr.tile = skip;
+    cr.ft = t;
     if (PAGED && sg == 0 && ctx_paged) {
-      if (cr.left > 0) pair_page(cr);
+      pair_page(cr, t);
     } else {
-      cr.pk += (size_t)skip * BK * cr.rowk;
-      cr.pv += (size_t)skip * BK * cr.rowv;
+      const int skip = sg == 0 ? t : t - nt0;
+      cr.pk += skip * cr.stk;
+      cr.pv += skip * cr.stv;
     }
   };
   // load the cursor's K tile into LDS byte address kdst and its V tile into vdst (K's loads
   // issued first), then advance to the next tile
   auto fetch_pair = [&](PairCursor& cr, uint32_t kdst, uint32_t vdst) {
+    const int t = cr.ft;
+    const bool part = t == pt0 || t == pt1;
     uint32_t ok[C::NPW], ov[C::NPW];
-    if (cr.left >= BK && cr.full_pitch) {
+    if (!part && cr.full_pitch) {
 #pragma unroll
       for (int j = 0; j < C::NPW; ++j) {
         ok[j] = oc_k[j];
         ov[j] = oc_v[j];
       }
     } else {
-      lane_offsets(cr.rowk, cr.left - 1, false, ok);
-      lane_offsets(cr.rowv, cr.left - 1, true, ov);
+      const int last = !part ? BK - 1 : (t == pt0 ? nk0 : nk1) - 1;
+      lane_offsets(cr.rowk, last, false, ok);
+      lane_offsets(cr.rowv, last, true, ov);
     }
 #pragma unroll
     for (int j = 0; j < C::NPW; ++j) {
@@ -1047,15 +1056,15 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       if (C::NINST % NW == 0 || i < C::NINST)
         dma16_sbase(cr.pv, ov[j], __builtin_amdgcn_readfirstlane(vdst + i * 1024));
     }
-    cr.left -= BK;
-    cr.tile += 1;
-    if (PAGED && cr.seg == 0 && ctx_paged) {  // one page per context tile
-      if (cr.left > 0) pair_page(cr);
+    cr.ft = t + 1;
+    if (t + 1 == nt0) {  // the main segment's first tile next
+      pair_seg(cr, 1);
+    } else if (PAGED && ctx_paged && t + 1 < nt0) {  // one page per context tile
+      pair_page(cr, t + 1);
     } else {
-      cr.pk += (size_t)BK * cr.rowk;
-      cr.pv += (size_t)BK * cr.rowv;
+      cr.pk += cr.stk;
+      cr.pv += cr.stv;
     }
-    if (cr.left <= 0 && cr.seg == 0 && w.seg[1].n > 0) pair_seg(cr, 1);
   };
   // load the cursor's tile into LDS dst and advance to the next tile
   auto fetch = [&](Cursor& cr, char* dst, bool is_v) {
@@ -1082,9 +1091,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     }
     if (cr.left <= 0 && cr.seg == 0 && w.seg[1].n > 0) cursor_seg(cr, 1, is_v);
   };
-  auto tile_keys = [&](int t) {
-    return t < nt0 ? min(BK, w.seg[0].n - t * BK) : min(BK, w.seg[1].n - (t - nt0) * BK);
-  };
+  auto tile_keys = [&](int t) { return t == pt0 ? nk0 : t == pt1 ? nk1 : BK; };
   // S^T = K Q^T from the K tile at byte offset kt from the first K buffer (prologue only;
   // the steps interleave it)
   auto qk = [&](uint32_t kt, f32x4 (&s)[C::NKB][QB]) {
