@@ -1624,7 +1624,11 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const char* tile = smem_raw + (t & 1) * C::TILEB;
-    if (t + 1 < ntiles) fetch(t + 1, (t + 1) & 1);
+    // a wave with query rows loads its share of tile t+1 once its S MFMAs have read tile
+    // t's K fragments (the DMA writes into LDS then overlap the P V phase rather than the
+    // b128 fragment reads of S; measured 2.6-3.3% faster at config 5 than loading at the
+    // top of the tile, and faster than any later point, which leaves the loads less time)
+    if (!wave_active && t + 1 < ntiles) fetch(t + 1, (t + 1) & 1);
     if (wave_active) {
       // Four phases of 32 fenced slots: slot f issues the LDS read of fragment f + LEAD
       // and the MFMA of fragment f.  K fragments f < 64 build S^T: half h = f / 32 covers
@@ -1728,6 +1732,7 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
 #pragma unroll
       for (int f = 32; f < 64; ++f) slot(f);
       __builtin_amdgcn_s_setprio(0);
+      if (t + 1 < ntiles) fetch(t + 1, (t + 1) & 1);
       half_check(1);
       __builtin_amdgcn_s_setprio(2);
 #pragma unroll
