@@ -868,7 +868,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   // log2 units
   const float cs = p.scale * kLog2e;
   v8 qf[QB][C::KC];
-  {
+  auto load_q = [&]() {
     const char* qbase = (const char*)p.q;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -885,7 +885,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
         qf[qb][kc] = raw;
       }
     }
-  }
+  };
+  if constexpr (C::PP) load_q();  // the single-group schedule loads Q after its first tiles
 
   // ---- per-lane LDS byte addresses (see k_swz / kv_swz): the K fragment of block kb,
   // step kc of the K tile at byte offset o from the first K buffer is at koff[kc%4] + o +
@@ -1406,6 +1407,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       pair_seek(pc, tb);
       fetch_pair(pc, kl, vl);
       if (te - tb > 1) fetch_pair(pc, kl + C::TILEB, vl + C::TILEB);
+      load_q();  // its wait for Q also covers the tile loads issued before it
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (wave_active) {
