@@ -118,13 +118,18 @@ FMLM_DEV int64_t key_elem(const BSeg& s, int64_t base, int64_t sn, int key) {
   return base + (int64_t)pg * s.page_elems + (int64_t)(key % FMLM_PAGE_ROWS) * sn;
 }
 
-// context rows of context batch cb (mlm_kernel_impl.py:297-313 packed, :132-141 dense)
-FMLM_DEV BSeg ctx_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int cb, int h) {
+// keys of the context segment of context batch cb (0 without context gradients), from its
+// row range [c0, c1)
+FMLM_DEV int ctx_seg_keys(const fmlm_attn_params& p, int c0, int c1) {
+  return (p.flags & FMLM_FLAG_PREFILL) || !p.k_ctx ? 0 : max(c1 - c0, 0);
+}
+
+// context rows of context batch cb (mlm_kernel_impl.py:297-313 packed, :132-141 dense),
+// given its first row c0 and key count n (ctx_range, ctx_seg_keys)
+FMLM_DEV BSeg ctx_seg_at(const fmlm_attn_params& p, const fmlm_attn_grads& g, int cb, int h, int c0, int n) {
   const bool mla = p.flags & FMLM_FLAG_MLA;
   BSeg s;
-  int c0, c1;
-  ctx_range(p, cb, c0, c1);
-  s.n = (p.flags & FMLM_FLAG_PREFILL) || !p.k_ctx ? 0 : max(c1 - c0, 0);
+  s.n = n;
   s.k = (const char*)p.k_ctx;
   s.v = (const char*)(mla ? p.k_ctx : p.v_ctx);
   s.dk = (char*)g.dk_ctx;
@@ -148,8 +153,8 @@ FMLM_DEV BSeg ctx_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int c
 
 // main keys of sequence b (mlm_kernel_impl.py:288-293, 360-379): its own tokens, or
 // with causal_query_seq_attn the packed tokens [0, cu[b+1]) (n = those of all of them
-// when b < 0)
-FMLM_DEV BSeg main_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int b, int h) {
+// when b < 0); si: the ranges of sequence b (b >= 0), or n = si.mainlen when b < 0
+FMLM_DEV BSeg main_seg_at(const fmlm_attn_params& p, const fmlm_attn_grads& g, int b, int h, const SeqInfo& si) {
   const bool mla = p.flags & FMLM_FLAG_MLA;
   const int64_t v_sb = mla ? p.k_sb : p.v_sb, v_sh = mla ? p.k_sh : p.v_sh, v_sn = mla ? p.k_sn : p.v_sn;
   const int64_t dv_sb = mla ? g.dk_sb : g.dv_sb, dv_sh = mla ? g.dk_sh : g.dv_sh, dv_sn = mla ? g.dk_sn : g.dv_sn;
@@ -167,14 +172,13 @@ FMLM_DEV BSeg main_seg(const fmlm_attn_params& p, const fmlm_attn_grads& g, int 
   s.dvsn = dv_sn;
   const bool causal = (p.flags & FMLM_FLAG_CAUSAL_SEQ) && p.cu_seqlens_q;
   if (causal) {  // packed K/V: token j is row h*sh + j*sn
-    s.n = b < 0 ? min(ldc(p.cu_seqlens_q, p.B), p.total_q) : seq_info(p, b).mainlen;
+    s.n = si.mainlen;
     s.kbase = (int64_t)h * p.k_sh;
     s.vbase = (int64_t)h * v_sh;
     s.dkbase = (int64_t)h * g.dk_sh;
     s.dvbase = (int64_t)h * dv_sh;
     return s;
   }
-  const SeqInfo si = seq_info(p, b);
   s.n = si.len;
   s.kbase = row_at(p.kv_layout, b, h, si.q0, 0, p.k_sb, p.k_sh, p.k_sn);
   s.vbase = row_at(p.kv_layout, b, h, si.q0, 0, v_sb, v_sh, v_sn);
@@ -428,51 +432,192 @@ struct KeyUnit {
   bool is_ctx;
   bool causal_main;   // main keys of the causal token range (key j seen by b iff j < cu[b+1])
   bool shared;        // key rows shared by all heads (head stride 0)
+  SeqInfo si_lo;      // ranges of sequence b_lo (b_lo < b_hi)
 };
 
-template <bool CAUSAL>
-FMLM_DEV bool resolve_key_unit(const fmlm_attn_params& p, const fmlm_attn_grads& g, int n_ctx, int keys,
-                               KeyUnit& k) {
+// ---------------------------------------------------------------------------
+// Unit records.  bwd_records_kernel resolves every unit of both grids once per call into
+// kRecInts ints, so that a workgroup reads its unit in one round trip instead of the
+// chains of dependent metadata loads (binary searches over the unit tables, then the
+// sequence and context ranges) that took 5-6 us per dK/dV unit.
+//   query unit (dq): [0] sequence b (-1: no rows), [1] its first row, [2..5] SeqInfo of b
+//     (q0, len, ctx, mainlen), [6] context batch, [7] its first row, [8] its keys
+//   key unit (dK/dV): [0] kind (0: none, 1: context tile, 2: main-key tile), [1] sequence
+//     or context batch, [2] first key, [3] keys of the segment, [4] the segment's first row
+//     (context row or sequence start), [5] b_lo: the first sequence whose queries attend
+//     to the tile (b_hi if none), [6] b_hi, [7..10] SeqInfo of b_lo
+// ---------------------------------------------------------------------------
+constexpr int kRecInts = 16;
+
+// the first N ints of record r, in one round trip: every load is issued before any of
+// them is used (the compiler would otherwise sink loads into the branches on field 0 and
+// wait for them one after another)
+template <int N>
+FMLM_DEV void load_record(const int32_t* r, int (&f)[N]) {
+  static_assert(N == 9 || N == 11, "record prefix");
+#pragma unroll
+  for (int i = 0; i < N; ++i) f[i] = ldc(r, i);
+  if constexpr (N == 9)
+    asm volatile("" ::"s"(f[0]), "s"(f[1]), "s"(f[2]), "s"(f[3]), "s"(f[4]), "s"(f[5]), "s"(f[6]), "s"(f[7]), "s"(f[8]));
+  else
+    asm volatile("" ::"s"(f[0]), "s"(f[1]), "s"(f[2]), "s"(f[3]), "s"(f[4]), "s"(f[5]), "s"(f[6]), "s"(f[7]), "s"(f[8]),
+                 "s"(f[9]), "s"(f[10]));
+}
+
+FMLM_DEV SeqInfo rec_seq_info(const int* f) {
+  SeqInfo si;
+  si.q0 = f[0];
+  si.len = f[1];
+  si.ctx = f[2];
+  si.mainlen = f[3];
+  return si;
+}
+
+FMLM_DEV void query_record(const fmlm_attn_params& p, const fmlm_attn_grads& g, int bq, int u, int32_t (&r)[kRecInts]) {
+  const UnitTables ut = unit_tables(p, g);
+#pragma unroll
+  for (int i = 0; i < kRecInts; ++i) r[i] = 0;
+  r[0] = -1;
+  if (u >= ldc(ut.q, p.B)) return;
+  const int rk = find_seq(ut.q, p.B, u);  // table entry: sequences by key count, largest first
+  const int b = ldc(ut.perm, rk);
+  const SeqInfo si = seq_info(p, b);
+  const int qpos0 = (u - ldc(ut.q, rk)) * bq;
+  if (qpos0 >= si.len) return;
+  const int cb = ctx_batch_of(p, b);
+  int c0, c1;
+  ctx_range(p, cb, c0, c1);
+  r[0] = b;
+  r[1] = qpos0;
+  r[2] = si.q0;
+  r[3] = si.len;
+  r[4] = si.ctx;
+  r[5] = si.mainlen;
+  r[6] = cb;
+  r[7] = c0;
+  r[8] = ctx_seg_keys(p, c0, c1);
+}
+
+// a tile of context batch / sequence `slot` (main keys: causal_main as in KeyUnit) from
+// key j0 is attended by the queries of sequence b
+FMLM_DEV bool seq_attends(const fmlm_attn_params& p, bool is_ctx, bool causal_main, int slot, int j0, int b,
+                          SeqInfo& si) {
+  if (is_ctx && ctx_batch_of(p, b) != slot) return false;
+  si = seq_info(p, b);
+  return si.len > 0 && (!causal_main || si.mainlen > j0);  // causal: tokens < cu[b+1]
+}
+
+FMLM_DEV void key_record(const fmlm_attn_params& p, const fmlm_attn_grads& g, int n_ctx, int keys, bool causal,
+                         int u, int32_t (&r)[kRecInts]) {
   const int32_t* cu = p.cu_seqlens_q;
+  const UnitTables ut = unit_tables(p, g);
+#pragma unroll
+  for (int i = 0; i < kRecInts; ++i) r[i] = 0;
+  const int n_main = causal ? (min(ldc(cu, p.B), p.total_q) + keys - 1) / keys : ldc(ut.k, p.B);
+  const int n_cunits = n_ctx > 0 ? ldc(ut.c, n_ctx) : 0;
+  int kind = 0, slot = 0, j0 = 0, n = 0, row0 = 0, b_lo = p.B, b_hi = p.B;
+  if (u < n_cunits) {
+    kind = 1;
+    slot = find_seq(ut.c, n_ctx, u);
+    j0 = (u - ldc(ut.c, slot)) * keys;
+    int c0, c1;
+    ctx_range(p, slot, c0, c1);
+    n = ctx_seg_keys(p, c0, c1);
+    row0 = c0;
+    // the sequences of this context batch: with one batch per sequence and no context
+    // index, sequence `slot` alone (ctx_batch_of), else any of them
+    const bool own = !p.ctx_index && p.ctx_batch > 1;
+    b_lo = own ? min(slot, p.B) : 0;
+    b_hi = own ? min(slot + 1, p.B) : p.B;
+  } else if (u - n_cunits < n_main) {
+    kind = 2;
+    const int um = u - n_cunits;
+    if (causal) {
+      j0 = um * keys;
+      n = min(ldc(cu, p.B), p.total_q);
+      b_lo = j0 < n ? find_seq(cu, p.B, j0) : p.B;
+    } else {
+      slot = find_seq(ut.k, p.B, um);
+      j0 = (um - ldc(ut.k, slot)) * keys;
+      const SeqInfo si = seq_info(p, slot);
+      n = si.len;
+      row0 = si.q0;
+      b_lo = slot;
+      b_hi = slot + 1;
+    }
+  }
+  if (kind == 0 || j0 >= n) return;
+  SeqInfo si{};
+  int b = b_lo;
+  for (; b < b_hi; ++b)
+    if (seq_attends(p, kind == 1, causal && kind == 2, slot, j0, b, si)) break;
+  r[0] = kind;
+  r[1] = slot;
+  r[2] = j0;
+  r[3] = n;
+  r[4] = row0;
+  r[5] = b;
+  r[6] = b_hi;
+  if (b < b_hi) {
+    r[7] = si.q0;
+    r[8] = si.len;
+    r[9] = si.ctx;
+    r[10] = si.mainlen;
+  }
+}
+
+// one thread per unit of either grid
+__global__ __launch_bounds__(256) void bwd_records_kernel(const fmlm_attn_params p, const fmlm_attn_grads g, int bq,
+                                                          int bk, int n_ctx, int32_t* qrec, int nq, int32_t* krec,
+                                                          int nk) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  int32_t r[kRecInts];
+  if (i < nq) {
+    query_record(p, g, bq, i, r);
+    int4* d = (int4*)(qrec + (int64_t)i * kRecInts);
+#pragma unroll
+    for (int j = 0; j < kRecInts / 4; ++j) d[j] = make_int4(r[4 * j], r[4 * j + 1], r[4 * j + 2], r[4 * j + 3]);
+  }
+  if (i < nk) {
+    key_record(p, g, n_ctx, bk, (p.flags & FMLM_FLAG_CAUSAL_SEQ) != 0, i, r);
+    int4* d = (int4*)(krec + (int64_t)i * kRecInts);
+#pragma unroll
+    for (int j = 0; j < kRecInts / 4; ++j) d[j] = make_int4(r[4 * j], r[4 * j + 1], r[4 * j + 2], r[4 * j + 3]);
+  }
+}
+
+// unit u of key head kh (grid_unit) from its record (krec: nk records); false for a
+// workgroup without keys (past the units, an empty tile, or a shared segment's other heads)
+template <bool CAUSAL>
+FMLM_DEV bool resolve_key_unit(const fmlm_attn_params& p, const fmlm_attn_grads& g, int n_ctx, const int32_t* krec,
+                               int nk, KeyUnit& k) {
   int u, kh;
   grid_unit(dkv_heads(p, n_ctx), u, kh);
   k.kh = kh;
-  const UnitTables ut = unit_tables(p, g);
-  const int n_main = CAUSAL ? (min(ldc(cu, p.B), p.total_q) + keys - 1) / keys : ldc(ut.k, p.B);
-  const int n_cunits = n_ctx > 0 ? ldc(ut.c, n_ctx) : 0;
-  k.is_ctx = u < n_cunits;
-  if (k.is_ctx) {
-    k.slot = find_seq(ut.c, n_ctx, u);
-    k.j0 = (u - ldc(ut.c, k.slot)) * keys;
-  } else {
-    const int um = u - n_cunits;
-    if (um >= n_main) return false;
-    if (CAUSAL) {
-      k.slot = 0;
-      k.j0 = um * keys;
-    } else {
-      k.slot = find_seq(ut.k, p.B, um);
-      k.j0 = (um - ldc(ut.k, k.slot)) * keys;
-    }
-  }
+  if (u >= nk) return false;
+  int f[11];
+  load_record(krec + (int64_t)u * kRecInts, f);
+  const int kind = f[0];
+  if (kind == 0) return false;
+  k.is_ctx = kind == 1;
+  k.slot = f[1];
+  k.j0 = f[2];
+  const int n = f[3], row0 = f[4];
+  k.b_lo = f[5];
+  k.b_hi = f[6];
+  k.si_lo = rec_seq_info(f + 7);
   k.causal_main = CAUSAL && !k.is_ctx;
   if (k.is_ctx) {
-    k.s = ctx_seg(p, g, k.slot, kh);
-    k.b_lo = 0;
-    k.b_hi = p.B;
+    k.s = ctx_seg_at(p, g, k.slot, kh, row0, n);
     k.shared = p.c_sh == 0;
-  } else if (CAUSAL) {
-    k.s = main_seg(p, g, -1, kh);
-    k.b_lo = k.j0 < k.s.n ? find_seq(cu, p.B, k.j0) : p.B;
-    k.b_hi = p.B;
-    k.shared = p.k_sh == 0;
   } else {
-    k.s = main_seg(p, g, k.slot, kh);
-    k.b_lo = k.slot;
-    k.b_hi = k.slot + 1;
+    SeqInfo sm{};
+    sm.q0 = row0;
+    sm.len = sm.mainlen = n;
+    k.s = main_seg_at(p, g, CAUSAL ? -1 : k.slot, kh, sm);
     k.shared = p.k_sh == 0;
   }
-  return k.j0 < k.s.n && !(k.shared && kh > 0);  // the grid covers the larger segment kind
+  return !(k.shared && kh > 0);  // the grid covers the larger segment kind
 }
 
 // Query steps of a key unit: (head hq, sequence b, rows [p0, p0 + qs)) over every
@@ -485,9 +630,8 @@ struct QuerySteps {
   const KeyUnit* k;
   int hq_hi, qs;
   FMLM_DEV bool seq_ok(int b) const {
-    if (k->is_ctx && ctx_batch_of(*p, b) != k->slot) return false;
-    const SeqInfo si = seq_info(*p, b);
-    return si.len > 0 && (!k->causal_main || si.mainlen > k->j0);  // causal: tokens < cu[b+1]
+    SeqInfo si;
+    return seq_attends(*p, k->is_ctx, k->causal_main, k->slot, k->j0, b, si);
   }
   FMLM_DEV QStep first_from(int hq, int b) const {
     while (hq < hq_hi) {
@@ -511,21 +655,22 @@ struct QuerySteps {
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kernel(const fmlm_attn_params p,
-                                                                     const fmlm_attn_grads g) {
+                                                                     const fmlm_attn_grads g,
+                                                                     const int32_t* qrec, int nq) {
   typedef BwdCfg<D> C;
   typedef typename Mfma<T>::v8 v8;
   constexpr int QB = C::QB;
   extern __shared__ __align__(16) char smem_raw[];
 
-  const UnitTables ut = unit_tables(p, g);
   int u, h;
   grid_unit((unsigned)p.H, u, h);
-  if (u >= ldc(ut.q, p.B)) return;
-  const int rk = find_seq(ut.q, p.B, u);  // table entry: sequences by key count, largest first
-  const int b = ldc(ut.perm, rk);
-  const SeqInfo si = seq_info(p, b);
-  const int qpos0 = (u - ldc(ut.q, rk)) * C::BQ;
-  if (qpos0 >= si.len) return;
+  if (u >= nq) return;
+  int rec[9];  // the unit's record (query_record)
+  load_record(qrec + (int64_t)u * kRecInts, rec);
+  const int b = rec[0];
+  if (b < 0) return;
+  const int qpos0 = rec[1];
+  const SeqInfo si = rec_seq_info(rec + 2);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
   const float c = p.scale * kLog2e;  // scores in log2 units
@@ -534,8 +679,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   // software-pipelined tile (below) for the double-buffered unpadded tiles
   constexpr bool PIPE = !C::PAD && C::DQ_NBUF == 2;
 
-  const BSeg sc = ctx_seg(p, g, ctx_batch_of(p, b), h);  // context, then main keys
-  const BSeg sm = main_seg(p, g, b, h);
+  const BSeg sc = ctx_seg_at(p, g, rec[6], h, rec[7], rec[8]);  // context, then main keys
+  const BSeg sm = main_seg_at(p, g, b, h, si);
   const int nt0 = (sc.n + kBwdBK - 1) / kBwdBK;
   const int nt = nt0 + (sm.n + kBwdBK - 1) / kBwdBK;
 
@@ -936,7 +1081,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kernel(const fmlm_attn_params p,
-                                                                      const fmlm_attn_grads g, int n_ctx) {
+                                                                      const fmlm_attn_grads g, int n_ctx,
+                                                                      const int32_t* krec, int nk) {
   typedef BwdCfg<D> C;
   typedef typename Mfma<T>::v8 v8;
   extern __shared__ __align__(16) char smem_raw[];
@@ -950,7 +1096,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   // software-pipelined step (below) for 64-row steps of unpadded tiles
   constexpr bool PIPE = !C::PAD && !C::MLA_ONLY && C::QS == 64;
   KeyUnit ku;
-  if (!resolve_key_unit<CAUSAL>(p, g, n_ctx, C::DKV_KEYS, ku)) return;
+  if (!resolve_key_unit<CAUSAL>(p, g, n_ctx, krec, nk, ku)) return;
   const BSeg& s = ku.s;
   const int j0 = ku.j0;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1081,10 +1227,10 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
 
   // the ranges of the current and the next step's sequences are read once per sequence:
   // consecutive steps of one sequence reuse them
-  QStep cur = steps.first_from(hq_lo, ku.b_lo);
-  SeqInfo si_cur{};
+  // the first step: sequence b_lo of the first head, with its ranges from the unit record
+  QStep cur{ku.b_lo < ku.b_hi ? hq_lo : hq_hi, ku.b_lo, 0};
+  SeqInfo si_cur = ku.si_lo;
   StepRows rows_cur{};
-  if (cur.hq < hq_hi) si_cur = seq_info(p, cur.b);
   int buf = 0;
   if constexpr (PIPE) {
     if (cur.hq < hq_hi) {
@@ -1396,21 +1542,22 @@ FMLM_DEV float row_sum(float x) {
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_params p, const fmlm_attn_grads g) {
+__global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_params p, const fmlm_attn_grads g,
+                                                               const int32_t* qrec, int nq) {
   typedef SimtBwdCfg<D> C;
   extern __shared__ __align__(16) char smem_raw[];
   float* const Kf = (float*)smem_raw;
   float* const Vf = Kf + C::DQK * D;
 
-  const UnitTables ut = unit_tables(p, g);
   int u, h;
   grid_unit((unsigned)p.H, u, h);
-  if (u >= ldc(ut.q, p.B)) return;
-  const int rk = find_seq(ut.q, p.B, u);  // table entry: sequences by key count, largest first
-  const int b = ldc(ut.perm, rk);
-  const SeqInfo si = seq_info(p, b);
-  const int qpos0 = (u - ldc(ut.q, rk)) * C::R;
-  if (qpos0 >= si.len) return;
+  if (u >= nq) return;
+  int rec[9];  // the unit's record (query_record)
+  load_record(qrec + (int64_t)u * kRecInts, rec);
+  const int b = rec[0];
+  if (b < 0) return;
+  const int qpos0 = rec[1];
+  const SeqInfo si = rec_seq_info(rec + 2);
   const int tid = threadIdx.x, row = tid / C::TPR, d0 = (tid % C::TPR) * C::DPT;
   const int pos = qpos0 + row;
   const bool ok = pos < si.len;
@@ -1435,8 +1582,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_p
   }
   const float delta = row_sum<C::TPR>(dsum);
 
-  const BSeg sc = ctx_seg(p, g, ctx_batch_of(p, b), h);
-  const BSeg sm = main_seg(p, g, b, h);
+  const BSeg sc = ctx_seg_at(p, g, rec[6], h, rec[7], rec[8]);
+  const BSeg sm = main_seg_at(p, g, b, h, si);
   const int nt0 = (sc.n + C::DQK - 1) / C::DQK;
   const int nt = nt0 + (sm.n + C::DQK - 1) / C::DQK;
   float m_i = -INFINITY, l_i = 0.f;
@@ -1513,7 +1660,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_simt_kernel(const fmlm_attn_p
 
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_simt_kernel(const fmlm_attn_params p, const fmlm_attn_grads g,
-                                                                int n_ctx) {
+                                                                int n_ctx, const int32_t* krec, int nk) {
   typedef SimtBwdCfg<D> C;
   constexpr int QS = C::BKS;
   extern __shared__ __align__(16) char smem_raw[];
@@ -1524,7 +1671,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_simt_kernel(const fmlm_attn_
 
   const bool mla = p.flags & FMLM_FLAG_MLA;
   KeyUnit ku;
-  if (!resolve_key_unit<CAUSAL>(p, g, n_ctx, C::R, ku)) return;
+  if (!resolve_key_unit<CAUSAL>(p, g, n_ctx, krec, nk, ku)) return;
   const BSeg& s = ku.s;
   const int tid = threadIdx.x, d0 = (tid % C::TPR) * C::DPT;
   const int key = ku.j0 + tid / C::TPR;
@@ -1738,6 +1885,38 @@ static int check_bwd(const fmlm_attn_params& p, const fmlm_attn_grads& g, BwdFns
 
 using namespace fmlm;
 
+// Units of the two grids and the workspace layout: the row statistics (2 H total_q
+// floats), the sequence order and the unit tables (ints, see UnitTables), then the query
+// and the key unit records (kRecInts ints each, 64-byte aligned).  bq, bk: query rows and
+// keys per unit; n_ctx: context batches with gradients.
+constexpr int kMinUnitRows = 16;  // the smallest bq / bk of any kernel pair
+struct BwdLayout {
+  int64_t qunits, kunits;  // units of the dq and of the dK / dV grid
+  int64_t qrec, krec;      // byte offsets of their records
+  int64_t bytes;
+};
+static BwdLayout bwd_layout(const fmlm_attn_params& p, int bq, int bk, int n_ctx) {
+  BwdLayout l;
+  const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
+  // at most total_q / bq + B query tiles; main keys: tiles per sequence, or of the causal
+  // token range
+  l.qunits = (int64_t)p.total_q / bq + p.B;
+  const int64_t munits = causal ? ((int64_t)p.total_q + bk - 1) / bk : (int64_t)p.total_q / bk + p.B;
+  // context rows over all batches: a packed context's rows per head, a paged one's pages
+  // per batch (ctx_rows counts pool pages there), or the uniform length per batch
+  const int64_t crows = n_ctx == 0            ? 0
+                        : p.ctx_block_table   ? (int64_t)n_ctx * std::max(p.ctx_pages_per_batch, 0) * FMLM_PAGE_ROWS
+                        : p.cu_seqlens_kv     ? (int64_t)std::max(p.ctx_rows, 0)
+                                              : (int64_t)n_ctx * std::max(p.ctx_len, 0);
+  l.kunits = munits + (n_ctx > 0 ? crows / bk + n_ctx : 0);
+  const int64_t tables = 2 * (int64_t)p.H * p.total_q * 4 +
+                         4 * ((int64_t)p.B + 2 * ((int64_t)p.B + 1) + (p.ctx_batch > 1 ? p.ctx_batch : 1) + 1);
+  l.qrec = (tables + 63) / 64 * 64;
+  l.krec = l.qrec + l.qunits * kRecInts * 4;
+  l.bytes = (l.krec + l.kunits * kRecInts * 4 + 255) / 256 * 256;
+  return l;
+}
+
 // The grid of `units` units x `heads` heads (grid_unit: heads fastest), at most 2^23
 // workgroups per row; false if it has 2^31 workgroups or more.
 static bool unit_grid(int64_t units, unsigned heads, dim3& grid) {
@@ -1751,11 +1930,10 @@ extern "C" int fmlm_attn_grads_size(void) { return (int)sizeof(fmlm_attn_grads);
 
 extern "C" int64_t fmlm_attn_bwd_workspace_bytes(const fmlm_attn_params* p) {
   if (!p || p->H < 0 || p->total_q < 0 || p->B < 0 || p->ctx_batch < 0) return FMLM_E_ARG;
-  // row statistics, then the sequence order (B ints) and the unit tables (B + 1, B + 1,
-  // context batches + 1 ints)
-  const int64_t bytes = 2 * (int64_t)p->H * p->total_q * 4 +
-                        4 * ((int64_t)p->B + 2 * ((int64_t)p->B + 1) + (p->ctx_batch > 1 ? p->ctx_batch : 1) + 1);
-  return (bytes + 255) / 256 * 256;
+  // every kernel pair's units have at least kMinUnitRows rows, and context gradients may
+  // be asked for whenever there is a context
+  const int n_ctx = p->k_ctx && !(p->flags & FMLM_FLAG_PREFILL) ? (p->ctx_batch > 1 ? p->ctx_batch : 1) : 0;
+  return bwd_layout(*p, kMinUnitRows, kMinUnitRows, n_ctx).bytes;
 }
 
 extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* gp, void* stream) {
@@ -1766,39 +1944,37 @@ extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* 
   int rc = check_bwd(p, g, f);
   if (rc) return rc;
   if (p.B == 0 || p.H == 0 || p.total_q == 0) return 0;
-  if (!g.workspace || g.workspace_bytes < fmlm_attn_bwd_workspace_bytes(pp)) return FMLM_E_WORKSPACE;
   if (p.H > 65535) return FMLM_E_ARG;
-  hipStream_t s = (hipStream_t)stream;
   const bool prefill = p.flags & FMLM_FLAG_PREFILL;
   const bool causal = p.flags & FMLM_FLAG_CAUSAL_SEQ;
-  fmlm_attn_params pc = p;
-  fmlm_attn_grads gc = g;
-  void* args[] = {(void*)&pc, (void*)&gc};
-
   const bool ctx_grads = g.dk_ctx && !prefill && p.k_ctx;
   int n_ctx = ctx_grads ? (p.ctx_batch > 1 ? p.ctx_batch : 1) : 0;
-  // 0. unit tables
+  const BwdLayout l = bwd_layout(p, f.bq, f.dkv_keys, n_ctx);
+  if (!g.workspace || g.workspace_bytes < fmlm_attn_bwd_workspace_bytes(pp) || g.workspace_bytes < l.bytes)
+    return FMLM_E_WORKSPACE;
+  dim3 qgrid, kgrid;
+  if (!unit_grid(l.qunits, (unsigned)p.H, qgrid) || !unit_grid(l.kunits, dkv_heads(p, n_ctx), kgrid)) return FMLM_E_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  fmlm_attn_params pc = p;
+  fmlm_attn_grads gc = g;
+  int32_t* qrec = (int32_t*)((char*)g.workspace + l.qrec);
+  int32_t* krec = (int32_t*)((char*)g.workspace + l.krec);
+  int nq = (int)l.qunits, nk = (int)l.kunits;
+
+  // 0. unit tables, then the records of both grids' units
   hipLaunchKernelGGL(bwd_units_kernel, dim3(1), dim3(kScanThreads), 0, s, p, g, f.bq, f.dkv_keys, n_ctx);
   if ((rc = launch_status())) return rc;
-  // 1. dq (+ the row statistics): at most total_q / BQ + B query tiles per head
+  const int64_t nrec = std::max(l.qunits, l.kunits);
+  hipLaunchKernelGGL(bwd_records_kernel, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, s, p, g, f.bq, f.dkv_keys,
+                     n_ctx, qrec, nq, krec, nk);
+  if ((rc = launch_status())) return rc;
+  // 1. dq (+ the row statistics)
   if ((rc = raise_lds(f.dq, f.dq_lds))) return rc;
-  const int64_t qunits = (int64_t)p.total_q / f.bq + p.B;
-  dim3 qgrid;
-  if (!unit_grid(qunits, (unsigned)p.H, qgrid)) return FMLM_E_ARG;
+  void* args[] = {(void*)&pc, (void*)&gc, (void*)&qrec, (void*)&nq};
   hipError_t e = hipLaunchKernel(f.dq, qgrid, dim3(kBwdNW * 64), args, (size_t)f.dq_lds, s);
   if (e != hipSuccess) return (int)e;
   // 2. dK / dV, context keys then main keys in one launch
-  const int64_t munits = causal ? ((int64_t)p.total_q + f.dkv_keys - 1) / f.dkv_keys : (int64_t)p.total_q / f.dkv_keys + p.B;
-  // context rows over all batches: a packed context's rows per head, a paged one's pages
-  // per batch (ctx_rows counts pool pages there), or the uniform length per batch
-  const int64_t crows = !ctx_grads                ? 0
-                        : p.ctx_block_table       ? (int64_t)n_ctx * p.ctx_pages_per_batch * FMLM_PAGE_ROWS
-                        : p.cu_seqlens_kv         ? (int64_t)p.ctx_rows
-                                                  : (int64_t)n_ctx * p.ctx_len;
-  const int64_t cunits = ctx_grads ? crows / f.dkv_keys + n_ctx : 0;
-  dim3 kgrid;
-  if (!unit_grid(munits + cunits, dkv_heads(p, n_ctx), kgrid)) return FMLM_E_ARG;
-  void* kargs[] = {(void*)&pc, (void*)&gc, (void*)&n_ctx};
+  void* kargs[] = {(void*)&pc, (void*)&gc, (void*)&n_ctx, (void*)&krec, (void*)&nk};
   if ((rc = raise_lds(f.dkv[causal ? 1 : 0], f.dkv_lds))) return rc;
   e = hipLaunchKernel(f.dkv[causal ? 1 : 0], kgrid, dim3(kBwdNW * 64), kargs, (size_t)f.dkv_lds, s);
   if (e != hipSuccess) return (int)e;

@@ -295,8 +295,8 @@ FMLM_API int fmlm_attn_fwd_noalloc(const fmlm_attn_params* p, void* stream);
  * Rows not listed are not written.  dout is laid out like o (o_layout).
  * bf16 / f16 (MFMA) and f32 (SIMT), D in {16, 32, 64, 128, 256, 512}; with
  * FMLM_FLAG_CAUSAL_SEQ the main keys must be packed (kv_layout PACKED).
- * workspace: fmlm_attn_bwd_workspace_bytes(p) bytes (per-row softmax statistics and the
- *           tile tables of the two kernels).
+ * workspace: fmlm_attn_bwd_workspace_bytes(p) bytes (per-row softmax statistics, the
+ *           tile tables of the two kernels and a 64-byte record per tile).
  * ------------------------------------------------------------------------- */
 typedef struct fmlm_attn_grads {
   const void* dout; int64_t do_sb, do_sh, do_sn;
