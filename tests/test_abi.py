@@ -86,9 +86,16 @@ def test_argument_rejection_without_launch():
     assert lib.fmlm_attn_bwd(p, g, None) == -5
     p.dtype = _lib.DTYPE_BF16
     assert lib.fmlm_attn_bwd(p, g, None) == -5  # no workspace
-    assert lib.fmlm_attn_bwd_workspace_bytes(p) == 256  # 2 floats per (head, row) + tile tables, rounded up
+    # 2 floats per (head, row), the tile tables (ints), then a 64-byte record per unit of
+    # either grid, counted at the smallest unit of 16 rows: total_q / 16 + B query units
+    # and as many main-key units (no context here)
+    def bwd_bytes(H, T, B=1):
+        tables = 2 * H * T * 4 + 4 * (B + 2 * (B + 1) + 1 + 1)
+        units = 2 * (T // 16 + B)
+        return ((tables + 63) // 64 * 64 + units * 64 + 255) // 256 * 256
+    assert lib.fmlm_attn_bwd_workspace_bytes(p) == bwd_bytes(1, 4) == 256
     p.H, p.total_q = 8, 4096
-    assert lib.fmlm_attn_bwd_workspace_bytes(p) == (2 * 8 * 4096 * 4 + 4 * (1 + 2 * 2 + 1 + 1) + 255) // 256 * 256
+    assert lib.fmlm_attn_bwd_workspace_bytes(p) == bwd_bytes(8, 4096)
     p.q = 264  # not 16-byte aligned
     assert lib.fmlm_attn_bwd(p, g, None) == -4
     with pytest.raises(RuntimeError, match="invalid argument"):
