@@ -585,15 +585,22 @@ def _backward_call(case: Case):
     plan = case.attention
     if plan is None:
         return None
-    plan()
+    # as under autograd: the forward stores the row statistics the backward reads; the
+    # backward keeps its own copy of the parameter block (later forward runs reset the field)
+    hh._ROW_STATS.on = True
+    try:
+        plan()
+    finally:
+        hh._ROW_STATS.on = False
+    params, lse = _lib.AttnParams.from_buffer_copy(plan.params), plan.lse
     out = plan.keep[1]
     dout = torch.randn(out.shape, device=out.device).to(out.dtype)
     g, keep = hh._backward_args(plan, out, dout, want_ctx=True)
 
     def call():
-        _lib.check(plan.lib.fmlm_attn_bwd(plan.params, g, plan.stream), "fmlm_attn_bwd")
+        _lib.check(plan.lib.fmlm_attn_bwd(params, g, plan.stream), "fmlm_attn_bwd")
 
-    return call, g, (keep, out, dout)
+    return call, g, (keep, out, dout, lse, params)
 
 
 def backward_kernels(case: Case, reps: int = 20) -> dict | None:
@@ -601,8 +608,9 @@ def backward_kernels(case: Case, reps: int = 20) -> dict | None:
     context) on this workload's prepared call, gradients of q, k, v and of the cached
     context: median of HIP-event times with L2/MALL flushed before each launch.
     Effective work = 2.5x the forward's FLOPs (the products dP = dO V^T, dV = P^T dO,
-    dq = dS K, dK = dS^T q besides S = q K^T), padding excluded; the kernels also
-    recompute S twice for dq (the row statistics, then dS), which is not counted."""
+    dq = dS K, dK = dS^T q besides S = q K^T), padding excluded; the dK/dV kernel
+    computes S and dP again, which is not counted.  The forward stores the row statistics first,
+    as under autograd."""
     bc = _backward_call(case)
     if bc is None:
         return None

@@ -313,6 +313,13 @@ FMLM_DEV int64_t seg_row(const KvSeg& s, int i, bool is_v, const int32_t* cu, in
   return base + (int64_t)bb * sb + (int64_t)(i - cu[bb]) * sn;
 }
 
+// Row statistic for the backward (fmlm_attn_params::lse): log2 of the sum of 2^z over the
+// row's keys, from a reference max m and l = sum 2^(z - m); +inf for a row without keys.
+// Row pos of sequence b (packed start q0) and head h.
+FMLM_DEV void store_lse(const fmlm_attn_params& p, int h, int q0, int pos, float m, float l) {
+  p.lse[(int64_t)h * p.total_q + q0 + pos] = l > 0.f ? m + __log2f(l) : INFINITY;
+}
+
 FMLM_DEV int4 ldc4(const int4* a, int i) {
   const int32_t* q = (const int32_t*)(a + i);
   return make_int4(ldc(q, 0), ldc(q, 1), ldc(q, 2), ldc(q, 3));
@@ -733,6 +740,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma_kernel(con
     const float inv = l > 0.f ? 1.f / l : 1.f;
     const int row = (wave * QB + qb) * 16 + l16;
     if (row >= w.qcount) continue;
+    if (p.lse && g == 0) store_lse(p, w.h, w.q0, w.qpos0 + row, m_i[qb], l);
     const int64_t off = w.o_row0 + (int64_t)row * w.o_sn;
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db) {
@@ -1468,6 +1476,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     const float inv = l > 0.f ? 1.f / l : 1.f;
     const int row = (wave * QB + qb) * 16 + l16;
     if (row >= w.qcount) continue;
+    if (p.lse && g == 0) store_lse(p, w.h, w.q0, w.qpos0 + row, m_i[qb], l);
     const int64_t off = w.o_row0 + (int64_t)row * w.o_sn;
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db) {
@@ -1507,7 +1516,7 @@ struct MlaRowsCfg {
   static constexpr int LDS_BYTES = 2 * TILEB;
 };
 
-template <typename T, bool PAGED>
+template <typename T, bool PAGED, bool LSE>
 __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
     const fmlm_attn_params p, const int4* __restrict__ units, const int32_t* __restrict__ hdr) {
   typedef MlaRowsCfg C;
@@ -1760,6 +1769,19 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
       for (int r = 0; r < 4; ++r) v4[r] = (T)(o[db][r] * inv);
       *(u32x2*)(dst + (db * 16 + g * 4) * 2) = *(const u32x2*)v4;
     }
+    // the row statistic (LSE instantiation only: the row and the sequence ranges it needs
+    // cost the kernel, at 256 VGPRs, registers across the tile loop), after the row's
+    // store: its (head, position) as for the q and o offsets
+    if (LSE && p.lse && g == 0) {
+      int rr = row;
+      asm volatile("" : "+v"(rr));
+      int hq = w.h, pq = w.qpos0 + rr;
+      if (hpack && w.len > 0) {
+        hq = pq / w.len;
+        pq -= hq * w.len;
+      }
+      store_lse(p, hq, w.q0, pq, m_i, l_i);
+    }
   }
 }
 
@@ -1888,6 +1910,7 @@ __global__ __launch_bounds__(SimtCfg<D>::NT) void attn_simt_kernel(
   }
   if (!ok) return;
   const float inv = l_i > 0.f ? 1.f / l_i : 1.f;
+  if (p.lse && part == 0) store_lse(p, w.h, w.q0, w.qpos0 + row, m_i, l_i);
   T* op = (T*)p.o + w.o_row0 + (int64_t)row * w.o_sn + d0;
 #pragma unroll
   for (int d = 0; d < C::DPT; ++d) op[d] = (T)(o[d] * inv);
@@ -1948,6 +1971,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const fmlm_attn_params p, in
       const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
       for (int sp = 0; sp < kMaxSplits; ++sp) s_w[r][sp] = l[sp] * inv;
+      if (p.lse) store_lse(p, h, si.q0, tile * BQ + r, M, L);
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < qcount * (D / 8); idx += blockDim.x) {
@@ -2011,11 +2035,15 @@ static Launch mfma3_launch(bool paged) {
 }
 
 // the paged instantiation only for paged contexts: the page lookup costs registers the
-// contiguous kernel (at 256 VGPRs) does not have
+// contiguous kernel (at 256 VGPRs) does not have; the LSE one only for calls that store
+// the row statistics
 template <typename T>
-static Launch mla_rows_launch(bool paged) {
+static Launch mla_rows_launch(bool paged, bool lse) {
   static_assert(MlaRowsCfg::BK == FMLM_PAGE_ROWS, "a paged context tile is one page");
-  const void* fn = paged ? (const void*)&attn_mla_rows_kernel<T, true> : (const void*)&attn_mla_rows_kernel<T, false>;
+  const void* fn = paged ? (lse ? (const void*)&attn_mla_rows_kernel<T, true, true>
+                                : (const void*)&attn_mla_rows_kernel<T, true, false>)
+                         : (lse ? (const void*)&attn_mla_rows_kernel<T, false, true>
+                                : (const void*)&attn_mla_rows_kernel<T, false, false>);
   return Launch{MlaRowsCfg::BQ, MlaRowsCfg::NT, MlaRowsCfg::LDS_BYTES, fn, false, true, true};
 }
 
@@ -2075,7 +2103,7 @@ static bool pick_mfma(const fmlm_attn_params& p, Launch& L) {
       return true;
     case 512:
       if (!(p.flags & FMLM_FLAG_MLA) || k != 1) return false;
-      L = mla_rows_launch<T>(p.ctx_block_table != nullptr);
+      L = mla_rows_launch<T>(p.ctx_block_table != nullptr, p.lse != nullptr);
       return true;
     default: return false;
   }

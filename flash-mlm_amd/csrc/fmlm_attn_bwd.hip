@@ -652,8 +652,10 @@ struct QuerySteps {
 
 // ---------------------------------------------------------------------------
 // dq kernel: grid (query-tile units, H), kBwdNW waves, QB blocks of 16 rows per wave.
+// LSE: the forward stored each row's log2-sum-exp (p.lse), so P = 2^(z - lse) needs no
+// running max, no row sum and no rescale (the software-pipelined tiles only).
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool LSE>
 __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kernel(const fmlm_attn_params p,
                                                                      const fmlm_attn_grads g,
                                                                      const int32_t* qrec, int nq) {
@@ -795,7 +797,10 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   // units, m a running max, l = sum_j 2^(z_j - m)):
   //   dq = scale / l * sum_j 2^(z_j - m) (dP_j - delta) k_j,
   // so dq^T accumulates K^T (2^(z - m) (dP - delta))^T like the forward's O^T and is
-  // rescaled with l whenever m moves (lazily: by more than kRescaleSlack).
+  // rescaled with l whenever m moves (lazily: by more than kRescaleSlack).  With LSE,
+  // m = lse and l = 1 throughout: -lse starts the S^T accumulators and -delta the dP^T
+  // ones, so the MFMAs yield z - lse and dP - delta.
+  static_assert(!LSE || (!C::PAD && C::DQ_NBUF == 2), "LSE: pipelined tiles only");
   f32x4 dq[C::NDB][QB];
 #pragma unroll
   for (int db = 0; db < C::NDB; ++db)
@@ -806,6 +811,10 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   for (int qb = 0; qb < QB; ++qb) {
     m_i[qb] = -INFINITY;
     l_i[qb] = 0.f;
+    if constexpr (LSE) {  // the row's log2-sum-exp; padding rows: +inf, so P = 0
+      const int row = qpos0 + (wave * QB + qb) * 16 + l16;
+      m_i[qb] = row < si.len ? p.lse[(int64_t)h * p.total_q + si.q0 + row] : INFINITY;
+    }
   }
   // NBUF = 2: tile t+1 loads while tile t is used; its buffer was last read by tile t-1,
   // which every wave has finished at the barrier before the issue
@@ -898,14 +907,22 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
       auto soft_block = [&](int kb, int e) {
         const int qb = e >> 1, r = (e & 1) * 2;
         if (r == 0) pin(dpb[kb][qb]);
-        const float mref = m_i[qb] == -INFINITY ? 0.f : m_i[qb];  // no key yet: every z is -inf
         f32x2 pv, ds;
+        if constexpr (LSE) {  // the accumulators hold z - lse and dP - delta
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          pv[i] = fast_exp2(sb[kb][qb][r + i] - mref);
-          ds[i] = pv[i] * (dpb[kb][qb][r + i] - delta[qb]);
+          for (int i = 0; i < 2; ++i) {
+            pv[i] = fast_exp2(sb[kb][qb][r + i]);
+            ds[i] = pv[i] * dpb[kb][qb][r + i];
+          }
+        } else {
+          const float mref = m_i[qb] == -INFINITY ? 0.f : m_i[qb];  // no key yet: every z is -inf
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            pv[i] = fast_exp2(sb[kb][qb][r + i] - mref);
+            ds[i] = pv[i] * (dpb[kb][qb][r + i] - delta[qb]);
+          }
+          l_i[qb] += pv[0] + pv[1];
         }
-        l_i[qb] += pv[0] + pv[1];
         uint32_t wd = __builtin_bit_cast(uint32_t, __builtin_convertvector(ds, typename Pair<T>::type));
         pin(wd);
         dsw[kb >> 1][qb][(kb & 1) * 2 + (r >> 1)] = wd;
@@ -919,7 +936,9 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
         const int kb = sl % C::NKB, kc = sl / C::NKB;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
-          sb[kb][qb] = Mfma<T>::run(a, qf[qb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sb[kb][qb]);
+          sb[kb][qb] = Mfma<T>::run(a, qf[qb][kc], kc > 0 ? sb[kb][qb]
+                                                   : LSE ? f32x4{-m_i[qb], -m_i[qb], -m_i[qb], -m_i[qb]}
+                                                         : f32x4{0.f, 0.f, 0.f, 0.f});
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -929,8 +948,22 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
         const int j = sl - NSS, kb = j / C::KC, kc = j % C::KC;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
-          dpb[kb][qb] = Mfma<T>::run(a, df[qb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dpb[kb][qb]);
-        if (kb == 0) {
+          dpb[kb][qb] = Mfma<T>::run(a, df[qb][kc], kc > 0 ? dpb[kb][qb]
+                                                    : LSE ? f32x4{-delta[qb], -delta[qb], -delta[qb], -delta[qb]}
+                                                          : f32x4{0.f, 0.f, 0.f, 0.f});
+        if (kb == 0 && LSE) {
+          // keys past a partial tile's end to -inf (P = 0), before block 0's exp
+          if (j == 0 && nk < kBwdBK) {
+            asm volatile("");  // (a real branch: full tiles skip the selects)
+#pragma unroll
+            for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+              for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  if (kb2 * 16 + gq * 4 + r >= nk) sb[kb2][qb][r] = -INFINITY;
+          }
+        } else if (kb == 0) {
           // the row max, then the rescale, all before block 0's exp in block 1's slots:
           // one query block per slot from slot 1 where block 0 has the slots for it,
           // else all in slot 0
@@ -1045,11 +1078,11 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     const bool any = l > 0.f;
-    dq_mul[qb] = any ? p.scale / l : 0.f;
+    dq_mul[qb] = LSE ? p.scale : any ? p.scale / l : 0.f;
     const int row = qpos0 + (wave * QB + qb) * 16 + l16;
     if (gq == 0 && row < si.len) {
       const int64_t at = (int64_t)h * p.total_q + si.q0 + row;
-      st_lse[at] = any ? m_i[qb] + __log2f(l) : INFINITY;
+      if (!LSE) st_lse[at] = any ? m_i[qb] + __log2f(l) : INFINITY;
       // the dK / dV kernel's dS = P (scale dP - scale delta); the latent's kernel (whose
       // spills move with any change of its code) keeps delta and multiplies by scale
       st_delta[at] = C::MLA_ONLY ? delta[qb] : delta[qb] * p.scale;
@@ -1102,8 +1135,10 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, gq = lane >> 4;
   const float c = p.scale * kLog2e;
-  const float* const st_lse = (const float*)g.workspace;
-  const float* const st_delta = st_lse + (int64_t)p.H * p.total_q;
+  // the row statistics: the forward's log2-sum-exp when it stored them, else the dq
+  // kernel's; delta from the dq kernel
+  const float* const st_delta = (const float*)g.workspace + (int64_t)p.H * p.total_q;
+  const float* const st_lse = p.lse ? (const float*)p.lse : (const float*)g.workspace;
 
   // this lane's keys (B-operand / accumulator column of each of the wave's KB 16-key
   // blocks) and their K, V fragments: kf[kb][kc] = K[key][kc*32 + 8g .. +8]
@@ -1677,8 +1712,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_simt_kernel(const fmlm_attn_
   const int key = ku.j0 + tid / C::TPR;
   const bool kok = key < s.n;
   const float c = p.scale * kLog2e;
-  const float* const st_lse = (const float*)g.workspace;
-  const float* const st_delta = st_lse + (int64_t)p.H * p.total_q;
+  // the row statistics: the forward's log2-sum-exp when it stored them, else the dq
+  // kernel's; delta from the dq kernel
+  const float* const st_delta = (const float*)g.workspace + (int64_t)p.H * p.total_q;
+  const float* const st_lse = p.lse ? (const float*)p.lse : (const float*)g.workspace;
 
   float kf[C::DPT], vf[C::DPT], dk[C::DPT], dv[C::DPT];
 #pragma unroll
@@ -1770,17 +1807,20 @@ struct BwdFns {
   const void* dq;
   const void* dkv[2];  // main keys per sequence / causal token range (+ context)
   int dq_lds, dkv_lds, bq, dkv_keys;
+  const void* dq_lse = nullptr;  // the dq kernel that reads the forward's row statistics
 };
 
 template <typename T, int D>
 static BwdFns bwd_fns() {
   typedef BwdCfg<D> C;
-  return BwdFns{(const void*)attn_bwd_dq_kernel<T, D>,
-                {(const void*)attn_bwd_dkv_kernel<T, D, false>, (const void*)attn_bwd_dkv_kernel<T, D, true>},
-                C::DQ_LDS,
-                C::DKV_LDS,
-                C::BQ,
-                C::DKV_KEYS};
+  BwdFns f{(const void*)attn_bwd_dq_kernel<T, D, false>,
+           {(const void*)attn_bwd_dkv_kernel<T, D, false>, (const void*)attn_bwd_dkv_kernel<T, D, true>},
+           C::DQ_LDS,
+           C::DKV_LDS,
+           C::BQ,
+           C::DKV_KEYS};
+  if constexpr (!C::PAD && C::DQ_NBUF == 2) f.dq_lse = (const void*)attn_bwd_dq_kernel<T, D, true>;
+  return f;
 }
 
 template <typename T, int D>
@@ -1968,10 +2008,11 @@ extern "C" int fmlm_attn_bwd(const fmlm_attn_params* pp, const fmlm_attn_grads* 
   hipLaunchKernelGGL(bwd_records_kernel, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, s, p, g, f.bq, f.dkv_keys,
                      n_ctx, qrec, nq, krec, nk);
   if ((rc = launch_status())) return rc;
-  // 1. dq (+ the row statistics)
-  if ((rc = raise_lds(f.dq, f.dq_lds))) return rc;
+  // 1. dq (+ the row statistics: delta, and the log2-sum-exp unless the forward stored it)
+  const void* const dq_fn = p.lse && f.dq_lse ? f.dq_lse : f.dq;
+  if ((rc = raise_lds(dq_fn, f.dq_lds))) return rc;
   void* args[] = {(void*)&pc, (void*)&gc, (void*)&qrec, (void*)&nq};
-  hipError_t e = hipLaunchKernel(f.dq, qgrid, dim3(kBwdNW * 64), args, (size_t)f.dq_lds, s);
+  hipError_t e = hipLaunchKernel(dq_fn, qgrid, dim3(kBwdNW * 64), args, (size_t)f.dq_lds, s);
   if (e != hipSuccess) return (int)e;
   // 2. dK / dV, context keys then main keys in one launch
   void* kargs[] = {(void*)&pc, (void*)&gc, (void*)&n_ctx, (void*)&krec, (void*)&nk};

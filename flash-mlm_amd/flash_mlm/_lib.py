@@ -97,6 +97,7 @@ class AttnParams(ctypes.Structure):
         ("ctx_page_stride", _c_i64),
         ("ctx_pages_per_batch", _c_i32),
         ("tile_config", _c_i32),
+        ("lse", _c_ptr),
     ]
 
 

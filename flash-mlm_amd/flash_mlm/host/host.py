@@ -17,6 +17,7 @@ the padded prefill length; the HIP kernel picks its own tiles from the head dim.
 
 from __future__ import annotations
 
+import threading
 import warnings
 import weakref
 
@@ -90,20 +91,35 @@ def _workspace(inference_cache: InferenceCache | None, nbytes: int, device: torc
     return torch.empty((1, nbytes), dtype=torch.uint8, device=device)
 
 
+# Set while a forward runs whose backward will follow (_Attention.forward): the launch
+# then has the kernels store each row's log2-sum-exp, which the backward reads instead of
+# recomputing it.
+_ROW_STATS = threading.local()
+
+
 class AttnLaunch:
     """A prepared fmlm_attn_fwd call: the parameter block plus the tensors it points to."""
 
-    __slots__ = ("lib", "params", "stream", "device", "keep", "unpack_kv")
+    __slots__ = ("lib", "params", "stream", "device", "keep", "unpack_kv", "lse")
 
     def __init__(self, lib, params, stream, device, keep):
         self.lib, self.params, self.stream, self.device, self.keep = lib, params, stream, device, keep
         # (B, N, H, kv_heads, rows, cu_q) when the kernel read packed copies of padded
         # K/V (causal_query_seq_attn): the backward unpacks their gradient
         self.unpack_kv = None
+        self.lse = None  # the row statistics of the last run, when it stored them
 
     def __call__(self) -> None:
+        p = self.params
+        # every run sets the field: a parameter block copied from a memo must not carry
+        # an earlier call's buffer
+        self.lse = None
+        p.lse = None
+        if getattr(_ROW_STATS, "on", False) and p.H > 0 and p.total_q > 0:
+            self.lse = torch.empty(p.H * p.total_q, dtype=torch.float32, device=self.device)
+            p.lse = self.lse.data_ptr()
         with _device_scope(self.device):
-            rc = self.lib.fmlm_attn_fwd(self.params, self.stream)
+            rc = self.lib.fmlm_attn_fwd(p, self.stream)
         _lib.check(rc, "fmlm_attn_fwd")
 
 
@@ -241,7 +257,11 @@ class _Attention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, impl, q, k, v, k_cache, v_cache):
-        out, plan = impl()
+        _ROW_STATS.on = True
+        try:
+            out, plan = impl()
+        finally:
+            _ROW_STATS.on = False
         ctx.plan = plan
         # saved so that autograd rejects a backward after any of them changed in place
         ctx.save_for_backward(out, q, k, v, k_cache, v_cache)

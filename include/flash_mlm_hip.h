@@ -246,6 +246,14 @@ typedef struct fmlm_attn_params {
    * while the other issues MFMAs.  Replaces the reference's autotuned
    * BLOCK_M / BLOCK_N / num_warps (mlm_kernel.py:57-166).  Ignored by f32 inputs.       */
   int32_t tile_config;
+  /* Row statistics for the backward: NULL, or H * total_q floats that fmlm_attn_fwd fills
+   * with each real query row's log2-sum-exp, row p of sequence b and head h at
+   * h * total_q + q0_b + p (q0_b = cu_seqlens_q[b], or b * N without cu_seqlens_q):
+   * log2(sum over its keys of 2^z), z = scale * log2(e) * q.k as the forward kernel
+   * computes it (fp32 accumulation); +inf for a row without keys.
+   * fmlm_attn_bwd given the same block reads it instead of recomputing it.  No
+   * counterpart in the reference, whose kernels return o only.                        */
+  float* lse;
 } fmlm_attn_params;
 
 /* Bytes of device workspace (and of a schedule buffer) fmlm_attn_fwd needs for these

@@ -27,6 +27,16 @@ def attend(q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float) -> np.ndar
     return p @ V
 
 
+def row_lse2(q: np.ndarray, K: np.ndarray, scale: float) -> np.ndarray:
+    """log2 of sum_j 2^(z_j) with z = scale * log2(e) * q K^T, per row of q [L, D] against
+    K [M, D] (M >= 1), in float64: logsumexp(scale q K^T) / ln 2, the row statistic the
+    forward stores for the backward (an extension: the reference's kernels return o
+    only).  Then attend(q, K, V) = sum_j 2^(z_j - lse) V_j."""
+    s = (q.astype(np.float64) @ K.astype(np.float64).T) * float(scale)
+    m = s.max(axis=1)
+    return (m + np.log(np.exp(s - m[:, None]).sum(axis=1))) / np.log(2.0)
+
+
 def attend_backward(q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float, dO: np.ndarray):
     """Gradients of ``attend`` for an upstream gradient dO [L, D]: returns (dq, dK, dV) in
     float64.  With P = softmax(scale q K^T) and O = P V:
@@ -83,8 +93,27 @@ def mlm_attention_packed(
     ``context_index`` (index-mapped context batching, an extension the reference lists on
     its roadmap, README.md:34-36) sets ``cb = context_index[b]`` instead.
     """
+    return _mlm_packed(q, k, v, lengths, scale, is_mla, causal_query_seq_attn, prefill, k_cache, v_cache,
+                       cu_seqlens_kv, total_context_len, context_batch_size, context_index, attend)
+
+
+def mlm_row_lse2_packed(q, k, lengths, scale, *, is_mla=False, causal_query_seq_attn=False, prefill=False,
+                        k_cache=None, cu_seqlens_kv=None, total_context_len=0, context_batch_size=1,
+                        context_index=None) -> np.ndarray:
+    """row_lse2 of every real query row over the key set of mlm_attention_packed (same
+    arguments, values unused): [B, H, N], zeros at padding positions."""
+    def lse(qq, K, V, sc):
+        return row_lse2(qq, K, sc)[:, None]
+
+    return _mlm_packed(q, k, k, lengths, scale, is_mla, causal_query_seq_attn, prefill, k_cache, k_cache,
+                       cu_seqlens_kv, total_context_len, context_batch_size, context_index, lse)[..., 0]
+
+
+def _mlm_packed(q, k, v, lengths, scale, is_mla, causal_query_seq_attn, prefill, k_cache, v_cache, cu_seqlens_kv,
+                total_context_len, context_batch_size, context_index, fn):
+    """fn(q rows, K_all, V_all, scale) -> [L, W] over each (sequence, head)'s key set."""
     B, H, N, D = q.shape
-    out = np.zeros((B, H, N, D), dtype=np.float64)
+    out = None
     cu_kv = None if cu_seqlens_kv is None else np.asarray(cu_seqlens_kv, dtype=np.int64)
     for b in range(B):
         Lq = int(lengths[b])
@@ -109,8 +138,11 @@ def mlm_attention_packed(
                 V_all = np.concatenate([V_ctx, V_main])
             else:
                 K_all, V_all = K_main, V_main
-            out[b, h, :Lq] = attend(q[b, h, :Lq], K_all, V_all, scale)
-    return out
+            r = fn(q[b, h, :Lq], K_all, V_all, scale)
+            if out is None:
+                out = np.zeros((B, H, N, r.shape[1]), dtype=np.float64)
+            out[b, h, :Lq] = r
+    return np.zeros((B, H, N, D), dtype=np.float64) if out is None else out
 
 
 def mlm_attention_packed_backward(
@@ -257,8 +289,25 @@ def mlm_attention_dense(
     else 0 (mlm_kernel_impl.py:132-141), or ``context_index[b]`` when given (the
     extension above).  MLA keeps per-head main keys and V = K.
     """
+    return _mlm_dense(q, k, v, scale, is_mla, prefill, k_cache, v_cache, context_len, context_batch_size,
+                      context_index, attend)
+
+
+def mlm_row_lse2_dense(q, k, scale, *, is_mla=False, prefill=False, k_cache=None, context_len=0,
+                       context_batch_size=1, context_index=None) -> np.ndarray:
+    """row_lse2 of every query row over the key set of mlm_attention_dense: [B, H, N]."""
+    def lse(qq, K, V, sc):
+        return row_lse2(qq, K, sc)[:, None]
+
+    return _mlm_dense(q, k, k, scale, is_mla, prefill, k_cache, k_cache, context_len, context_batch_size,
+                      context_index, lse)[..., 0]
+
+
+def _mlm_dense(q, k, v, scale, is_mla, prefill, k_cache, v_cache, context_len, context_batch_size, context_index,
+               fn):
+    """fn(q rows, K_all, V_all, scale) -> [N, W] over each (sequence, head)'s key set."""
     B, H, N, D = q.shape
-    out = np.zeros((B, H, N, D), dtype=np.float64)
+    out = None
     for b in range(B):
         cb = int(context_index[b]) if context_index is not None else (b if context_batch_size > 1 else 0)
         for h in range(H):
@@ -272,8 +321,11 @@ def mlm_attention_dense(
                 V_all = np.concatenate([V_ctx, V_main])
             else:
                 K_all, V_all = K_main, V_main
-            out[b, h] = attend(q[b, h], K_all, V_all, scale)
-    return out
+            r = fn(q[b, h], K_all, V_all, scale)
+            if out is None:
+                out = np.zeros((B, H, N, r.shape[1]), dtype=np.float64)
+            out[b, h] = r
+    return np.zeros((B, H, N, D), dtype=np.float64) if out is None else out
 
 
 def effective_flops(lengths_q, lengths_ctx, num_heads: int, head_dim: int, *, causal_query_seq_attn=False, prefill=False) -> float:

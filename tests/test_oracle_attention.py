@@ -203,3 +203,53 @@ def test_effective_flops_formula():
     assert ar.effective_flops([2, 3], [5, 1], 2, 4, causal_query_seq_attn=True) == 4 * 2 * 4 * (2 * 7 + 3 * 6)
     assert ar.effective_flops([2, 3], [5, 1], 2, 4, prefill=True) == 4 * 2 * 4 * (2 * 2 + 3 * 3)
     assert ar.effective_flops([2, 3], 4, 1, 1) == 4 * (2 * 6 + 3 * 7)
+
+
+def test_row_lse2_closed_forms():
+    """row_lse2 (the forward's row statistic for the backward) against what the
+    mathematics fixes: one key gives its own score in log2 units, M equal keys add
+    log2(M), and 2^(z - lse) are the softmax weights, so they reproduce attend()."""
+    rng = np.random.default_rng(11)
+    q, K, V = _rand(rng, 5, 8), _rand(rng, 7, 8), _rand(rng, 7, 8)
+    scale = 0.41
+    z = (q.astype(np.float64) @ K.astype(np.float64).T) * scale / np.log(2.0)  # log2 units
+    np.testing.assert_allclose(ar.row_lse2(q, K[:1], scale), z[:, 0], rtol=0, atol=1e-12)
+    K3 = np.repeat(K[2:3], 3, axis=0)
+    np.testing.assert_allclose(ar.row_lse2(q, K3, scale), z[:, 2] + np.log2(3.0), rtol=0, atol=1e-12)
+    lse = ar.row_lse2(q, K, scale)
+    w = np.exp2(z - lse[:, None])
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, atol=1e-12)
+    np.testing.assert_allclose(w @ V.astype(np.float64), ar.attend(q, K, V, scale), atol=1e-12)
+    # brute force on the explicit sum, for scores far from 0 (no overflow in float64)
+    q40 = q.astype(np.float64) * 40
+    big = ar.row_lse2(q40, K, scale)
+    zb = (q40 @ K.astype(np.float64).T) * scale / np.log(2.0)
+    np.testing.assert_allclose(big, np.log2(np.exp2(zb).sum(axis=1)), rtol=1e-12)
+
+
+@pytest.mark.parametrize("mla", [False, True])
+@pytest.mark.parametrize("causal", [False, True])
+def test_row_lse2_packed_and_dense_on_explicit_key_sets(mla, causal):
+    rng = np.random.default_rng(21 + mla + 2 * causal)
+    c = _packed_case(rng, mla=mla)
+    scale = 0.37
+    got = ar.mlm_row_lse2_packed(c["q"], c["k"], c["L"], scale, is_mla=mla, causal_query_seq_attn=causal,
+                                 k_cache=c["kc"], cu_seqlens_kv=c["cu_kv"], total_context_len=c["Tc"],
+                                 context_batch_size=c["cbs"])
+    B, H, N, _ = c["q"].shape
+    for b in range(B):
+        for h in range(H):
+            K, _ = _keys_for(c, b, h, mla=mla, causal=causal, prefill=False)
+            np.testing.assert_allclose(got[b, h, : c["L"][b]], ar.row_lse2(c["q"][b, h, : c["L"][b]], K, scale),
+                                       atol=1e-12)
+        assert np.all(got[b, :, c["L"][b]:] == 0)
+    # dense: every query sees [context || its own N keys]
+    q, k = c["q"], c["k"]
+    Lc = 3
+    kc = _rand(rng, B * Lc, 8) if mla else _rand(rng, B * H * Lc, 8)
+    got = ar.mlm_row_lse2_dense(q, k, scale, is_mla=mla, k_cache=kc, context_len=Lc, context_batch_size=B)
+    for b in range(B):
+        for h in range(H):
+            start = b * Lc if mla else (b * H + h) * Lc
+            K = np.concatenate([kc[start:start + Lc], k[b, h]])  # MLA keeps per-head main keys
+            np.testing.assert_allclose(got[b, h], ar.row_lse2(q[b, h], K, scale), atol=1e-12)
