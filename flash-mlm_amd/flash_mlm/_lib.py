@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libflash_mlm_hip.so"
 _LIB_PATH = Path(os.environ.get("FMLM_LIB_PATH", Path(__file__).resolve().parent / "_native" / LIB_NAME))
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_BF16 = 0
 DTYPE_F16 = 1

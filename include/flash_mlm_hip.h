@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FMLM_ABI_VERSION 4
+#define FMLM_ABI_VERSION 5
 
 /* element types */
 enum {
