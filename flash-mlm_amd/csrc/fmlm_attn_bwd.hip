@@ -653,7 +653,7 @@ struct QuerySteps {
 // ---------------------------------------------------------------------------
 // dq kernel: grid (query-tile units, H), kBwdNW waves, QB blocks of 16 rows per wave.
 // LSE: the forward stored each row's log2-sum-exp (p.lse), so P = 2^(z - lse) needs no
-// running max, no row sum and no rescale (the software-pipelined tiles only).
+// running max, no row sum and no rescale.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LSE>
 __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kernel(const fmlm_attn_params p,
@@ -798,9 +798,8 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
   //   dq = scale / l * sum_j 2^(z_j - m) (dP_j - delta) k_j,
   // so dq^T accumulates K^T (2^(z - m) (dP - delta))^T like the forward's O^T and is
   // rescaled with l whenever m moves (lazily: by more than kRescaleSlack).  With LSE,
-  // m = lse and l = 1 throughout: -lse starts the S^T accumulators and -delta the dP^T
-  // ones, so the MFMAs yield z - lse and dP - delta.
-  static_assert(!LSE || (!C::PAD && C::DQ_NBUF == 2), "LSE: pipelined tiles only");
+  // m = lse and l = 1 throughout; in the software-pipelined tiles -lse starts the S^T
+  // accumulators and -delta the dP^T ones, so the MFMAs yield z - lse and dP - delta.
   f32x4 dq[C::NDB][QB];
 #pragma unroll
   for (int db = 0; db < C::NDB; ++db)
@@ -1012,6 +1011,18 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) dp[kb][qb] = Mfma<T>::run(a, df[qb][kc], dp[kb][qb]);
       }
+    if constexpr (LSE) {
+      if (nk < kBwdBK) {  // a partial tile: keys past its end to -inf (P = 0)
+        asm volatile("");  // (a real branch: full tiles skip the selects)
+#pragma unroll
+        for (int kb = 0; kb < C::NKB; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (kb * 16 + gq * 4 + r >= nk) s[kb][qb][r] = -INFINITY;
+      }
+    } else {
     // running max (row-uniform after the xor steps) and lazy rescale
     bool grow_any = false;
     float m_new[QB];
@@ -1042,12 +1053,14 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
         for (int db = 0; db < C::NDB; ++db) dq[db][qb] *= alpha;
       }
     }
+    }
     // 2^(z - m) (dP - delta), packed as B operands: element 4h + r of step ks is key
     // 32ks + 16h + 4g + r
     v8 dsf[C::NKS][QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const float mref = m_i[qb] == -INFINITY ? 0.f : m_i[qb];  // no key yet: every z is -inf
+      // no key yet: every z is -inf (LSE: m is the row's statistic, +inf for padding rows)
+      const float mref = !LSE && m_i[qb] == -INFINITY ? 0.f : m_i[qb];
       float rs = 0.f;
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb)
@@ -1057,7 +1070,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dq_kerne
           rs += pv;
           dsf[kb >> 1][qb][(kb & 1) * 4 + r] = (T)(pv * (dp[kb][qb][r] - delta[qb]));
         }
-      l_i[qb] += rs;
+      if (!LSE) l_i[qb] += rs;
     }
 #pragma unroll
     for (int ks = 0; ks < C::NKS; ++ks)
@@ -1819,7 +1832,9 @@ static BwdFns bwd_fns() {
            C::DKV_LDS,
            C::BQ,
            C::DKV_KEYS};
-  if constexpr (!C::PAD && C::DQ_NBUF == 2) f.dq_lse = (const void*)attn_bwd_dq_kernel<T, D, true>;
+  // not for the 512-wide latent: at one wave per SIMD its allocation without the running
+  // max (208 VGPRs + 144 AGPRs against 256 + 218) ran 14% slower
+  if constexpr (!C::MLA_ONLY) f.dq_lse = (const void*)attn_bwd_dq_kernel<T, D, true>;
   return f;
 }
 
