@@ -1336,6 +1336,17 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
       f32x4 sc[NRB][KB], dp[NRB][KB], L4[NRB], D4[NRB];
       u32x4 pbw[2][KB], dsw[2][KB];
       v8 fr[LEAD + 1];
+      // keys this step does not see (past the segment, or causal: not before cu[b+1]) start
+      // their S^T accumulators at an infinity that the scale turns into -inf, so their P
+      // is 0 without a select per element (a zero scale is replaced by a tiny one, which
+      // leaves every finite score's 2^(s c) at 1 in fp32)
+      const float cm = c != 0.f ? c : 1e-30f;
+      f32x4 kin4[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const float kin = (kok[kb] && key[kb] < lim) ? 0.f : cm > 0.f ? -INFINITY : INFINITY;
+        kin4[kb] = f32x4{kin, kin, kin, kin};
+      }
       auto issue = [&](int r) {
         if (r < NR) {
           const int rb = r / RBS, kc = (r % RBS) >> 1;
@@ -1352,11 +1363,10 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
           pin(sc[rb][kb]);
           pin(dp[rb][kb]);
         }
-        const bool kvalid = kok[kb] && key[kb] < lim;
         f32x2 pv, ds;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          pv[i] = kvalid ? fast_exp2(fmaf(sc[rb][kb][r + i], c, -L4[rb][r + i])) : 0.f;
+          pv[i] = fast_exp2(fmaf(sc[rb][kb][r + i], cm, -L4[rb][r + i]));  // masked keys: 2^-inf = 0
           ds[i] = pv[i] * fmaf(dp[rb][kb][r + i], p.scale, -D4[rb][r + i]);
         }
         uint32_t wp = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv, typename Pair<T>::type));
@@ -1383,7 +1393,7 @@ __global__ __launch_bounds__(kBwdNW * 64, BwdCfg<D>::WPS) void attn_bwd_dkv_kern
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
             if ((sl & 1) == 0)
-              sc[rb][kb] = Mfma<T>::run(a, kf[kb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[rb][kb]);
+              sc[rb][kb] = Mfma<T>::run(a, kf[kb][kc], kc == 0 ? kin4[kb] : sc[rb][kb]);
             else
               dp[rb][kb] = Mfma<T>::run(a, vf[kb][kc], kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dp[rb][kb]);
           }

@@ -508,3 +508,32 @@ def test_backward_more_sequences_than_the_rank_limit(causal, device):
     _close(q.grad, g[0], "dq")
     _close(k.grad, g[1], "dk")
     _close(v.grad, g[2], "dv")
+
+
+@pytest.mark.parametrize("scale", [-0.2, 0.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_non_positive_scale(scale, causal, device):
+    """A negative or zero softmax scale (the entry points pass any float through): keys a
+    query does not see must still get P = 0 in every kernel, whatever sign the scale gives
+    their masked scores."""
+    gen = torch.Generator().manual_seed(7400 + int(scale * 10) + causal)
+    lengths = [70, 1, 0, 133, 40]
+    B, H, N, D, dtype = len(lengths), 2, 140, 64, torch.bfloat16
+    q, k, v = (_leaf((B, H, N, D), dtype, device, gen) for _ in range(3))
+    cache, kc, vc, cu_kv, total = _packed_cache([129, 0, 64, 7, 90], H=H, D=D, mla=False, dtype=dtype,
+                                                device=device, gen=gen)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0, block_n=64, causal_query_seq_attn=causal)
+    dout = torch.randn(out.shape, generator=gen).to(dtype).to(device)
+    out.backward(dout)
+    from flash_mlm import unpack_from_kernel
+    g = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)), lengths, scale, k_cache=_np(kc),
+        v_cache=_np(vc), cu_seqlens_kv=cu_kv, total_context_len=total, context_batch_size=B,
+        causal_query_seq_attn=causal)
+    names = ("dq", "dk", "dv", "dk_cache", "dv_cache")
+    for got, ref, name in zip((q.grad, k.grad, v.grad, kc.grad, vc.grad), g, names):
+        if scale == 0.0 and name in ("dq", "dk", "dk_cache"):  # dS = scale * ... = 0
+            assert float(got.abs().max()) == 0.0, name
+            continue
+        _close(got, ref, name)
