@@ -331,29 +331,33 @@ FMLM_DEV UnitTables unit_tables(const fmlm_attn_params& p, const fmlm_attn_grads
 
 constexpr int kScanThreads = 1024;
 
-// exclusive prefix sums of ceil(len / tile) over n entries, one workgroup
+// exclusive prefix sums of ceil(len / tile) over n entries, one workgroup: each thread
+// sums a run of entries, the runs are scanned within each wave by lane shuffles, and each
+// wave adds the totals of the waves before it (two barriers, where a scan over all
+// kScanThreads partial sums took twenty)
 template <typename LenFn>
 FMLM_DEV void scan_tiles(int n, int tile, LenFn len, int32_t* out, int32_t* part) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (n + kScanThreads - 1) / kScanThreads;
   const int i0 = min(tid * per, n), i1 = min(i0 + per, n);
   int sum = 0;
   for (int i = i0; i < i1; ++i) sum += (max(len(i), 0) + tile - 1) / tile;
-  part[tid] = sum;
-  __syncthreads();
-  for (int off = 1; off < kScanThreads; off <<= 1) {  // inclusive Hillis-Steele scan
-    const int v = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
+  int incl = sum;  // inclusive scan within the wave
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off);
+    if (lane >= off) incl += v;
   }
-  int run = tid > 0 ? part[tid - 1] : 0;
+  if (lane == 63) part[wave] = incl;  // wave totals
+  __syncthreads();
+  int run = incl - sum;
+  for (int w = 0; w < wave; ++w) run += part[w];
   for (int i = i0; i < i1; ++i) {
     out[i] = run;
     run += (max(len(i), 0) + tile - 1) / tile;
   }
-  if (tid == kScanThreads - 1) out[n] = part[tid];
-  __syncthreads();
+  if (tid == kScanThreads - 1) out[n] = run;  // the last thread's run ends at the total
+  __syncthreads();  // part is rewritten by the next scan
 }
 
 // keys a query row of sequence b attends to (context, then its own or causal main keys)
