@@ -3,7 +3,8 @@ real query row's log2-sum-exp, which the forward stores when a backward will fol
 which fmlm_attn_bwd then reads instead of recomputing).  Every forward kernel is covered:
 the pipelined MFMA kernel (dense and packed, unsplit and split key ranges, where
 merge_kernel writes the statistic), the 512-wide MLA kernel (head-packed tiles and dense
-rows) and the fp32 SIMT kernel.  Reference: the float64 oracle's row_lse2
+rows), the fp32 SIMT kernel, and the paged-context instantiations (bit-equal to the same
+context stored contiguously).  Reference: the float64 oracle's row_lse2
 (oracle/attention_ref.py), pinned by closed forms in test_oracle_attention.py.
 
 Tolerance, in log2 units: |gpu - ref| <= 2e-2 + 2e-3 |ref|.  The kernels round
@@ -159,3 +160,51 @@ def test_backward_with_and_without_statistics_agree(D, device):
         err = float(np.abs(a - b).max())
         print(f"{name}: max |with - without| / max = {err / scale:.2e}")
         assert err <= 1e-2 * scale, name
+
+
+@pytest.mark.parametrize("mla,D", [(True, 512), (False, 128)])
+def test_row_stats_paged_context_equal_contiguous(mla, D, device):
+    """The paged instantiations (MLA: its own LSE instantiation) store the same statistics,
+    bit for bit, as the same context stored contiguously, and match the oracle."""
+    from oracle import pack_ref
+    PAGE = 64
+    lens = [65, 200, 3]
+    g = torch.Generator().manual_seed(8100 + D)
+    H, dtype = 2, torch.bfloat16
+    h_kv = 1 if mla else H
+    need = [(n + PAGE - 1) // PAGE for n in lens]
+    P = sum(need) + 2
+    perm = torch.randperm(P, generator=g)
+    bt = torch.full((len(lens), max(need)), -1, dtype=torch.int32)
+    i = 0
+    for c, n in enumerate(need):
+        bt[c, :n] = perm[i:i + n]
+        i += n
+    kp = (torch.randn((h_kv, P, PAGE, D), generator=g) * 0.5).to(dtype).to(device)
+    vp = None if mla else (torch.randn((h_kv, P, PAGE, D), generator=g) * 0.5).to(dtype).to(device)
+    paged = InferenceCache()
+    paged.prefill_paged_kv_cache(0, k_pages=kp, v_pages=vp, block_table=bt.to(device),
+                                 context_lens=torch.tensor(lens, dtype=torch.int32), is_mla=mla, num_heads=H, head_dim=D)
+    kc, cu = pack_ref.gather_pages(_np(kp).transpose(1, 0, 2, 3), bt.numpy(), lens)
+    vc = None if mla else pack_ref.gather_pages(_np(vp).transpose(1, 0, 2, 3), bt.numpy(), lens)[0]
+    flat = InferenceCache()
+    flat.prefill_kv_cache(0, k_cache=torch.from_numpy(kc).to(dtype).to(device),
+                          v_cache=None if mla else torch.from_numpy(vc).to(dtype).to(device),
+                          total_context_len=int(cu[-1]), cu_seqlens_kv=torch.from_numpy(cu).to(torch.int32).to(device),
+                          context_batch_size=len(lens), is_mla=mla, num_heads=H, head_dim=D)
+    lengths = [40, 130, 7]
+    B, N = len(lengths), 130
+    q, k, v = (_leaf((B, H, N, D), dtype, device, g) for _ in range(3))
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    stats = []
+    for cache in (paged, flat):
+        out = flash_attn_mlm_compressed(q, k, k if mla else v, H, meta, 1.0 / math.sqrt(D), cache, 0, is_mla=mla,
+                                        block_n=64)
+        stats.append(out.grad_fn.plan.lse.clone())
+    assert torch.equal(stats[0], stats[1])
+    ref = ar.mlm_row_lse2_packed(_np(q), _np(k), lengths, 1.0 / math.sqrt(D), is_mla=mla, k_cache=kc,
+                                 cu_seqlens_kv=cu, total_context_len=int(cu[-1]), context_batch_size=B)
+    plan = out.grad_fn.plan
+    got = _gpu_rows(plan, lengths, np.concatenate([[0], np.cumsum(lengths)]))
+    for b, L in enumerate(lengths):
+        _check(got[b], ref[b, :, :L], f"b={b}")
