@@ -1701,7 +1701,10 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
           if (h == 1)  // half 0's P, computed against the old maximum
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              typename Pair<T>::type v = __builtin_bit_cast(typename Pair<T>::type, pf[0][e]);
+              // element e through a local: a __builtin_bit_cast of the vector element
+              // itself compiles (clang of ROCm 7.2) to a read of element 0
+              const uint32_t u = pf[0][e];
+              typename Pair<T>::type v = __builtin_bit_cast(typename Pair<T>::type, u);
               const f32x2 x = __builtin_convertvector(v, f32x2) * alpha;
               pf[0][e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
             }

@@ -1142,6 +1142,38 @@ def test_mla_latent512_rising_scores(dtype, device):
     _close(unpack_from_kernel(out, meta, H), ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mla_latent512_rescale_inside_tile(dtype, device):
+    """A tile's second half raises the maximum of some rows of a wave by ~10 (log2 units),
+    past the rescale slack, and leaves the others' (so the whole wave rescales, with
+    factor 1 on those rows): the first half's P, computed against the old maximum, must
+    keep each of its elements.  Its keys carry scores of +2 (keys 4g, 4g+1 of the first
+    16-key block) and -2 (the rest), so P elements that trade places show, in the
+    output's dim 1 (the latent is V: dim 1 holds the +-8 that set those scores)."""
+    torch.manual_seed(3200)
+    lengths = [64, 100]
+    B, H, N, D = len(lengths), 2, 100, 512
+    q = _randn((B, H, N, D), device, dtype, std=0.5)
+    k = _randn((B, H, N, D), device, dtype, std=0.5)
+    # dim d adds q_d * k_d * scale * log2(e) = 0.255 * k_d (log2 units) for q_d = 4
+    q[:, :, 0::2, 0] = 4.0  # even positions see key 40's boost, odd ones do not
+    q[:, :, 1::2, 0] = 0.0
+    q[..., 1] = 4.0
+    key = torch.arange(N, device=device)
+    k0 = torch.zeros(N, device=device)
+    k0[32:64] = -40.0
+    k0[40] = 48.0  # +12.2 on even positions: their maximum rises by ~10 in the second half
+    k1 = torch.where((key < 16) & (key % 4 < 2), 8.0, -8.0)
+    k1[32:] = 0.0
+    k[:, 0, :, 0] = k0.to(dtype)  # MLA: head 0 of k is the latent
+    k[:, 0, :, 1] = k1.to(dtype)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    scale = 1.0 / math.sqrt(D)
+    out = flash_attn_mlm_compressed(q, k, k, H, meta, scale, is_mla=True, block_n=64)
+    ref = _packed_oracle(q, k, k, lengths, scale, is_mla=True)
+    _close(unpack_from_kernel(out, meta, H), ref)
+
+
 @pytest.mark.parametrize("cbs", [1, 2])
 def test_mla_latent512_dense(cbs, device):
     torch.manual_seed(3100 + cbs)
