@@ -1554,20 +1554,22 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
                                              : (int64_t)w.b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)pq * p.o_sn;
   }
 
-  // ---- Q^T fragments (B operand of S^T = K Q^T) for step kc, pre-scaled by
-  // scale*log2(e) (one rounding to the input type): S comes out in log2 units
-  const float cs = p.scale * kLog2e;
+  // ---- Q^T fragments (B operand of S^T = K Q^T) for step kc, as stored but for the
+  // sign of a negative scale.  Scores in log2 units are c * (K Q^T), c = |scale|*log2(e),
+  // applied in fp32 by the FMA that subtracts the running max (as the reference scales
+  // the fp32 product; a Q pre-scaled in the input type would round each q*c to 8 bits at
+  // bf16).  The floor keeps -inf * c == -inf for masked keys at scale 0.
+  const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
+  const float c = fmaxf(fabsf(p.scale) * kLog2e, 1e-30f);
   v8 qf[C::KC];
   {
     const bool ok = row < w.qcount;
     const char* src = (const char*)p.q + q_off * 2;
 #pragma unroll
     for (int kc = 0; kc < C::KC; ++kc) {
-      v8 raw = v8{};
-      if (ok) raw = *(const v8*)(src + (kc * 32 + g * 8) * 2);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) raw[e] = (T)((float)raw[e] * cs);
-      qf[kc] = raw;
+      u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+      if (ok) raw = *(const u32x4*)(src + (kc * 32 + g * 8) * 2);
+      qf[kc] = __builtin_bit_cast(v8, raw ^ qsign);
     }
   }
   // ---- per-lane LDS offsets (kv_swz layout, 1 KiB rows): the K fragment of block kb,
@@ -1668,7 +1670,7 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
       // P of key block kb, keys 4g + r and 4g + r + 1 (r even), against the running max
       auto exp_pair = [&](int kb, int r, bool add_l) {
         if (r == 0) pin(s[kb]);
-        f32x2 x = f32x2{fast_exp2(s[kb][r] - m_i), fast_exp2(s[kb][r + 1] - m_i)};
+        f32x2 x = f32x2{fast_exp2(fmaf(s[kb][r], c, -m_i)), fast_exp2(fmaf(s[kb][r + 1], c, -m_i))};
         if (add_l) l_i += x[0] + x[1];
         uint32_t wv = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
         pin(wv);
@@ -1689,7 +1691,7 @@ __global__ __launch_bounds__(MlaRowsCfg::NT, 1) void attn_mla_rows_kernel(
         }
         float mx = vmax(vmax(vmax(s[2 * h][0], s[2 * h][1]), vmax(s[2 * h][2], s[2 * h][3])),
                         vmax(vmax(s[2 * h + 1][0], s[2 * h + 1][1]), vmax(s[2 * h + 1][2], s[2 * h + 1][3])));
-        mx = lane_max_xor16_32(mx);
+        mx = lane_max_xor16_32(mx) * c;  // log2 units (c > 0)
         const bool grow = mx > m_i + kRescaleSlack;
         if (__builtin_amdgcn_ballot_w64(grow)) {
           const float m_new = grow ? mx : m_i;

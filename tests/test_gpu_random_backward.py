@@ -1,0 +1,119 @@
+"""Seeded random sweep of the attention backward against the float64 oracle
+(oracle/attention_ref.py mlm_attention_packed_backward, pinned by finite differences):
+random batch shapes, lengths (empty sequences included), per-batch contexts, head dims
+(the 512-wide latent included), MLA, causal_query_seq_attn and dtypes; half of the cases
+add per-key score offsets (q[..., 0] = 4, k[..., 0] drawn per key; fp16 only) so the
+forward's row statistics, which the backward reads, come out of rescales.  Tolerance as in
+test_gpu_backward.py: |gpu - ref| <= TOL * max|ref| + TOL * |ref| per gradient, TOL = 2e-2.
+Inputs are std 0.5 (the forward's pre-scaled Q keeps bf16 inside the budget there)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flash_mlm import InferenceCache, build_pack_metadata, flash_attn_mlm_compressed, unpack_from_kernel
+from oracle import attention_ref as ar
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _close(got, ref, what):
+    got = _np(got)
+    scale = float(np.abs(ref).max()) if ref.size else 0.0
+    if scale == 0.0:
+        assert float(np.abs(got).max()) == 0.0, f"{what}: nonzero gradient where the reference is zero"
+        return
+    err = np.abs(got - ref)
+    worst = float((err - (TOL * scale + TOL * np.abs(ref))).max())
+    assert worst <= 0, f"{what}: max err {float(err.max()):.3e} (ref max {scale:.3e})"
+
+
+@pytest.mark.parametrize("seed", list(range(12)))
+def test_random_backward_packed(seed, device):
+    rng = np.random.default_rng(9500 + seed)
+    gen = torch.Generator().manual_seed(9500 + seed)
+    D = int(rng.choice([32, 64, 128, 256, 512]))
+    mla = D == 512 or bool(rng.random() < 0.3)
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+    causal = bool(rng.random() < 0.35)
+    # offsets only at fp16: the forward and dq kernels below the latent round q * scale
+    # to the input type, which at bf16 tilts P by up to ~3% for scores of ~20 (log2
+    # units), and dq's cancelling sum amplifies that past the budget
+    spike = bool(rng.random() < 0.5) and dtype == torch.float16
+    small = D == 512  # the latent's oracle and kernels are the slow ones
+    B = int(rng.integers(1, 3 if small else 5))
+    H = int(rng.integers(1, 3 if small else 4))
+    lengths = [int(x) for x in rng.integers(0, 90 if small else 150, size=B)]
+    if max(lengths) == 0:
+        lengths[0] = 1
+    N = max(lengths)
+    use_ctx = bool(rng.random() < 0.6)
+    heads = 1 if mla else H
+
+    def leaf(shape, extra=None):
+        t = torch.randn(shape, generator=gen) * 0.5
+        if extra is not None:
+            extra(t)
+        return t.to(dtype).to(device).requires_grad_()
+
+    def q_spike(t):
+        t[..., 0] = 4.0
+
+    k0 = torch.from_numpy(rng.uniform(-30.0, 30.0, size=(B, N))).float()
+
+    def k_spike(t):
+        if mla:
+            t[:, 0, :, 0] = k0
+        else:
+            t[..., 0] = k0[:, None, :]
+
+    q = leaf((B, H, N, D), q_spike if spike else None)
+    k = leaf((B, H, N, D), k_spike if spike else None)
+    v = leaf((B, H, N, D))
+    cache, kc, vc, cu_kv, total = None, None, None, None, 0
+    if use_ctx:
+        ctx = [int(x) for x in rng.integers(0, 90 if small else 150, size=B)]
+        ctx[0] = max(ctx[0], 1)
+        cu_kv = np.concatenate([[0], np.cumsum(ctx)]).astype(np.int32)
+        total = int(cu_kv[-1])
+        c0 = torch.from_numpy(rng.uniform(-30.0, 30.0, size=heads * total)).float()
+
+        def kc_spike(t):
+            t[:, 0] = c0
+
+        kc = leaf((heads * total, D), kc_spike if spike else None)
+        vc = None if mla else leaf((heads * total, D))
+        cache = InferenceCache()
+        cache.prefill_kv_cache(0, k_cache=kc, v_cache=vc, total_context_len=total,
+                               cu_seqlens_kv=torch.from_numpy(cu_kv).to(device), context_batch_size=B, is_mla=mla,
+                               num_heads=H, head_dim=D)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device, dtype=torch.int32), N, block_n=64)
+    scale = 1.0 / math.sqrt(D)
+    out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0 if cache is not None else None, is_mla=mla,
+                                    block_n=64, causal_query_seq_attn=causal)
+    dout = (torch.randn(out.shape, generator=gen) * 0.5).to(dtype).to(device)
+    out.backward(dout)
+    g = ar.mlm_attention_packed_backward(
+        _np(q), _np(k), _np(v), _np(unpack_from_kernel(dout, meta, H)), lengths, scale, is_mla=mla,
+        causal_query_seq_attn=causal, k_cache=None if kc is None else _np(kc),
+        v_cache=None if vc is None else _np(vc), cu_seqlens_kv=cu_kv, total_context_len=total,
+        context_batch_size=B)
+    _close(q.grad, g[0], "dq")
+    _close(k.grad, g[1], "dk")
+    if mla:
+        assert v.grad is None
+    else:
+        _close(v.grad, g[2], "dv")
+    if kc is not None:
+        _close(kc.grad, g[3], "dk_cache")
+        if not mla:
+            _close(vc.grad, g[4], "dv_cache")

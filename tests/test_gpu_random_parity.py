@@ -168,3 +168,35 @@ def test_random_long_context_split(seed, device):
     ref = ar.mlm_attention_packed(_np(q), _np(k), _np(v), lengths, scale, k_cache=_np(kc), v_cache=_np(vc),
                                   cu_seqlens_kv=[int(x) for x in cu_kv], total_context_len=Tc, context_batch_size=B)
     np.testing.assert_allclose(_np(unpack_from_kernel(out, meta, H)), ref, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("seed", list(range(4)))
+def test_random_latent512_bf16_large_scores(seed, device):
+    """The 512-wide latent kernel scales scores in fp32 (Q as stored, the scale in the
+    FMA that subtracts the running max), so bf16 inputs of std 2 (scores of std 4), where
+    a Q pre-scaled in bf16 would exceed the budget, stay inside 1e-2."""
+    rng = np.random.default_rng(9300 + seed)
+    torch.manual_seed(9300 + seed)
+    B, H, D = int(rng.integers(1, 4)), int(rng.integers(1, 5)), 512
+    lengths = [int(x) for x in rng.integers(1, 160, size=B)]
+    N = max(lengths)
+    ctx = [int(x) for x in rng.integers(0, 200, size=B)]
+    cu_kv = np.zeros(B + 1, dtype=np.int64)
+    cu_kv[1:] = np.cumsum(ctx)
+    Tc = int(cu_kv[-1])
+    q, k = ((torch.randn((B, H, N, D), device=device) * 2.0).to(torch.bfloat16) for _ in range(2))
+    kc = (torch.randn((max(Tc, 1), D), device=device) * 2.0).to(torch.bfloat16)[:Tc]
+    cache = None
+    if Tc:
+        cache = InferenceCache()
+        cache.prefill_kv_cache(layer_id=0, k_cache=kc, v_cache=kc, total_context_len=Tc,
+                               cu_seqlens_kv=torch.tensor(cu_kv, dtype=torch.int32, device=device),
+                               context_batch_size=B, is_mla=True, num_heads=H, head_dim=D)
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    scale = (-1.0 if seed == 3 else 1.0) / math.sqrt(D)
+    out = flash_attn_mlm_compressed(q, k, k, H, meta, scale, cache, 0 if cache is not None else None, is_mla=True,
+                                    block_n=64)
+    ref = ar.mlm_attention_packed(_np(q), _np(k), _np(k), lengths, scale, is_mla=True,
+                                  k_cache=_np(kc) if Tc else None, cu_seqlens_kv=[int(x) for x in cu_kv] if Tc else None,
+                                  total_context_len=Tc, context_batch_size=B)
+    np.testing.assert_allclose(_np(unpack_from_kernel(out, meta, H)), ref, atol=2e-2, rtol=1e-2)
