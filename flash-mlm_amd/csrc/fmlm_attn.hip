@@ -871,10 +871,19 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15;
   const int g = lane >> 4;
-  // ---- Q fragments (B operand of S^T): lane (q + 16g), block qb, step kc, pre-scaled by
-  // scale*log2(e) (one rounding to the input type) so that S comes out of the MFMAs in
-  // log2 units
+  // ---- Q fragments (B operand of S^T): lane (q + 16g), block qb, step kc.  fp16: pre-scaled
+  // by scale*log2(e) (one rounding to the input type) so that S comes out of the MFMAs in
+  // log2 units.  bf16 (FP32_SCALE): as stored but for the sign of a negative scale, with
+  // c = |scale|*log2(e) applied in fp32 to the accumulators (the running max kept in log2
+  // units, the accumulators' in raw units): bf16's 8-bit mantissa would round q*c to an
+  // error that large scores turn into a tilt of P past the output tolerance, as the
+  // reference's fp32-scaled product does not; fp16's 11 bits keep it below.  The floor
+  // keeps -inf * c == -inf for masked keys at scale 0.
+  constexpr bool FP32_SCALE = std::is_same<T, bf16>::value;
   const float cs = p.scale * kLog2e;
+  const uint32_t qsign = p.scale < 0.f ? 0x80008000u : 0u;
+  const float c = fmaxf(fabsf(p.scale) * kLog2e, 1e-30f);
+  const float rc = 1.f / c;
   v8 qf[QB][C::KC];
   auto load_q = [&]() {
     const char* qbase = (const char*)p.q;
@@ -886,11 +895,17 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
 #pragma unroll
       for (int kc = 0; kc < C::KC; ++kc) {
         const int col = kc * 32 + g * 8;
-        v8 raw = v8{};
-        if (ok && col < D) raw = *(const v8*)(qbase + (off + col) * 2);
+        if constexpr (FP32_SCALE) {
+          u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+          if (ok && col < D) raw = *(const u32x4*)(qbase + (off + col) * 2);
+          qf[qb][kc] = __builtin_bit_cast(v8, raw ^ qsign);
+        } else {
+          v8 raw = v8{};
+          if (ok && col < D) raw = *(const v8*)(qbase + (off + col) * 2);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) raw[e] = (T)((float)raw[e] * cs);
-        qf[qb][kc] = raw;
+          for (int e = 0; e < 8; ++e) raw[e] = (T)((float)raw[e] * cs);
+          qf[qb][kc] = raw;
+        }
       }
     }
   };
@@ -1154,7 +1169,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
     float m_new[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const float m = mx[qb] + sbase[qb];
+      const float m = FP32_SCALE ? fmaf(mx[qb], c, sbase[qb]) : mx[qb] + sbase[qb];
       const bool grow = m > m_i[qb] + kRescaleSlack;
       m_new[qb] = grow ? m : m_i[qb];
       need_rescale = need_rescale || grow;
@@ -1163,7 +1178,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         const float alpha = fast_exp2(m_i[qb] - m_new[qb]);  // 1 where unchanged, 0 on the first tile
-        const float shift = sbase[qb] - m_new[qb];               // 0 where unchanged
+        const float shift = FP32_SCALE ? (sbase[qb] - m_new[qb]) * rc : sbase[qb] - m_new[qb];  // 0 where unchanged
         m_i[qb] = m_new[qb];
         lsum[qb] *= alpha;
 #pragma unroll
@@ -1201,9 +1216,12 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
   auto run_slots = [&](auto s0c, auto s1c, f32x4 (&sc)[C::NKB][QB], f32x4 (&sn)[C::NKB][QB],
                        float (&mx)[QB], uint32_t kn, uint32_t vt) {
     constexpr int S0 = decltype(s0c)::value, S1 = decltype(s1c)::value;
-    f32x4 minit[QB];  // -m_i splat: the initial S accumulators
+    f32x4 minit[QB];  // -m_i splat (in the accumulators' units): the initial S accumulators
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) minit[qb] = f32x4{-m_i[qb], -m_i[qb], -m_i[qb], -m_i[qb]};
+    for (int qb = 0; qb < QB; ++qb) {
+      const float mr = FP32_SCALE ? -m_i[qb] * rc : -m_i[qb];
+      minit[qb] = f32x4{mr, mr, mr, mr};
+    }
     v8 fr[C::LEAD + 1];
     auto issue = [&](int r) {
       if (r < C::NKF) {
@@ -1225,8 +1243,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_mfma3_kernel(
       const int qb = pi / (C::NKB * 2), kb = (pi >> 1) % C::NKB, r = (pi & 1) * 2;
       if (r == 0) pin(sc[kb][qb]);
       f32x2 x = f32x2{sc[kb][qb][r], sc[kb][qb][r + 1]};
-      x[0] = fast_exp2(x[0]);
-      x[1] = fast_exp2(x[1]);
+      x[0] = fast_exp2(FP32_SCALE ? x[0] * c : x[0]);
+      x[1] = fast_exp2(FP32_SCALE ? x[1] * c : x[1]);
       uint32_t wv = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename Pair<T>::type));
       pin(wv);
       pf[kb >> 1][qb][(kb & 1) * 2 + (pi & 1)] = wv;
