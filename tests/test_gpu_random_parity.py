@@ -86,7 +86,7 @@ def test_random_packed(seed, device):
         if kc is not None:
             kc[:, 0] = _spike(q, k, rng, h_kv * Tc, device).to(dtype)
     meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
-    scale = 1.0 / math.sqrt(D)
+    scale = (-1.0 if rng.random() < 0.25 else 1.0) / math.sqrt(D)  # a negative scale flips Q's sign
     out = flash_attn_mlm_compressed(q, k, v, H, meta, scale, cache, 0 if cache is not None else None, is_mla=is_mla,
                                     block_n=64, causal_query_seq_attn=causal,
                                     context_batch_size=1 if ctx_mode == "shared" else None)
@@ -125,7 +125,7 @@ def test_random_dense(seed, device):
         cache = InferenceCache()
         cache.prefill_kv_cache(0, k_cache=kc, v_cache=None if is_mla else vc, context_batch_size=cbs, is_mla=is_mla,
                                num_heads=H, head_dim=D, total_context_len=cbs * C)
-    scale = 1.0 / math.sqrt(D)
+    scale = (-1.0 if rng.random() < 0.25 else 1.0) / math.sqrt(D)
     out = flash_attn_mlm(q, k, v, scale, inference_cache=cache, layer_id=0 if cache is not None else None, is_mla=is_mla)
     assert torch.isfinite(out).all()
     ref = ar.mlm_attention_dense(_np(q), _np(k), _np(v), scale, is_mla=is_mla,
