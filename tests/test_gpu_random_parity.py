@@ -196,3 +196,60 @@ def test_random_latent512_bf16_large_scores(seed, device):
                                   k_cache=_np(kc) if Tc else None, cu_seqlens_kv=[int(x) for x in cu_kv] if Tc else None,
                                   total_context_len=Tc, context_batch_size=B)
     np.testing.assert_allclose(_np(unpack_from_kernel(out, meta, H)), ref, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("seed", list(range(6)))
+def test_random_paged_context(seed, device):
+    """Contexts in a shuffled page pool (InferenceCache.prefill_paged_kv_cache): random
+    lengths, head dims (the 512 latent included), dtypes, inputs up to std 2 and per-key
+    score offsets in the pages, against the oracle over the gathered rows."""
+    from oracle import pack_ref
+
+    page = 64
+    rng = np.random.default_rng(9400 + seed)
+    gen = torch.Generator().manual_seed(9400 + seed)
+    D = int(rng.choice([64, 128, 512]))
+    mla = D == 512 or bool(rng.random() < 0.3)
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+    std = float(rng.choice([0.5, 1.0, 2.0]))
+    spike = bool(rng.random() < 0.5)
+    causal = bool(rng.random() < 0.3)
+    B, H = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+    lengths = [int(x) for x in rng.integers(1, 150, size=B)]
+    N = max(lengths)
+    ctx = [int(x) for x in rng.integers(0, 300, size=B)]
+    ctx[0] = max(ctx[0], 1)
+    h_kv = 1 if mla else H
+    need = [(n + page - 1) // page for n in ctx]
+    P = sum(need) + 2
+    perm = torch.randperm(P, generator=gen)
+    bt = torch.full((B, max(max(need), 1)), -1, dtype=torch.int32)
+    k_ = 0
+    for b_, n in enumerate(need):
+        bt[b_, :n] = perm[k_ : k_ + n]
+        k_ += n
+    kp = torch.randn((h_kv, P, page, D), generator=gen) * std
+    vp = None if mla else (torch.randn((h_kv, P, page, D), generator=gen) * std).to(dtype).to(device)
+    q = torch.randn((B, H, N, D), generator=gen) * (0.5 if spike else std)
+    k = torch.randn((B, H, N, D), generator=gen) * std
+    v = (torch.randn((B, H, N, D), generator=gen) * std).to(dtype).to(device)
+    if spike:
+        q[..., 0] = 4.0
+        kp[..., 0] = torch.from_numpy(rng.uniform(-30.0, 30.0, size=(h_kv, P, page))).float()
+        k[..., 0] = torch.from_numpy(rng.uniform(-30.0, 30.0, size=(B, 1, N))).float()
+    kp = kp.to(dtype).to(device)
+    q, k = q.to(dtype).to(device), k.to(dtype).to(device)
+    cache = InferenceCache()
+    cache.prefill_paged_kv_cache(0, k_pages=kp, v_pages=vp, block_table=bt.to(device),
+                                 context_lens=torch.tensor(ctx, dtype=torch.int32), is_mla=mla, num_heads=H, head_dim=D)
+    kc, cu = pack_ref.gather_pages(_np(kp).transpose(1, 0, 2, 3), bt.numpy(), ctx)
+    vc = None if mla else pack_ref.gather_pages(_np(vp).transpose(1, 0, 2, 3), bt.numpy(), ctx)[0]
+    meta = build_pack_metadata(torch.tensor(lengths, device=device), N, 64)
+    scale = 1.0 / math.sqrt(D)
+    out = flash_attn_mlm_compressed(q, k, k if mla else v, H, meta, scale, cache, 0, is_mla=mla, block_n=64,
+                                    causal_query_seq_attn=causal)
+    ref = ar.mlm_attention_packed(_np(q), _np(k), _np(k if mla else v), lengths, scale, is_mla=mla,
+                                  causal_query_seq_attn=causal, k_cache=kc, v_cache=vc,
+                                  cu_seqlens_kv=[int(x) for x in cu], total_context_len=int(cu[-1]),
+                                  context_batch_size=B)
+    np.testing.assert_allclose(_np(unpack_from_kernel(out, meta, H)), ref, atol=1e-2 * max(1.0, std), rtol=1e-2)
