@@ -45,11 +45,13 @@ def test_random_backward_packed(seed, device):
     mla = D == 512 or bool(rng.random() < 0.3)
     dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float16
     causal = bool(rng.random() < 0.35)
-    # offsets at fp16 only: with them, dS = P (dP - delta) of the few dominant keys is a
-    # difference of near-equal terms that the product rounds to the input type, and dq =
-    # sum dS k (sum dS = 0) cancels against keys of +-30 in the offset dimension; at bf16
-    # that leaves up to ~30% of max |dq| (measured with the scores themselves scaled in
-    # fp32 or rounded to bf16 alike: 0.21 vs 0.19 of 0.76), past the 2e-2 budget
+    # offsets of +-12 in k (scores to ~12 log2 units at D = 32), at fp16 only: dS =
+    # P (dP - delta) of the few dominant keys is a difference of near-equal terms that the
+    # product rounds to the input type, and dq = sum dS k (sum dS = 0) cancels against the
+    # offset dimension's large k.  With offsets of +-30 that left up to ~30% of max |dq| at
+    # bf16 (with the scores scaled in fp32 or rounded to bf16 alike: 0.21 vs 0.19 of 0.76)
+    # and 8% in one fp16 case of a 60-seed sweep, past the 2e-2 budget; at +-12, fp16
+    # passed 72 of 72 seeds and bf16 failed 6 of 72 (up to ~4% of max |dq|)
     spike = bool(rng.random() < 0.5) and dtype == torch.float16
     small = D == 512  # the latent's oracle and kernels are the slow ones
     B = int(rng.integers(1, 3 if small else 5))
@@ -70,7 +72,7 @@ def test_random_backward_packed(seed, device):
     def q_spike(t):
         t[..., 0] = 4.0
 
-    k0 = torch.from_numpy(rng.uniform(-30.0, 30.0, size=(B, N))).float()
+    k0 = torch.from_numpy(rng.uniform(-12.0, 12.0, size=(B, N))).float()
 
     def k_spike(t):
         if mla:
@@ -87,7 +89,7 @@ def test_random_backward_packed(seed, device):
         ctx[0] = max(ctx[0], 1)
         cu_kv = np.concatenate([[0], np.cumsum(ctx)]).astype(np.int32)
         total = int(cu_kv[-1])
-        c0 = torch.from_numpy(rng.uniform(-30.0, 30.0, size=heads * total)).float()
+        c0 = torch.from_numpy(rng.uniform(-12.0, 12.0, size=heads * total)).float()
 
         def kc_spike(t):
             t[:, 0] = c0
