@@ -30,14 +30,18 @@ def _close(got, ref, what):
     got = _np(got)
     scale = float(np.abs(ref).max()) if ref.size else 0.0
     if scale == 0.0:
-        assert float(np.abs(got).max()) == 0.0, f"{what}: nonzero gradient where the reference is zero"
+        # every row sees one key (seed 153: one sequence of one row, no context): P = 1, so
+        # dS = dP - delta is zero but for rounding (dP from the MFMA over V, delta from the
+        # stored output), and the GPU's gradient is that rounding (1.8e-7 at seed 153)
+        worst = float(np.abs(got).max())
+        assert worst <= 1e-4, f"{what}: max {worst:.3e} where the reference is zero"
         return
     err = np.abs(got - ref)
     worst = float((err - (TOL * scale + TOL * np.abs(ref))).max())
     assert worst <= 0, f"{what}: max err {float(err.max()):.3e} (ref max {scale:.3e})"
 
 
-@pytest.mark.parametrize("seed", list(range(12)))
+@pytest.mark.parametrize("seed", list(range(12)) + [153])
 def test_random_backward_packed(seed, device):
     rng = np.random.default_rng(9500 + seed)
     gen = torch.Generator().manual_seed(9500 + seed)
